@@ -1,0 +1,186 @@
+/*
+ * kvskip_amd: C ABI of the MI355X (gfx950) decode-attention hot path.
+ *
+ * Every entry point takes plain pointers to device memory, element strides and sizes,
+ * and a HIP stream (hipStream_t passed as void*; NULL = the null stream). Nothing is
+ * allocated inside the library: outputs and split-K partial buffers are passed in by the
+ * caller. Entry points validate their arguments on the host before any device work and
+ * return KVSKIP_OK (0) or a negative KVSKIP_E* code; kvskip_last_error() then holds a
+ * message for the calling thread. No entry point synchronises with the host.
+ *
+ * Units. Scores are q.k * scale. blk_max and lse are natural-log units; the split-K
+ * partials (part_ml) are in log2 units (running max, running sum), as are all internal
+ * softmax states. Blocks are 64 tokens from position 0; nb = ceil(T / 64).
+ *
+ * Each entry point names the reference interface it replaces (format37/kvskip, paths
+ * relative to its repository root).
+ */
+#ifndef KVSKIP_AMD_H
+#define KVSKIP_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVSKIP_BLOCK 64
+
+enum {
+  KVSKIP_OK = 0,
+  KVSKIP_E_INVALID = -1,     /* argument validation failed (message in kvskip_last_error) */
+  KVSKIP_E_UNSUPPORTED = -2, /* head dim / group size / flag combination not instantiated */
+  KVSKIP_E_LAUNCH = -3       /* the HIP runtime rejected a launch */
+};
+
+/* Attention launch block: replaces kvskip::Params (kernels/kvskip.h:13-60).
+ * q [B, Hq, D] bf16; k, v [B, Hkv, T, D] bf16 with arbitrary batch/head/token element
+ * strides, D contiguous, all strides multiples of 8 elements, base 16-byte aligned. */
+typedef struct kvskip_attn_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int32_t B, Hq, Hkv, T, D;
+  float scale;                 /* softmax scale (natural units) */
+
+  /* masked mode: per (b, kv head) ascending list of block indices to read */
+  const int32_t* block_idx;    /* [B, Hkv, max_blocks] */
+  const int32_t* block_cnt;    /* [B, Hkv] */
+  int32_t max_blocks;
+
+  /* split-K: num_splits > 1 needs both partial buffers */
+  int32_t num_splits;
+  float* part_acc;             /* [B, Hq, num_splits, D] un-normalised, relative to the part max */
+  float* part_ml;              /* [B, Hq, num_splits, 2] (max, sum) in log2 units */
+
+  void* out;                   /* [B, Hq, D] bf16 (NULL in stats-only mode) */
+  float* out_f32;              /* optional [B, Hq, D] */
+  float* lse;                  /* optional [B, Hq] natural-log log-sum-exp of the attended scores */
+
+  /* per-block statistics, [B, Hq, nb]: max score (natural units) and sum exp(s - max);
+   * blocks not read are left untouched (callers pre-fill -inf / 0) */
+  float* blk_max;
+  float* blk_sum;
+
+  /* two-pass V-skip: pass 1 writes P = exp(s - blk_max) as fp16 [B, Hq, nb*64];
+   * pass 2 reads it back with blk_scale [B, Hkv, nb, G] */
+  void* p_out;
+  const void* p_in;
+  const float* blk_scale;
+
+  /* single-pass V-skip */
+  float tau;                   /* keep V of a block if some head's weight estimate >= tau */
+  int32_t local;               /* newest blocks always kept (block 0 always kept too) */
+  int32_t* vcount;             /* optional [B, Hkv] V blocks loaded (atomically added) */
+  const float* lse_prev;       /* optional [B, Hq] natural-log normaliser estimate; NULL: block-0 bound */
+} kvskip_attn_args;
+
+/* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block
+ * statistics (stats), stats-only reading K alone (load_v = 0, needs stats) and fp16 P (p_out,
+ * needs stats). num_splits > 1 adds the log-sum-exp merge of the partials.
+ * Replaces kvskip::launch_decode (kernels/kvskip.h:113-114, kernels/kvskip_kernel.cu:761-769),
+ * reached from kvskip_ext.decode (kernels/kvskip_ext.cpp:25-101). Any G = Hq / Hkv in 1..8. */
+int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream);
+
+/* Two-pass V-skip, pass 2: out = sum over listed blocks of blk_scale * P . V (no softmax);
+ * num_splits > 1 adds the plain sum of the partials.
+ * Replaces kvskip::launch_pv (kernels/kvskip.h:117, kernels/kvskip_kernel.cu:754-759),
+ * reached from kvskip_ext.pv (kernels/kvskip_ext.cpp:106-146). */
+int kvskip_pv(const kvskip_attn_args* a, void* stream);
+
+/* Single-pass V-skip: every K block is read; the V block is read (and the block enters the
+ * softmax) only for block 0, the `local` newest blocks, or when some head of the group has
+ * block log-sum-exp - lse0 >= log(tau), lse0 = lse_prev or the block-0 log-sum-exp.
+ * Replaces kvskip::launch_vskip1 (kernels/kvskip.h:118, kernels/kvskip_kernel.cu:747-752),
+ * reached from kvskip_ext.vskip1 (kernels/kvskip_ext.cpp:149-195). */
+int kvskip_vskip1(const kvskip_attn_args* a, void* stream);
+
+/* Streaming read of `bytes` (multiple of 16) bytes at x: the achievable read ceiling.
+ * Replaces kvskip::launch_read (kernels/kvskip.h:120), kvskip_ext.read_bw
+ * (kernels/kvskip_ext.cpp:321-325). out: one uint32 (written only if a sentinel hits). */
+int kvskip_read(const void* x, int64_t bytes, uint32_t* out, int32_t blocks, void* stream);
+
+/* Refresh planner, before the attention pass. Replaces kvskip::PlanParams + launch_plan
+ * (kernels/kvskip.h:63-89,115, kernels/kvskip_planner.cu:75-227,309-312), reached from
+ * kvskip_ext.plan (kernels/kvskip_ext.cpp:205-267). Any D in {64, 128}, G in 1..8. */
+typedef struct kvskip_plan_args {
+  const void* q;               /* [B, Hq, D] bf16 */
+  int64_t q_sb, q_sh;
+  const void* k;               /* [B, Hkv, T, D] bf16 cache view, the new token at T - 1 */
+  int64_t k_sb, k_sh, k_st;
+  float* csum;                 /* [B, Hkv, NBC, D] per-block key sums (fp32), updated if add_token */
+  const float* lse_ref;        /* [B, Hq, NBC] block log-sum-exp at the head's last refresh */
+  const float* cs_ref;         /* [B, Hq, NBC] centroid scores at that refresh */
+  const uint8_t* keep;         /* [B, Hkv, NBC] stored set */
+  const float* lse_att;        /* [B, Hq] previous step's attended log-sum-exp */
+  int32_t* age;                /* [B, Hkv] steps since the last refresh (updated) */
+  const int32_t* flags;        /* [Hkv] bit 0 always refresh, bit 1 token-index head, bit 2 index union */
+  const uint8_t* idx;          /* [B, NBC] token-index blocks, or NULL */
+  const float* calib;          /* [B, Hkv] estimate correction, or NULL */
+  float* est;                  /* [B, Hkv] out: uncorrected estimate, or NULL */
+  const uint8_t* aix;          /* [B, Hkv] heads latched onto the index, or NULL (needs idx) */
+  float* cs_now;               /* [B, Hq, NBC] out: this step's centroid scores */
+  uint8_t* trig;               /* [B, Hkv] out: refresh decision */
+  int32_t* block_idx;          /* [B, Hkv, NBC] out: blocks to read, ascending */
+  int32_t* block_cnt;          /* [B, Hkv] out */
+  int32_t B, Hq, Hkv, T, D, NBC, local, max_age, add_token, calib_on, calib_kind;
+  float scale, delta;
+} kvskip_plan_args;
+
+int kvskip_plan(const kvskip_plan_args* p, void* stream);
+
+/* Refresh planner, after the attention pass. Replaces kvskip::UpdateParams + launch_update
+ * (kernels/kvskip.h:91-111,116, kernels/kvskip_planner.cu:229-305,314-318), reached from
+ * kvskip_ext.update (kernels/kvskip_ext.cpp:270-319). */
+typedef struct kvskip_update_args {
+  const float* blk_max;        /* [B, Hq, nb] stats of this step's pass (-inf / 0 where not read) */
+  const float* blk_sum;
+  const uint8_t* trig;         /* [B, Hkv] */
+  const float* cs_now;         /* [B, Hq, NBC] */
+  uint8_t* keep;               /* [B, Hkv, NBC] updated on refreshing heads */
+  float* lse_ref;              /* [B, Hq, NBC] updated on refreshing heads */
+  float* cs_ref;               /* [B, Hq, NBC] updated on refreshing heads */
+  float* lse_att;              /* [B, Hq] updated on every head */
+  const int32_t* flags;        /* [Hkv] or NULL */
+  const uint8_t* idx;          /* [B, NBC] or NULL */
+  const float* est;            /* [B, Hkv] plan's uncorrected estimate (with calib) */
+  float* calib;                /* [B, Hkv] or NULL: no learning */
+  uint8_t* aix;                /* [B, Hkv] or NULL */
+  float calib_rate, aix_thr, level;
+  int32_t calib_free, calib_kind;
+  int32_t B, Hq, Hkv, T, NBC, local;
+} kvskip_update_args;
+
+int kvskip_update(const kvskip_update_args* p, void* stream);
+
+/* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
+ * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums
+ * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. */
+int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv,
+                      int32_t T, int32_t D, float* csum, int32_t NBC, void* stream);
+
+/* Token index of a decode step: idx[b, blk] = 1 if block blk (of the first T tokens) holds an
+ * earlier copy of ids[b, T-1] or the position right after one; blocks >= nb up to NBC are
+ * zeroed. The device form of index_steps / index_blocks (src/lab.py:149-167,
+ * src/run_free.py:103-113). ids [B, ids_stride] int32. */
+int kvskip_token_index(const int32_t* ids, int64_t ids_stride, int32_t B, int32_t T, uint8_t* idx,
+                       int32_t NBC, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kvskip_last_error(void);
+
+/* Library version string. */
+const char* kvskip_version(void);
+
+/* sizeof of the argument blocks (0: kvskip_attn_args, 1: kvskip_plan_args, 2: kvskip_update_args),
+ * -1 otherwise: lets a binding check its struct layout. Library utility, no reference counterpart. */
+int kvskip_struct_size(int which);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVSKIP_AMD_H */

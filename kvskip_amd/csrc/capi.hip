@@ -1,0 +1,233 @@
+// C ABI of kvskip_amd: host-side argument validation, derived launch constants, launches.
+// Validation never touches the device, so every error path runs without a GPU.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "internal.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return KVSKIP_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(KVSKIP_E_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_kv(const void* ptr, int64_t sb, int64_t sh, int64_t st, const char* name) {
+  if (ptr == nullptr) return fail(KVSKIP_E_INVALID, "%s must be a CUDA bf16 tensor", name);
+  if (sb % 8 != 0 || sh % 8 != 0 || st % 8 != 0)
+    return fail(KVSKIP_E_INVALID, "%s strides must be multiples of 8 elements (16-byte rows)", name);
+  if (!aligned16(ptr)) return fail(KVSKIP_E_INVALID, "%s must be 16-byte aligned", name);
+  return KVSKIP_OK;
+}
+
+// Common checks of q/k/v and sizes; fills the derived parts of the kernel block.
+int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_v, kvs::AttnP* p) {
+  if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (a->B < 1 || a->Hq < 1 || a->Hkv < 1 || a->T < 1)
+    return fail(KVSKIP_E_INVALID, "sizes must be positive (B=%d Hq=%d Hkv=%d T=%d)", a->B, a->Hq, a->Hkv, a->T);
+  if (a->Hq % a->Hkv != 0) return fail(KVSKIP_E_INVALID, "Hq must be a multiple of Hkv");
+  const int G = a->Hq / a->Hkv;
+  if (!kvs::attn_supported(a->D, G))
+    return fail(KVSKIP_E_UNSUPPORTED, "kvskip: unsupported head dim / group size (D=%d, G=%d)", a->D, G);
+  if (need_q) {
+    if (a->q == nullptr) return fail(KVSKIP_E_INVALID, "q must be CUDA bf16 [B, Hq, D]");
+    if (a->q_sb % 8 != 0 || a->q_sh % 8 != 0 || !aligned16(a->q))
+      return fail(KVSKIP_E_INVALID, "q rows must be 16-byte aligned");
+  }
+  int rc;
+  if (need_k && (rc = check_kv(a->k, a->k_sb, a->k_sh, a->k_st, "k")) != KVSKIP_OK) return rc;
+  if (need_v && (rc = check_kv(a->v, a->v_sb, a->v_sh, a->v_st, "v")) != KVSKIP_OK) return rc;
+  if (a->num_splits < 1) return fail(KVSKIP_E_INVALID, "num_splits >= 1");
+  if (a->num_splits > 1 && a->part_ml == nullptr)
+    return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
+  std::memset(p, 0, sizeof(*p));
+  p->q = static_cast<const uint16_t*>(a->q);
+  p->k = static_cast<const uint16_t*>(a->k);
+  p->v = static_cast<const uint16_t*>(a->v);
+  p->q_sb = a->q_sb; p->q_sh = a->q_sh;
+  p->k_sb = a->k_sb; p->k_sh = a->k_sh; p->k_st = a->k_st;
+  p->v_sb = a->v_sb; p->v_sh = a->v_sh; p->v_st = a->v_st;
+  p->B = a->B; p->Hq = a->Hq; p->Hkv = a->Hkv; p->T = a->T;
+  p->nb = (a->T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK;
+  p->scale_log2 = static_cast<float>(static_cast<double>(a->scale) * 1.4426950408889634);
+  p->block_idx = a->block_idx;
+  p->block_cnt = a->block_cnt;
+  p->max_blocks = a->max_blocks;
+  p->num_splits = a->num_splits;
+  p->part_acc = a->part_acc;
+  p->part_ml = a->part_ml;
+  p->out = static_cast<uint16_t*>(a->out);
+  p->out_f32 = a->out_f32;
+  p->lse = a->lse;
+  p->blk_max = a->blk_max;
+  p->blk_sum = a->blk_sum;
+  p->p_out = static_cast<uint16_t*>(a->p_out);
+  p->p_in = static_cast<const uint16_t*>(a->p_in);
+  p->blk_scale = a->blk_scale;
+  p->t_pad = static_cast<int64_t>(p->nb) * KVSKIP_BLOCK;
+  p->local = a->local;
+  p->vcount = a->vcount;
+  p->lse_prev = a->lse_prev;
+  return KVSKIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kvskip_last_error(void) { return g_err; }
+
+const char* kvskip_version(void) { return "kvskip_amd 0.1 (gfx950)"; }
+
+int kvskip_struct_size(int which) {
+  switch (which) {
+    case 0: return static_cast<int>(sizeof(kvskip_attn_args));
+    case 1: return static_cast<int>(sizeof(kvskip_plan_args));
+    case 2: return static_cast<int>(sizeof(kvskip_update_args));
+    default: return -1;
+  }
+}
+
+int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+  kvs::AttnP p;
+  int rc = prepare_attn(a, true, true, load_v != 0, &p);
+  if (rc != KVSKIP_OK) return rc;
+  if (!load_v && !stats) return fail(KVSKIP_E_INVALID, "load_v=false only makes sense with stats=true");
+  if (a->p_out != nullptr && !stats) return fail(KVSKIP_E_INVALID, "write_p needs stats=true");
+  if (load_v && a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required with load_v");
+  if (stats && (a->blk_max == nullptr || a->blk_sum == nullptr))
+    return fail(KVSKIP_E_INVALID, "stats needs blk_max and blk_sum");
+  if (load_v && a->num_splits > 1 && a->part_acc == nullptr)
+    return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
+  const bool masked = a->block_idx != nullptr;
+  if (masked) {
+    if (a->block_cnt == nullptr) return fail(KVSKIP_E_INVALID, "block_cnt is required with block_idx");
+    if (a->max_blocks < 0) return fail(KVSKIP_E_INVALID, "block_idx must be contiguous int32 [B, Hkv, max_blocks]");
+  }
+  if (!load_v) p.out = nullptr;
+  const int G = a->Hq / a->Hkv;
+  return launched(kvs::launch_decode(p, a->D, G, masked, stats != 0, load_v != 0,
+                                     static_cast<hipStream_t>(stream)),
+                  "kvskip_decode");
+}
+
+int kvskip_pv(const kvskip_attn_args* a, void* stream) {
+  kvs::AttnP p;
+  int rc = prepare_attn(a, false, false, true, &p);
+  if (rc != KVSKIP_OK) return rc;
+  if (a->p_in == nullptr) return fail(KVSKIP_E_INVALID, "P: fp16 [B, Hq, t_pad]");
+  if (!aligned16(a->p_in)) return fail(KVSKIP_E_INVALID, "P must be 16-byte aligned");
+  if (a->blk_scale == nullptr) return fail(KVSKIP_E_INVALID, "blk_scale: contiguous fp32 [B, Hkv, nb, G]");
+  if (a->block_idx == nullptr) return fail(KVSKIP_E_INVALID, "block_idx");
+  if (a->block_cnt == nullptr) return fail(KVSKIP_E_INVALID, "block_cnt");
+  if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
+  if (a->num_splits > 1 && a->part_acc == nullptr)
+    return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
+  const int G = a->Hq / a->Hkv;
+  return launched(kvs::launch_pv(p, a->D, G, static_cast<hipStream_t>(stream)), "kvskip_pv");
+}
+
+int kvskip_vskip1(const kvskip_attn_args* a, void* stream) {
+  kvs::AttnP p;
+  int rc = prepare_attn(a, true, true, true, &p);
+  if (rc != KVSKIP_OK) return rc;
+  if (!(a->tau > 0.f) || a->local < 0) return fail(KVSKIP_E_INVALID, "tau > 0, local >= 0, num_splits >= 1");
+  if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
+  if (a->num_splits > 1 && a->part_acc == nullptr)
+    return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
+  p.log2_tau = static_cast<float>(std::log2(static_cast<double>(a->tau)));
+  const int G = a->Hq / a->Hkv;
+  return launched(kvs::launch_vskip1(p, a->D, G, static_cast<hipStream_t>(stream)), "kvskip_vskip1");
+}
+
+int kvskip_read(const void* x, int64_t bytes, uint32_t* out, int32_t blocks, void* stream) {
+  if (x == nullptr || out == nullptr) return fail(KVSKIP_E_INVALID, "x: contiguous CUDA, 16-byte multiple");
+  if (bytes % 16 != 0 || !aligned16(x)) return fail(KVSKIP_E_INVALID, "x: contiguous CUDA, 16-byte multiple");
+  if (blocks < 1) return fail(KVSKIP_E_INVALID, "blocks >= 1");
+  return launched(kvs::launch_read(x, bytes, out, blocks, static_cast<hipStream_t>(stream)), "kvskip_read");
+}
+
+int kvskip_plan(const kvskip_plan_args* p, void* stream) {
+  if (p == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (p->q == nullptr || p->k == nullptr) return fail(KVSKIP_E_INVALID, "q: CUDA bf16 [B, Hq, D]");
+  if (p->B < 1 || p->Hkv < 1 || p->Hq < 1 || p->T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
+  if (p->Hq % p->Hkv != 0) return fail(KVSKIP_E_INVALID, "Hq must be a multiple of Hkv");
+  const int G = p->Hq / p->Hkv;
+  if (!((p->D == 64 || p->D == 128) && (G == 1 || G == 2 || G == 4 || G == 7 || G == 8)))
+    return fail(KVSKIP_E_UNSUPPORTED, "planner kernels: D in {64, 128}, G in {1, 2, 4, 7, 8} (D=%d, G=%d)", p->D, G);
+  int rc = check_kv(p->k, p->k_sb, p->k_sh, p->k_st, "k");
+  if (rc != KVSKIP_OK) return rc;
+  if (p->csum == nullptr || p->lse_ref == nullptr || p->cs_ref == nullptr || p->keep == nullptr ||
+      p->lse_att == nullptr || p->age == nullptr || p->flags == nullptr || p->cs_now == nullptr ||
+      p->trig == nullptr || p->block_idx == nullptr || p->block_cnt == nullptr)
+    return fail(KVSKIP_E_INVALID, "plan: missing state tensor");
+  if (!aligned16(p->csum)) return fail(KVSKIP_E_INVALID, "csum must be 16-byte aligned");
+  const int nb = (p->T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK;
+  if (nb > p->NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
+  if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
+  if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
+  return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
+}
+
+int kvskip_update(const kvskip_update_args* p, void* stream) {
+  if (p == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (p->blk_max == nullptr || p->blk_sum == nullptr) return fail(KVSKIP_E_INVALID, "blk_max must be contiguous CUDA fp32");
+  if (p->trig == nullptr || p->cs_now == nullptr || p->keep == nullptr || p->lse_ref == nullptr ||
+      p->cs_ref == nullptr || p->lse_att == nullptr)
+    return fail(KVSKIP_E_INVALID, "update: missing state tensor");
+  if (p->B < 1 || p->Hkv < 1 || p->Hq < 1 || p->T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
+  if (p->Hq % p->Hkv != 0) return fail(KVSKIP_E_INVALID, "Hq must be a multiple of Hkv");
+  const int G = p->Hq / p->Hkv;
+  if (!(G == 1 || G == 2 || G == 4 || G == 7 || G == 8))
+    return fail(KVSKIP_E_UNSUPPORTED, "planner kernels: G in {1, 2, 4, 7, 8} (G=%d)", G);
+  const int nb = (p->T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK;
+  if (nb > p->NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
+  if (nb > kvs::planner_max_blocks(G))
+    return fail(KVSKIP_E_UNSUPPORTED, "update: %d blocks exceed the LDS capacity (%d)", nb, kvs::planner_max_blocks(G));
+  if (p->calib != nullptr) {
+    if (p->flags == nullptr || p->est == nullptr) return fail(KVSKIP_E_INVALID, "calibration needs flags and est");
+    if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
+  }
+  if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
+  return launched(kvs::launch_update(*p, static_cast<hipStream_t>(stream)), "kvskip_update");
+}
+
+int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,
+                      int32_t D, float* csum, int32_t NBC, void* stream) {
+  if (k == nullptr || csum == nullptr) return fail(KVSKIP_E_INVALID, "block_sums: null tensor");
+  if (B < 1 || Hkv < 1 || T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
+  if (D != 64 && D != 128) return fail(KVSKIP_E_UNSUPPORTED, "block_sums: D in {64, 128}");
+  if ((T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK > NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
+  return launched(kvs::launch_block_sums(k, k_sb, k_sh, k_st, B, Hkv, T, D, csum, NBC, static_cast<hipStream_t>(stream)),
+                  "kvskip_block_sums");
+}
+
+int kvskip_token_index(const int32_t* ids, int64_t ids_stride, int32_t B, int32_t T, uint8_t* idx, int32_t NBC,
+                       void* stream) {
+  if (ids == nullptr || idx == nullptr) return fail(KVSKIP_E_INVALID, "token_index: null tensor");
+  if (B < 1 || T < 1 || ids_stride < T) return fail(KVSKIP_E_INVALID, "token_index: ids must be [B, >= T] int32");
+  if ((T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK > NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
+  return launched(kvs::launch_token_index(ids, ids_stride, B, T, idx, NBC, static_cast<hipStream_t>(stream)),
+                  "kvskip_token_index");
+}
+
+}  // extern "C"

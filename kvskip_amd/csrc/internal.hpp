@@ -1,0 +1,62 @@
+// Launch-side declarations shared between the C ABI (capi.hip) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvskip_amd.h"
+
+namespace kvs {
+
+// Kernel argument block of the attention kernels: the validated C-ABI arguments plus the
+// derived constants the kernels use (log2-domain scale, nb, log2 tau, P row length).
+struct AttnP {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_sb, q_sh;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int B, Hq, Hkv, T, nb;
+  float scale_log2;
+  const int* block_idx;
+  const int* block_cnt;
+  int max_blocks;
+  int num_splits;
+  float* part_acc;
+  float* part_ml;
+  uint16_t* out;
+  float* out_f32;
+  float* lse;
+  float* blk_max;
+  float* blk_sum;
+  uint16_t* p_out;
+  const uint16_t* p_in;
+  const float* blk_scale;
+  int64_t t_pad;
+  float log2_tau;
+  int local;
+  int* vcount;
+  const float* lse_prev;
+};
+
+// Head dims / group sizes with instantiated attention kernels.
+bool attn_supported(int D, int G);
+
+// Each returns a hipError_t of the launch(es).
+hipError_t launch_decode(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, hipStream_t s);
+hipError_t launch_vskip1(const AttnP& p, int D, int G, hipStream_t s);
+hipError_t launch_pv(const AttnP& p, int D, int G, hipStream_t s);
+hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, hipStream_t s);
+
+hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s);
+hipError_t launch_update(const kvskip_update_args& p, hipStream_t s);
+hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
+                             int D, float* csum, int NBC, hipStream_t s);
+hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,
+                              hipStream_t s);
+
+// Largest block count the planner kernels hold in LDS for a group of G query heads.
+int planner_max_blocks(int G);
+
+}  // namespace kvs

@@ -1,0 +1,327 @@
+"""Operator surface of the reference's torch extension `kvskip_ext`, on the kvskip_amd C ABI.
+
+Same functions, positional/keyword signatures, defaults, output lists and validation messages as
+kernels/kvskip_ext.cpp:327-351 (decode, pv, vskip1, plan, update, read_bw). Outputs are allocated
+with torch on the inputs' device; launches go to torch's current stream; nothing synchronises.
+Absent outputs are returned as None (the reference returns undefined tensors).
+
+Two extra operators (block_sums, token_index) expose the device-side planner initialisation and
+token index; they have no counterpart in kvskip_ext.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _native
+from ._native import AttnArgs, PlanArgs, UpdateArgs
+
+TILE = 64
+
+
+def _fail(msg: str):
+    raise RuntimeError(msg)
+
+
+def _require(cond: bool, msg: str):
+    if not cond:
+        _fail(msg)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def check_kv(t: torch.Tensor, name: str):
+    """kernels/kvskip_ext.cpp:12-19."""
+    _require(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a CUDA bf16 tensor")
+    _require(t.dim() == 4, f"{name} must be [B, Hkv, T, D]")
+    _require(t.stride(3) == 1, f"{name} must have a contiguous last dim")
+    _require(t.stride(2) % 8 == 0 and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0,
+             f"{name} strides must be multiples of 8 elements (16-byte rows)")
+    _require(t.data_ptr() % 16 == 0, f"{name} must be 16-byte aligned")
+    T, D = t.shape[2], t.shape[3]
+    _require((T - 1) * t.stride(2) + D < 2**30, f"{name}: one head's rows must span < 2 GiB")
+
+
+def check_q(q: torch.Tensor):
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3, "q must be CUDA bf16 [B, Hq, D]")
+    _require(q.stride(2) == 1 and q.stride(1) % 8 == 0 and q.stride(0) % 8 == 0 and q.data_ptr() % 16 == 0,
+             "q rows must be 16-byte aligned")
+
+
+def check_f32(t: torch.Tensor, name: str):
+    _require(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(), f"{name} must be contiguous CUDA fp32")
+
+
+def _attn_args(q, k, v, scale, B, Hq, Hkv, T, D) -> AttnArgs:
+    a = AttnArgs()
+    if q is not None:
+        a.q = q.data_ptr()
+        a.q_sb, a.q_sh = q.stride(0), q.stride(1)
+    if k is not None:
+        a.k = k.data_ptr()
+        a.k_sb, a.k_sh, a.k_st = k.stride(0), k.stride(1), k.stride(2)
+    if v is not None:
+        a.v = v.data_ptr()
+        a.v_sb, a.v_sh, a.v_st = v.stride(0), v.stride(1), v.stride(2)
+    a.B, a.Hq, a.Hkv, a.T, a.D = B, Hq, Hkv, T, D
+    a.scale = float(scale)
+    return a
+
+
+def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
+           want_f32=False, write_p=False):
+    """Split-K decode attention (kernels/kvskip_ext.cpp:25-101).
+
+    Returns [out bf16 [B,Hq,D], lse fp32 [B,Hq], blk_max, blk_sum ([B,Hq,nb] or None), out_f32 (or None),
+    P fp16 [B,Hq,nb*64] (write_p) or None]."""
+    check_q(q)
+    check_kv(k, "k")
+    check_kv(v, "v")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
+             and v.shape[2] == T, "shape mismatch between q, k, v")
+    _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    _require(num_splits >= 1, "num_splits >= 1")
+    _require(load_v or stats, "load_v=false only makes sense with stats=true")
+    _require(not write_p or stats, "write_p needs stats=true")
+    _require(stages in (2, 3), "kvskip: unsupported head dim / stages")
+    masked = block_idx is not None
+    nb = (T + TILE - 1) // TILE
+    dev = q.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev) if load_v else None
+    out32 = torch.empty(B, Hq, D, **f32) if (load_v and want_f32) else None
+    lse = torch.empty(B, Hq, **f32)
+    bmax = bsum = None
+    if stats:
+        bmax = torch.full((B, Hq, nb), -math.inf, **f32)
+        bsum = torch.zeros(B, Hq, nb, **f32)
+    pbuf = torch.empty(B, Hq, nb * TILE, dtype=torch.float16, device=dev) if write_p else None
+    part_acc = part_ml = None
+    if num_splits > 1:
+        part_acc = torch.empty(B, Hq, num_splits, D, **f32) if load_v else None
+        part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
+    a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
+    if masked:
+        _require(block_cnt is not None, "block_cnt is required with block_idx")
+        bi, bc = block_idx, block_cnt
+        _require(bi.is_cuda and bi.dtype == torch.int32 and bi.dim() == 3 and bi.is_contiguous()
+                 and bi.shape[0] == B and bi.shape[1] == Hkv, "block_idx must be contiguous int32 [B, Hkv, max_blocks]")
+        _require(bc.is_cuda and bc.dtype == torch.int32 and bc.is_contiguous() and bc.numel() == B * Hkv,
+                 "block_cnt must be contiguous int32 [B, Hkv]")
+        a.block_idx, a.block_cnt, a.max_blocks = bi.data_ptr(), bc.data_ptr(), bi.shape[2]
+    a.num_splits = int(num_splits)
+    a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
+    a.out, a.out_f32, a.lse = _ptr(out), _ptr(out32), lse.data_ptr()
+    a.blk_max, a.blk_sum = _ptr(bmax), _ptr(bsum)
+    a.p_out = _ptr(pbuf)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_decode(ctypes.byref(a), int(bool(stats)), int(bool(load_v)), _stream(dev)))
+    return [out, lse, bmax, bsum, out32, pbuf]
+
+
+def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
+    """Two-pass V-skip, pass 2 (kernels/kvskip_ext.cpp:106-146). Returns [out bf16, out_f32 or None]."""
+    check_kv(v, "v")
+    _require(P.is_cuda and P.dtype == torch.float16 and P.dim() == 3 and P.is_contiguous(), "P: fp16 [B, Hq, t_pad]")
+    _require(blk_scale.is_cuda and blk_scale.dtype == torch.float32 and blk_scale.dim() == 4
+             and blk_scale.is_contiguous(), "blk_scale: contiguous fp32 [B, Hkv, nb, G]")
+    B, Hkv, T, D = v.shape
+    Hq = P.shape[1]
+    _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    G = Hq // Hkv
+    nb = (T + TILE - 1) // TILE
+    _require(P.shape[0] == B and P.shape[2] == nb * TILE, "P shape")
+    _require(tuple(blk_scale.shape) == (B, Hkv, nb, G), "blk_scale shape")
+    _require(block_idx.dtype == torch.int32 and block_idx.is_contiguous() and block_idx.shape[0] == B
+             and block_idx.shape[1] == Hkv, "block_idx")
+    _require(block_cnt.dtype == torch.int32 and block_cnt.is_contiguous() and block_cnt.numel() == B * Hkv,
+             "block_cnt")
+    _require(num_splits >= 1, "num_splits >= 1")
+    dev = v.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    out32 = torch.empty(B, Hq, D, **f32) if want_f32 else None
+    part_acc = torch.empty(B, Hq, num_splits, D, **f32) if num_splits > 1 else None
+    part_ml = torch.empty(B, Hq, num_splits, 2, **f32) if num_splits > 1 else None
+    a = _attn_args(None, None, v, 1.0, B, Hq, Hkv, T, D)
+    a.block_idx, a.block_cnt, a.max_blocks = block_idx.data_ptr(), block_cnt.data_ptr(), block_idx.shape[2]
+    a.num_splits = int(num_splits)
+    a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
+    a.out, a.out_f32 = out.data_ptr(), _ptr(out32)
+    a.p_in, a.blk_scale = P.data_ptr(), blk_scale.data_ptr()
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_pv(ctypes.byref(a), _stream(dev)))
+    return [out, out32]
+
+
+def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=False, lse_prev=None):
+    """Single-pass V-skip (kernels/kvskip_ext.cpp:149-195). Returns [out, lse, out_f32 or None, vcount or None]."""
+    check_q(q)
+    check_kv(k, "k")
+    check_kv(v, "v")
+    _require(tau > 0.0 and local >= 0 and num_splits >= 1, "tau > 0, local >= 0, num_splits >= 1")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
+             and v.shape[2] == T, "shape mismatch between q, k, v")
+    _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    dev = q.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    out32 = torch.empty(B, Hq, D, **f32) if want_f32 else None
+    lse = torch.empty(B, Hq, **f32)
+    vcount = torch.zeros(B, Hkv, dtype=torch.int32, device=dev) if count else None
+    part_acc = part_ml = None
+    if num_splits > 1:
+        part_acc = torch.empty(B, Hq, num_splits, D, **f32)
+        part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
+    a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
+    a.num_splits = int(num_splits)
+    a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
+    a.out, a.out_f32, a.lse = out.data_ptr(), _ptr(out32), lse.data_ptr()
+    a.tau, a.local, a.vcount = float(tau), int(local), _ptr(vcount)
+    if lse_prev is not None:
+        _require(lse_prev.is_cuda and lse_prev.dtype == torch.float32 and lse_prev.is_contiguous()
+                 and lse_prev.numel() == B * Hq, "lse_prev: contiguous fp32 [B, Hq]")
+        a.lse_prev = lse_prev.data_ptr()
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_vskip1(ctypes.byref(a), _stream(dev)))
+    return [out, lse, out32, vcount]
+
+
+def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
+         max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None):
+    """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place."""
+    _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
+    check_kv(k, "k")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    for t, n in ((csum, "csum"), (lse_ref, "lse_ref"), (cs_ref, "cs_ref"), (lse_att, "lse_att"), (cs_now, "cs_now")):
+        check_f32(t, n)
+    NBC = keep.shape[2]
+    _require((T + TILE - 1) // TILE <= NBC, "block capacity exceeded")
+    _require(csum.shape[2] == NBC and lse_ref.shape[2] == NBC and cs_ref.shape[2] == NBC and cs_now.shape[2] == NBC
+             and block_idx.shape[2] == NBC, "capacity mismatch")
+    _require(age.dtype == torch.int32 and age.is_contiguous() and age.numel() == B * Hkv, "age: int32 [B, Hkv]")
+    _require(flags.dtype == torch.int32 and flags.numel() == Hkv, "flags: int32 [Hkv]")
+    _require(keep.dtype == torch.uint8 and keep.is_contiguous(), "keep: contiguous uint8 [B, Hkv, NBC]")
+    _require(trig.dtype == torch.uint8 and block_idx.dtype == torch.int32 and block_cnt.dtype == torch.int32,
+             "trig uint8, block_idx / block_cnt int32")
+    p = PlanArgs()
+    p.q, p.q_sb, p.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k, p.k_sb, p.k_sh, p.k_st = k.data_ptr(), k.stride(0), k.stride(1), k.stride(2)
+    p.csum, p.lse_ref, p.cs_ref, p.keep = csum.data_ptr(), lse_ref.data_ptr(), cs_ref.data_ptr(), keep.data_ptr()
+    p.lse_att, p.age, p.flags = lse_att.data_ptr(), age.data_ptr(), flags.data_ptr()
+    if idx is not None:
+        _require(idx.is_cuda and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[0] == B
+                 and idx.shape[1] == NBC, "idx: contiguous uint8 [B, NBC]")
+        p.idx = idx.data_ptr()
+    if calib is not None:
+        check_f32(calib, "calib")
+        _require(calib.numel() == B * Hkv, "calib: [B, Hkv]")
+        p.calib = calib.data_ptr()
+    if est is not None:
+        check_f32(est, "est")
+        _require(est.numel() == B * Hkv, "est: [B, Hkv]")
+        p.est = est.data_ptr()
+    p.calib_on, p.calib_kind = int(bool(calib_on)), int(calib_kind)
+    if aix is not None:
+        _require(aix.is_cuda and aix.dtype == torch.uint8 and aix.is_contiguous() and aix.numel() == B * Hkv,
+                 "aix: contiguous uint8 [B, Hkv]")
+        _require(idx is not None, "aix needs idx")
+        p.aix = aix.data_ptr()
+    p.cs_now, p.trig = cs_now.data_ptr(), trig.data_ptr()
+    p.block_idx, p.block_cnt = block_idx.data_ptr(), block_cnt.data_ptr()
+    p.B, p.Hq, p.Hkv, p.T, p.D, p.NBC = B, Hq, Hkv, T, D, NBC
+    p.local, p.max_age, p.add_token = int(local), int(max_age), int(bool(add_token))
+    p.scale, p.delta = float(scale), float(delta)
+    dev = q.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
+
+
+def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
+           est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0):
+    """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place."""
+    check_f32(blk_max, "blk_max")
+    check_f32(blk_sum, "blk_sum")
+    B, Hkv, NBC = keep.shape
+    Hq = lse_att.shape[1]
+    _require(blk_max.shape[2] == (T + TILE - 1) // TILE, "stats length mismatch")
+    _require(keep.dtype == torch.uint8 and keep.is_contiguous(), "keep: contiguous uint8 [B, Hkv, NBC]")
+    p = UpdateArgs()
+    p.blk_max, p.blk_sum, p.trig, p.cs_now = blk_max.data_ptr(), blk_sum.data_ptr(), trig.data_ptr(), cs_now.data_ptr()
+    p.keep, p.lse_ref, p.cs_ref, p.lse_att = keep.data_ptr(), lse_ref.data_ptr(), cs_ref.data_ptr(), lse_att.data_ptr()
+    p.B, p.Hq, p.Hkv, p.T, p.NBC, p.local = B, Hq, Hkv, int(T), NBC, int(local)
+    p.level = float(level)
+    if calib is not None:
+        _require(flags is not None and est is not None, "calibration needs flags and est")
+        _require(flags.is_cuda and flags.dtype == torch.int32 and flags.numel() == Hkv, "flags: int32 [Hkv]")
+        check_f32(est, "est")
+        check_f32(calib, "calib")
+        _require(est.numel() == B * Hkv and calib.numel() == B * Hkv, "est / calib: [B, Hkv]")
+        p.flags, p.est, p.calib = flags.data_ptr(), est.data_ptr(), calib.data_ptr()
+        p.calib_rate, p.calib_free, p.calib_kind = float(calib_rate), int(bool(calib_free)), int(calib_kind)
+        if aix is not None:
+            _require(aix.is_cuda and aix.dtype == torch.uint8 and aix.is_contiguous() and aix.numel() == B * Hkv,
+                     "aix: contiguous uint8 [B, Hkv]")
+            _require(idx is not None, "aix needs idx")
+            p.aix, p.aix_thr = aix.data_ptr(), float(aix_thr)
+        if idx is not None:
+            _require(idx.is_cuda and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[0] == B
+                     and idx.shape[1] == NBC, "idx: contiguous uint8 [B, NBC]")
+            p.idx = idx.data_ptr()
+    dev = keep.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_update(ctypes.byref(p), _stream(dev)))
+
+
+def read_bw(x, out, blocks):
+    """Streaming read of x (bandwidth ceiling), kernels/kvskip_ext.cpp:321-325."""
+    _require(x.is_cuda and x.is_contiguous() and (x.numel() * x.element_size()) % 16 == 0,
+             "x: contiguous CUDA, 16-byte multiple")
+    dev = x.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_read(x.data_ptr(), x.numel() * x.element_size(), out.data_ptr(),
+                                                int(blocks), _stream(dev)))
+
+
+def block_sums(k, NBC, out=None):
+    """Per-block key sums [B, Hkv, NBC, D] fp32 of k [B, Hkv, T, D] (blocks >= nb are zero)."""
+    check_kv(k, "k")
+    B, Hkv, T, D = k.shape
+    _require((T + TILE - 1) // TILE <= NBC, "block capacity exceeded")
+    if out is None:
+        out = torch.empty(B, Hkv, NBC, D, dtype=torch.float32, device=k.device)
+    check_f32(out, "csum")
+    _require(tuple(out.shape) == (B, Hkv, NBC, D), "csum: [B, Hkv, NBC, D]")
+    with torch.cuda.device(k.device):
+        _native.check(_native.lib().kvskip_block_sums(k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), B, Hkv, T, D,
+                                                      out.data_ptr(), NBC, _stream(k.device)))
+    return out
+
+
+def token_index(ids, T, NBC, out=None):
+    """Token-index blocks [B, NBC] uint8 of the step whose current token is ids[:, T-1]."""
+    _require(ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 2 and ids.stride(1) == 1,
+             "ids: CUDA int32 [B, >= T]")
+    B = ids.shape[0]
+    _require(ids.shape[1] >= T >= 1, "ids: CUDA int32 [B, >= T]")
+    if out is None:
+        out = torch.empty(B, NBC, dtype=torch.uint8, device=ids.device)
+    _require(out.dtype == torch.uint8 and out.is_contiguous() and tuple(out.shape) == (B, NBC), "idx: uint8 [B, NBC]")
+    with torch.cuda.device(ids.device):
+        _native.check(_native.lib().kvskip_token_index(ids.data_ptr(), ids.stride(0), B, int(T), out.data_ptr(), NBC,
+                                                       _stream(ids.device)))
+    return out

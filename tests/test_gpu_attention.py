@@ -1,0 +1,209 @@
+"""GPU parity of the attention kernels (through the C ABI, via kvskip_amd.ext) against the fp64
+CPU oracle, on seeded inputs; the cases of the reference's bench/test_decode.py:66-196 plus the
+BASELINE configurations.
+
+Tolerances (bf16 in, fp32 accumulate): bf16 output rel. L2 error <= 2e-3 (the bar in the
+north star; bf16 rounding of the output alone is ~1.1e-3), fp32 output <= 2e-5, lse and block
+statistics (natural units) |err| <= 2e-4, block sums rel. <= 2e-4.
+"""
+
+import math
+
+import pytest
+import torch
+
+from kvskip_amd import kvskip as K
+from kvskip_amd import workloads as W
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-3
+F32_TOL = 2e-5
+LSE_TOL = 2e-4
+
+
+def rand_qkv(B, Hq, Hkv, T, D, seed, sink_gap=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    if sink_gap:
+        k[:, :, 0] *= 8.0                       # a sink with a ~30-nat gap (bench/test_decode.py:173)
+    return q, k.to(torch.bfloat16), v
+
+
+def to_gpu(*xs):
+    return [x.cuda() for x in xs]
+
+
+def check_decode(q, k, v, scale, gq, gk, gv, keep=None, num_splits=None, label=""):
+    plan = None
+    if keep is not None:
+        plan = K.make_plan(keep.cuda())
+    r = K.decode(gq, gk, gv, scale, plan=plan, num_splits=num_splits, out_f32=True)
+    ref, lse = O.decode(q, k, v, scale, keep=keep)
+    e16 = O.rel_err(r["out"].cpu(), ref)
+    e32 = O.rel_err(r["out_f32"].cpu(), ref)
+    el = (r["lse"].cpu().double() - lse).abs().max().item()
+    print(f"{label} splits={r['num_splits']}: bf16 {e16:.2e} f32 {e32:.2e} lse {el:.2e}", flush=True)
+    assert e16 <= BF16_TOL and e32 <= F32_TOL and el <= LSE_TOL, (label, e16, e32, el)
+    return r
+
+
+def test_cfg1_dense(gpu):
+    L = W.cfg1()
+    gq, gk, gv = to_gpu(L.q, L.k, L.v)
+    for ns in (None, 1, 7, 64):
+        check_decode(L.q, L.k, L.v, L.scale, gq, gk, gv, num_splits=ns, label="cfg1")
+
+
+@pytest.mark.parametrize("D,T,ns", [(64, 1000, None), (64, 33, 3), (128, 64, 4), (128, 65, 9), (128, 3000, 64)])
+def test_edge_cases(gpu, D, T, ns):
+    """bench/test_decode.py:168-176: short / ragged T, more splits than blocks, huge score gaps."""
+    q, k, v = rand_qkv(2, 32, 8, T, D, seed=T + D, sink_gap=True)
+    check_decode(q, k, v, D ** -0.5, *to_gpu(q, k, v), num_splits=ns, label=f"D{D} T{T}")
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 7, 8])
+@pytest.mark.parametrize("D", [64, 128])
+def test_group_sizes(gpu, G, D):
+    q, k, v = rand_qkv(2, 4 * G, 4, 777, D, seed=10 * G + D)
+    check_decode(q, k, v, D ** -0.5, *to_gpu(q, k, v), label=f"G{G} D{D}")
+    keep = W.random_block_list(2, 4, O.nblocks(777), 0.4, seed=G)
+    check_decode(q, k, v, D ** -0.5, *to_gpu(q, k, v), keep=keep, num_splits=3, label=f"G{G} D{D} masked")
+
+
+def test_strided_layouts(gpu):
+    """FA2 memory layout [B, T, Hkv, D] seen as [B, Hkv, T, D] (bench/test_decode.py:90-93), a
+    growing-cache view (token stride D, head stride capacity * D), and a batch of 12."""
+    q, k, v = rand_qkv(3, 32, 8, 1500, 128, seed=5)
+    gq, gk, gv = to_gpu(q, k, v)
+    ks = gk.transpose(1, 2).contiguous().transpose(1, 2)
+    vs = gv.transpose(1, 2).contiguous().transpose(1, 2)
+    check_decode(q, k, v, 128 ** -0.5, gq, ks, vs, label="bshd")
+    cap = torch.zeros(3, 8, 2048, 128, dtype=torch.bfloat16, device="cuda")
+    cap2 = torch.zeros_like(cap)
+    cap[:, :, :1500] = gk
+    cap2[:, :, :1500] = gv
+    check_decode(q, k, v, 128 ** -0.5, gq, cap[:, :, :1500], cap2[:, :, :1500], label="capacity view")
+    q, k, v = rand_qkv(12, 32, 8, 700, 128, seed=6)
+    check_decode(q, k, v, 128 ** -0.5, *to_gpu(q, k, v), label="batch12")
+
+
+def test_stats_and_stats_only(gpu):
+    q, k, v = rand_qkv(2, 32, 8, 2000, 128, seed=7, sink_gap=True)
+    gq, gk, gv = to_gpu(q, k, v)
+    scale = 128 ** -0.5
+    r = K.decode(gq, gk, gv, scale, stats=True, num_splits=5)
+    M, S = O.block_stats(q, k, scale)
+    fin = torch.isfinite(M)
+    em = (r["blk_max"].cpu().double() - M)[fin].abs().max().item()
+    es = ((r["blk_sum"].cpu().double() - S) / S)[fin].abs().max().item()
+    lw = (O.block_logw(r["blk_max"].cpu().double(), r["blk_sum"].cpu().double()) - O.block_logw(M, S)).abs().max().item()
+    print(f"stats: max |d blk_max| {em:.2e}, rel d blk_sum {es:.2e}, |d block lse| {lw:.2e}", flush=True)
+    assert em <= LSE_TOL and es <= 2e-4 and lw <= LSE_TOL
+    r2 = K.decode(gq, gk, gv, scale, stats=True, load_v=False)
+    assert torch.equal(r2["blk_max"], r["blk_max"]) and torch.equal(r2["blk_sum"], r["blk_sum"]), \
+        "stats-only differs from dense+stats"
+    assert r2["out"] is None
+    lse = torch.logsumexp(O.scores(q, k, scale), -1)
+    assert (r2["lse"].cpu().double() - lse).abs().max().item() <= LSE_TOL
+
+
+def test_masked_cfg2(gpu):
+    """T 32768, D 128, 32/8 heads, structured K, 35% block list + block stats."""
+    L, keep = W.cfg2()
+    gq, gk, gv = to_gpu(L.q, L.k, L.v)
+    for ns in (None, 1, 5):
+        check_decode(L.q, L.k, L.v, L.scale, gq, gk, gv, keep=keep, num_splits=ns, label="cfg2 masked")
+    plan = K.make_plan(keep.cuda())
+    rms = K.decode(gq, gk, gv, L.scale, plan=plan, stats=True)
+    rd = K.decode(gq, gk, gv, L.scale, stats=True)
+    vis = keep.cuda().repeat_interleave(4, 1)
+    assert torch.isinf(rms["blk_max"][~vis]).all() and (rms["blk_sum"][~vis] == 0).all(), \
+        "masked stats touched a skipped block"
+    assert torch.equal(rms["blk_max"][vis], rd["blk_max"][vis]) and torch.equal(rms["blk_sum"][vis], rd["blk_sum"][vis])
+    M, S = O.block_stats(L.q, L.k, L.scale, keep=keep)
+    x_dev = O.block_logw(rms["blk_max"].cpu().double(), rms["blk_sum"].cpu().double())
+    x_ref = O.block_logw(M, S)
+    fin = torch.isfinite(x_ref)
+    assert torch.equal(torch.isfinite(x_dev), fin)
+    assert (x_dev - x_ref)[fin].abs().max().item() <= LSE_TOL
+    # per query head per block (max, LSE, mass) as the config asks
+    mass_dev = torch.softmax(x_dev.masked_fill(~fin, -math.inf), -1)
+    mass_ref = torch.softmax(x_ref, -1)
+    assert (mass_dev - mass_ref).abs().max().item() <= 1e-4
+    check_decode(L.q, L.k, L.v, L.scale, gq, gk, gv, label="cfg2 dense")
+
+
+def test_write_p_and_two_pass(gpu):
+    q, k, v = rand_qkv(1, 32, 8, 3000, 128, seed=8, sink_gap=True)
+    gq, gk, gv = to_gpu(q, k, v)
+    scale = 128 ** -0.5
+    r = K.decode(gq, gk, gv, scale, stats=True, load_v=False, write_p=True)
+    P = O.p_values(q, k, scale)
+    err = (r["p"].cpu().double() - P).abs().max().item()
+    assert err <= 1e-3, err                                  # fp16 P
+    for rule, val in (("topp", 0.99), ("tau", 1e-4)):
+        r2 = K.vskip_two_pass(gq, gk, gv, scale, rule=rule, value=val, out_f32=True)
+        _, keep = O.vskip_two_pass(q, k, v, scale, rule=rule, value=val)
+        keep_dev = r2["keep"].cpu()
+        mism = (keep_dev != keep).float().mean().item()
+        ref_out, _ = O.decode(q, k, v, scale, keep=keep_dev)   # kernels judged on the set they were given
+        e16 = O.rel_err(r2["out"].cpu(), ref_out)
+        e32 = O.rel_err(r2["out_f32"].cpu(), ref_out)
+        print(f"vskip2 {rule}: kept {keep.float().mean():.3f} (selection mismatch {mism:.4f}) "
+              f"bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
+        assert mism <= 0.01
+        assert e16 <= BF16_TOL and e32 <= 5e-4          # fp16 P bounds the fp32 output error
+
+
+@pytest.mark.parametrize("tau", [1e-4, 1e-3])
+def test_vskip1_sink_and_lse_prev(gpu, tau):
+    """bench/test_decode.py:131-151: kept set equals the fp64 rule's (except decisions within
+    fp32 noise of the threshold), output vs fp64 over that set; with the sink bound and with an
+    exact lse_prev."""
+    q, k, v = rand_qkv(2, 32, 8, 2500, 128, seed=9, sink_gap=True)
+    gq, gk, gv = to_gpu(q, k, v)
+    scale = 128 ** -0.5
+    lse_exact = torch.logsumexp(O.scores(q, k, scale), -1)
+    for lp in (None, lse_exact.float()):
+        r = K.vskip_one_pass(gq, gk, gv, scale, tau=tau, out_f32=True, count=True,
+                             lse_prev=None if lp is None else lp.cuda().contiguous())
+        keep, z = O.vskip1_keep(q, k, scale, tau, 2, lse_prev=lp)
+        vcount_ref = keep.sum(-1)
+        borderline = ((z.abs() < 1e-4) & ~O.always_keep(keep.shape[-1], 2)).sum(-1)
+        diff = (r["v_tiles"].cpu() - vcount_ref).abs()
+        assert (diff <= borderline).all(), (r["v_tiles"], vcount_ref)
+        ref, lse = O.decode(q, k, v, scale, keep=keep)
+        e16 = O.rel_err(r["out"].cpu(), ref)
+        e32 = O.rel_err(r["out_f32"].cpu(), ref)
+        print(f"vskip1 tau {tau:g} lse_prev={lp is not None}: kept {keep.float().mean():.3f} "
+              f"bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
+        assert e16 <= BF16_TOL and e32 <= F32_TOL
+        assert (r["lse"].cpu().double() - lse).abs().max().item() <= LSE_TOL
+
+
+def test_vskip1_cfg3(gpu):
+    """T 65536, no sink, lse_prev = exact normaliser perturbed by +-5%, tau 1e-4."""
+    L = W.cfg3()
+    lse_exact = torch.logsumexp(O.scores(L.q, L.k, L.scale), -1)
+    lp = W.perturbed_lse(lse_exact, seed=33)
+    gq, gk, gv = to_gpu(L.q, L.k, L.v)
+    r = K.vskip_one_pass(gq, gk, gv, L.scale, tau=1e-4, out_f32=True, count=True, lse_prev=lp.cuda())
+    keep, z = O.vskip1_keep(L.q, L.k, L.scale, 1e-4, 2, lse_prev=lp)
+    borderline = ((z.abs() < 1e-4) & ~O.always_keep(keep.shape[-1], 2)).sum(-1)
+    assert ((r["v_tiles"].cpu() - keep.sum(-1)).abs() <= borderline).all()
+    ref, _ = O.decode(L.q, L.k, L.v, L.scale, keep=keep)
+    e16, e32 = O.rel_err(r["out"].cpu(), ref), O.rel_err(r["out_f32"].cpu(), ref)
+    print(f"cfg3 vskip1: V kept {keep.float().mean():.3f} bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
+    assert e16 <= BF16_TOL and e32 <= F32_TOL
+
+
+def test_read_bw(gpu):
+    x = torch.ones(1 << 24, dtype=torch.bfloat16, device="cuda")
+    o = torch.zeros(1, dtype=torch.int32, device="cuda")
+    K.ext().read_bw(x, o, 1024)
+    torch.cuda.synchronize()
+    assert int(o.item()) == 0
