@@ -1,0 +1,511 @@
+// Shared device code of the split-K flash-decode kernels for gfx950 (attn_decode.hip: dense,
+// block-list, per-block statistics, stats-only, fp16 P; attn_vskip.hip: single-pass V-skip,
+// two-pass V-skip pass 2, read ceiling).
+//
+// Work decomposition. num_splits * Hkv * B workgroups of 4 wavefronts; a workgroup owns one
+// contiguous range of "items" (64-token blocks, or entries of a block list) of one KV head
+// and serves all G query heads of that head, so each K/V byte is read once. Workgroups are
+// dispatched round-robin over the 8 XCDs; the launch index is remapped so that consecutive
+// work items (the splits of one KV head) land on the same XCD and share its L2.
+// Inside the workgroup the 4 wavefronts are independent streams: wavefront w takes items w,
+// w+4, ... and keeps its own online-softmax state for the G heads, so the main loop has no
+// workgroup barrier. A wavefront processes a whole 64-token block at a time, so the
+// per-block statistics fall out of its own registers. The 4 states are merged once, in LDS,
+// at the end. With num_splits > 1 each workgroup writes its partial state; the last
+// workgroup of a KV head to arrive (a self-resetting ticket counter) merges all partials in
+// the same kernel.
+//
+// Pipeline per wavefront: K(j) and V(j) are in flight when block j starts; after QK(j) the K
+// loads of block j+1 are issued, after PV(j) its V loads. The last block is peeled off the
+// loop so every load in the loop is unconditional (exact wait counts).
+//
+// QK runs on one of two engines (chosen per launch, KVSKIP_AMD_QK=valu|mfma):
+//   mfma  v_mfma_f32_16x16x32_bf16 with the G query heads as the 16 M rows (zero-padded), 16
+//         tokens as N and 32 dims as K: Q is 4 VGPRs per 32 dims whatever G, a 64-token block
+//         is 4 x (D/32) MFMAs, and the scores come out as lane (j = lane/16, c = lane%16)
+//         holding heads 4j..4j+3 of token c of each 16-token tile; block max / sum are 4-step
+//         DPP reductions inside the 16-lane row.
+//   valu  (below) dot products on v_dot2_f32_bf16.
+// Lane layouts (64 lanes, D = 64 or 128):
+//   K   8 lanes per token row, 8 rows per load; lane (r8 = lane/8, sub = lane%8) holds rows
+//       8*rg + r8 (rg = 0..7), dims [8 sub, 8 sub + 8) (+64 for D = 128), as packed bf16.
+//       QK = v_dot2_f32_bf16 against the unscaled bf16 query (exact products, fp32 sums),
+//       then a 3-step DPP sum over the 8 lanes of the row; the score is scaled after.
+//   V   D/8 lanes per row, 8 dims per lane, 16-byte loads; lane accumulates its rows for
+//       all G heads in fp32 (acc[G][8]); P reaches the V layout through a per-wavefront
+//       LDS tile [64][G] written after the softmax.
+// Softmax runs in log2 units (v_exp_f32); per head and block: block max mt, e = 2^(s - mt)
+// (the block statistics), p = e * 2^(mt - m_run). K/V are read through buffer resources
+// bounded to the head's rows, so rows past T read as zeros; their scores are masked to -inf.
+#pragma once
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace kvs {
+namespace {
+
+constexpr int NWAVE = 4;
+constexpr int NT = NWAVE * WAVE;
+
+template <int D>
+struct Lay {
+  static_assert(D == 64 || D == 128, "head dim");
+  static constexpr int KC = D / 64;         // 16-byte K chunks per lane per row
+  static constexpr int VLPR = D / 8;        // lanes per V row
+  static constexpr int VRPI = WAVE / VLPR;  // V rows per load instruction
+  static constexpr int VN = BLK / VRPI;     // V load instructions per block
+};
+
+template <int G>
+constexpr int gpad() {
+  return G <= 4 ? 4 : 8;
+}
+
+// Work coordinates of this workgroup: the launch index i is dispatched to XCD i % 8; work item
+// w = (i % 8) * (n / 8) + i / 8 gives each XCD a contiguous run of work items.
+__device__ __forceinline__ void work_coords(int S, int Hkv, int B, int& split, int& h, int& b) {
+  const int n = S * Hkv * B;
+  int i = blockIdx.x;
+  if (n % 8 == 0) i = (i % 8) * (n / 8) + i / 8;
+  split = i % S;
+  const int r = i / S;
+  h = r % Hkv;
+  b = r / Hkv;
+}
+
+// Byte range of one (b, head) of a K or V view: rows 0..T-1 of D bf16 each, row stride st.
+__device__ __forceinline__ uint32_t head_bytes(int T, int64_t st, int D) {
+  return static_cast<uint32_t>((static_cast<int64_t>(T - 1) * st + D) * 2);
+}
+
+// K block at token t0: lane (r8, sub) gets rows t0 + 8 rg + r8, 16-byte chunks sub (+8).
+// koff = r8 * k_st * 2 + 16 * sub (per lane, fixed).
+template <int D>
+__device__ __forceinline__ void load_k_block(u32x4 (&kr)[8][Lay<D>::KC], rsrc_t rk, uint32_t koff, int64_t k_st,
+                                             int t0) {
+  const uint32_t rowb = static_cast<uint32_t>(k_st * 2);
+#pragma unroll
+  for (int rg = 0; rg < 8; ++rg) {
+    const uint32_t so = static_cast<uint32_t>(t0 + 8 * rg) * rowb;
+#pragma unroll
+    for (int c = 0; c < Lay<D>::KC; ++c) kr[rg][c] = bload16<BUF_NT>(rk, koff + 128 * c, so);
+  }
+}
+
+// V block at token t0: lane (vrow, vsub) gets rows t0 + VRPI i + vrow, dims 8 vsub .. +8.
+// voff = vrow * v_st * 2 + 16 * vsub.
+template <int D>
+__device__ __forceinline__ void load_v_block(u32x4 (&vr)[Lay<D>::VN], rsrc_t rv, uint32_t voff, int64_t v_st,
+                                             int t0) {
+  constexpr int VRPI = Lay<D>::VRPI;
+  const uint32_t rowb = static_cast<uint32_t>(v_st * 2);
+#pragma unroll
+  for (int i = 0; i < Lay<D>::VN; ++i)
+    vr[i] = bload16<BUF_NT>(rv, voff, static_cast<uint32_t>(t0 + VRPI * i) * rowb);
+}
+
+// Scores of one block in log2 units: s[rg][g] for row 8*rg + lane/8; rows t0 + r >= t_lim are
+// masked to -inf (t_lim = T, or 0 for an invalid list entry).
+template <int D, int G>
+__device__ __forceinline__ void qk_block(float (&s)[8][G], const u32x4 (&kr)[8][Lay<D>::KC],
+                                         const u32x4 (&qv)[G][Lay<D>::KC], float scale_log2, int t0, int t_lim,
+                                         int lane) {
+#pragma unroll
+  for (int rg = 0; rg < 8; ++rg)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float a = 0.f;
+#pragma unroll
+      for (int c = 0; c < Lay<D>::KC; ++c) a = dot8(qv[g][c], kr[rg][c], a);
+      s[rg][g] = a;
+    }
+#pragma unroll
+  for (int rg = 0; rg < 8; ++rg)
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[rg][g] = sum8(s[rg][g]);
+  const int r8 = lane >> 3;
+#pragma unroll
+  for (int rg = 0; rg < 8; ++rg) {
+    const bool ok = t0 + 8 * rg + r8 < t_lim;
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[rg][g] = ok ? s[rg][g] * scale_log2 : NEG_INF;
+  }
+}
+
+// acc[g][e] += sum over the block's rows of P[row][g] * V[row][dims of this lane].
+template <int D, int G>
+__device__ __forceinline__ void pv_block(float (&acc)[G][8], const u32x4 (&vr)[Lay<D>::VN], const float* sPw,
+                                         int lane) {
+  constexpr int GP = gpad<G>();
+  constexpr int VRPI = Lay<D>::VRPI;
+  const int vrow = lane / Lay<D>::VLPR;
+#pragma unroll
+  for (int i = 0; i < Lay<D>::VN; ++i) {
+    const float* pr = sPw + (VRPI * i + vrow) * GP;
+    float pg[GP];
+#pragma unroll
+    for (int u = 0; u < GP; u += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(pr + u);
+      pg[u] = t.x;
+      pg[u + 1] = t.y;
+      pg[u + 2] = t.z;
+      pg[u + 3] = t.w;
+    }
+    float vf[8];
+    vf[0] = bf_lo(vr[i].x);
+    vf[1] = bf_hi(vr[i].x);
+    vf[2] = bf_lo(vr[i].y);
+    vf[3] = bf_hi(vr[i].y);
+    vf[4] = bf_lo(vr[i].z);
+    vf[5] = bf_hi(vr[i].z);
+    vf[6] = bf_lo(vr[i].w);
+    vf[7] = bf_hi(vr[i].w);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
+  }
+}
+
+// Sum acc over the lanes that hold the same dims (the V row slots).
+template <int D, int G>
+__device__ __forceinline__ void reduce_acc_rows(float (&acc)[G][8]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = acc[g][e];
+      if constexpr (D == 64) a += dpp<DPP_ROR8>(a);
+      a += xshfl(a, 16);
+      a += xshfl(a, 32);
+      acc[g][e] = a;
+    }
+}
+
+// LDS of the workgroup epilogue.
+template <int D, int G>
+struct MergeLds {
+  float acc[NWAVE * G * D];            // per-wavefront accumulators
+  float ml[NWAVE * G * 2];             // per-wavefront (m, l)
+  float w[G * MAX_SPLITS];             // split weights 2^(m_s - M) (last workgroup)
+  float red[NT * 4];                   // partial sums of the split merge
+  float gml[G * 2];                    // merged (M, L) per head
+  int last;
+};
+
+// Last workgroup of a KV head: merge the num_splits partials of its G heads and write the
+// outputs. plain: the partials simply add up (two-pass pass 2).
+template <int D, int G, bool LOAD_V>
+__device__ __forceinline__ void merge_splits(const AttnP& p, int64_t hq0, MergeLds<D, G>& L, bool plain) {
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int S = p.num_splits;
+  for (int g = wave; g < G; g += NWAVE) {
+    const float* ml = p.part_ml + (hq0 + g) * S * 2;
+    float mx = NEG_INF;
+    if (!plain)
+      for (int s = lane; s < S; s += WAVE) mx = fmaxf(mx, ml[2 * s]);
+    mx = wave_max(mx);
+    const float mu = mx == NEG_INF ? 0.f : mx;
+    float ls = 0.f;
+    for (int s = lane; s < S; s += WAVE) {
+      const float w = plain ? 1.f : fexp2(ml[2 * s] - mu);
+      L.w[g * MAX_SPLITS + s] = w;
+      if (!plain) ls += ml[2 * s + 1] * w;
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) {
+      L.gml[2 * g] = mx;
+      L.gml[2 * g + 1] = plain ? 1.f : ls;
+    }
+  }
+  __syncthreads();
+  if constexpr (LOAD_V) {
+    constexpr int NQ = G * D / 4;            // output quads
+    constexpr int TPQ = NT / NQ;             // threads per quad (>= 1)
+    if (tid < NQ * TPQ) {
+      const int qd = tid % NQ, part = tid / NQ;
+      const int g = qd / (D / 4), d4 = qd % (D / 4);
+      const float* pa = p.part_acc + (hq0 + g) * S * D + 4 * d4;
+      const float* w = L.w + g * MAX_SPLITS;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+      for (int s = part; s < S; s += TPQ) {
+        const float4 v = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D);
+        const float f = w[s];
+        a.x = fmaf(v.x, f, a.x);
+        a.y = fmaf(v.y, f, a.y);
+        a.z = fmaf(v.z, f, a.z);
+        a.w = fmaf(v.w, f, a.w);
+      }
+      *reinterpret_cast<float4*>(L.red + 4 * (part * NQ + qd)) = a;
+    }
+    __syncthreads();
+    if (tid < NQ) {
+      const int qd = tid, g = qd / (D / 4), d4 = qd % (D / 4);
+      float4 a = *reinterpret_cast<const float4*>(L.red + 4 * qd);
+      for (int t = 1; t < TPQ; ++t) {
+        const float4 b4 = *reinterpret_cast<const float4*>(L.red + 4 * (t * NQ + qd));
+        a.x += b4.x;
+        a.y += b4.y;
+        a.z += b4.z;
+        a.w += b4.w;
+      }
+      const float l = L.gml[2 * g + 1];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float o[4] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv};
+      const int64_t base = (hq0 + g) * D + 4 * d4;
+      const uint32_t lo = static_cast<uint32_t>(f2bf(o[0])) | (static_cast<uint32_t>(f2bf(o[1])) << 16);
+      const uint32_t hi = static_cast<uint32_t>(f2bf(o[2])) | (static_cast<uint32_t>(f2bf(o[3])) << 16);
+      *reinterpret_cast<uint2*>(p.out + base) = make_uint2(lo, hi);
+      if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + base) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  if (!plain && tid < G && p.lse) {
+    const float M = L.gml[2 * tid], l = L.gml[2 * tid + 1];
+    p.lse[hq0 + tid] = l > 0.f ? (M + flog2(l)) * LN2 : NEG_INF;
+  }
+}
+
+// Workgroup epilogue: merge the 4 wavefront states (m, l in log2 units, acc un-normalised),
+// then write out/out_f32/lse (one split) or the split partials (+ the in-kernel split merge).
+template <int D, int G, bool LOAD_V>
+__device__ __forceinline__ void finish(const AttnP& p, float (&m)[G], float (&l)[G], float (&acc)[G][8], int b,
+                                       int h, int split, MergeLds<D, G>& L, bool plain) {
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  constexpr int VLPR = Lay<D>::VLPR;
+  if constexpr (LOAD_V) {
+    reduce_acc_rows<D, G>(acc);
+    if (lane < VLPR) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) L.acc[(wave * G + g) * D + 8 * lane + e] = acc[g][e];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      L.ml[(wave * G + g) * 2] = m[g];
+      L.ml[(wave * G + g) * 2 + 1] = l[g];
+    }
+  }
+  __syncthreads();
+  const int S = p.num_splits;
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+  if constexpr (LOAD_V) {
+    for (int o = tid; o < G * D; o += NT) {
+      const int g = o / D, d = o % D;
+      float A = 0.f, Ls = 0.f;
+      if (plain) {
+#pragma unroll
+        for (int w = 0; w < NWAVE; ++w) A += L.acc[(w * G + g) * D + d];
+        Ls = 1.f;
+      } else {
+        float M = NEG_INF;
+#pragma unroll
+        for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, L.ml[(w * G + g) * 2]);
+        const float mu = M == NEG_INF ? 0.f : M;
+#pragma unroll
+        for (int w = 0; w < NWAVE; ++w) {
+          const float f = fexp2(L.ml[(w * G + g) * 2] - mu);
+          Ls += L.ml[(w * G + g) * 2 + 1] * f;
+          A += L.acc[(w * G + g) * D + d] * f;
+        }
+      }
+      const int64_t hq = hq0 + g;
+      if (S == 1) {
+        const float o_ = Ls > 0.f ? A / Ls : 0.f;
+        p.out[hq * D + d] = f2bf(o_);
+        if (p.out_f32) p.out_f32[hq * D + d] = o_;
+      } else {
+        p.part_acc[(hq * S + split) * D + d] = A;
+      }
+    }
+  }
+  if (!plain && tid < G) {
+    const int g = tid;
+    float M = NEG_INF, Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, L.ml[(w * G + g) * 2]);
+    const float mu = M == NEG_INF ? 0.f : M;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) Ls += L.ml[(w * G + g) * 2 + 1] * fexp2(L.ml[(w * G + g) * 2] - mu);
+    const int64_t hq = hq0 + g;
+    if (S == 1) {
+      if (p.lse) p.lse[hq] = Ls > 0.f ? (M + flog2(Ls)) * LN2 : NEG_INF;
+    } else {
+      p.part_ml[(hq * S + split) * 2] = M;
+      p.part_ml[(hq * S + split) * 2 + 1] = Ls;
+    }
+  }
+  if (S == 1 || p.ticket == nullptr) return;
+  // Publish this partial, take a ticket; the last arrival merges.
+  __threadfence();
+  __syncthreads();
+  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  if (tid == 0) L.last = atomicAdd(p.ticket + bh, 1) == S - 1;
+  __syncthreads();
+  if (!L.last) return;
+  __threadfence();
+  merge_splits<D, G, LOAD_V>(p, hq0, L, plain);
+  if (tid == 0) p.ticket[bh] = 0;
+}
+
+template <int D, int G>
+__device__ __forceinline__ void load_q(u32x4 (&qv)[G][Lay<D>::KC], const AttnP& p, int b, int h, int lane) {
+  const int sub = lane & 7;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint16_t* qp = p.q + b * p.q_sb + (static_cast<int64_t>(h) * G + g) * p.q_sh + 8 * sub;
+#pragma unroll
+    for (int c = 0; c < Lay<D>::KC; ++c) qv[g][c] = ld16(qp + 64 * c);
+  }
+}
+
+// One block's softmax step for head g: updates (m, l), returns alpha (rescale of acc) and the
+// factor c with p = e * c; e = 2^(s - mt) and the block stats (mt, st) are left for the caller.
+template <int G>
+__device__ __forceinline__ void block_softmax(const float (&s)[8][G], int g, float& m, float& l, float (&e)[8],
+                                              float& mt, float& st, float& alpha, float& c) {
+  float x = s[0][g];
+#pragma unroll
+  for (int rg = 1; rg < 8; ++rg) x = fmaxf(x, s[rg][g]);
+  mt = max_rows8(x);
+  const float mtu = mt == NEG_INF ? 0.f : mt;
+  float sum = 0.f;
+#pragma unroll
+  for (int rg = 0; rg < 8; ++rg) {
+    e[rg] = fexp2(s[rg][g] - mtu);
+    sum += e[rg];
+  }
+  st = sum_rows8(sum);
+  const float m_new = fmaxf(m, mt);
+  const float mu = m_new == NEG_INF ? 0.f : m_new;
+  alpha = fexp2(m - mu);
+  c = mt == NEG_INF ? 0.f : fexp2(mt - mu);
+  l = l * alpha + st * c;
+  m = m_new;
+}
+
+
+// ---------------------------------------------------------------- MFMA QK engine
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct MLay {
+  static constexpr int KS = D / 32;  // 32-dim k-steps of v_mfma_f32_16x16x32_bf16
+};
+
+// Sum / max over the 16 lanes of each DPP row (every lane gets the row result).
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<DPP_XOR1>(v);
+  v += dpp<DPP_XOR2>(v);
+  v += dpp<DPP_HALF_MIRROR>(v);
+  return v + dpp<DPP_MIRROR>(v);
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  v = fmaxf(v, dpp<DPP_XOR2>(v));
+  v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  return fmaxf(v, dpp<DPP_MIRROR>(v));
+}
+
+// Lane value of another lane as a uniform (scalar) value.
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// B operand (K^T) of one 64-token block: kr[nt][kk] = 16 bytes of row t0 + 16 nt + lane%16 at
+// 16-byte chunk 4 kk + lane/16. koffm = (lane % 16) * k_st * 2 + 16 * (lane / 16).
+template <int D>
+__device__ __forceinline__ void load_k_block_mf(u32x4 (&kr)[4][MLay<D>::KS], rsrc_t rk, uint32_t koffm,
+                                                int64_t k_st, int t0) {
+  const uint32_t rowb = static_cast<uint32_t>(k_st * 2);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const uint32_t so = static_cast<uint32_t>(t0 + 16 * nt) * rowb;
+#pragma unroll
+    for (int kk = 0; kk < MLay<D>::KS; ++kk) kr[nt][kk] = bload16<BUF_NT>(rk, koffm + 64 * kk, so);
+  }
+}
+
+// A operand (Q): lane (j, c = lane%16) holds head c's dims of chunk 4 kk + j (zero for c >= G).
+template <int D, int G>
+__device__ __forceinline__ void load_q_mf(u32x4 (&qa)[MLay<D>::KS], const AttnP& p, int b, int h, int lane) {
+  const int c = lane & 15, j = lane >> 4;
+  const uint16_t* qp = p.q + b * p.q_sb + (static_cast<int64_t>(h) * G + c) * p.q_sh + 8 * j;
+#pragma unroll
+  for (int kk = 0; kk < MLay<D>::KS; ++kk) qa[kk] = c < G ? ld16(qp + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Scores of one block in log2 units, MFMA layout: s[nt][i] = head 4*(lane/16) + i, token
+// t0 + 16 nt + lane%16; tokens >= t_lim masked to -inf.
+template <int D>
+__device__ __forceinline__ void qk_block_mf(float (&s)[4][4], const u32x4 (&kr)[4][MLay<D>::KS],
+                                            const u32x4 (&qa)[MLay<D>::KS], float scale_log2, int t0, int t_lim,
+                                            int lane) {
+  const int c = lane & 15;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    f32x4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < MLay<D>::KS; ++kk)
+      a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[kk]),
+                                                  __builtin_bit_cast(bf16x8_t, kr[nt][kk]), a, 0, 0, 0);
+    const bool ok = t0 + 16 * nt + c < t_lim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[nt][i] = ok ? a[i] * scale_log2 : NEG_INF;
+  }
+}
+
+// Log-sum-exp merge of the split partials when no ticket array is given; one workgroup per
+// (b, query head), one thread per dim. With out == nullptr (stats-only) only lse is produced.
+template <int D>
+__global__ void __launch_bounds__(D) combine_kernel(const AttnP p) {
+  const int64_t hq = blockIdx.x;
+  const int d = threadIdx.x;
+  const int S = p.num_splits;
+  const float* ml = p.part_ml + hq * S * 2;
+  float M = NEG_INF;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+  const float mu = M == NEG_INF ? 0.f : M;
+  float L = 0.f, A = 0.f;
+  const bool with_v = p.out != nullptr;
+  for (int s = 0; s < S; ++s) {
+    const float w = fexp2(ml[2 * s] - mu);
+    L += ml[2 * s + 1] * w;
+    if (with_v) A += p.part_acc[(hq * S + s) * D + d] * w;
+  }
+  if (with_v) {
+    const float o = L > 0.f ? A / L : 0.f;
+    p.out[hq * D + d] = f2bf(o);
+    if (p.out_f32) p.out_f32[hq * D + d] = o;
+  }
+  if (d == 0 && p.lse) p.lse[hq] = L > 0.f ? (M + flog2(L)) * LN2 : NEG_INF;
+}
+
+template <int D>
+__global__ void __launch_bounds__(D) combine_sum_kernel(const AttnP p) {
+  const int64_t hq = blockIdx.x;
+  const int d = threadIdx.x;
+  float A = 0.f;
+  for (int s = 0; s < p.num_splits; ++s) A += p.part_acc[(hq * p.num_splits + s) * D + d];
+  p.out[hq * D + d] = f2bf(A);
+  if (p.out_f32) p.out_f32[hq * D + d] = A;
+}
+
+
+inline dim3 attn_grid(const AttnP& p) { return dim3(p.num_splits * p.Hkv * p.B); }
+
+// Instantiated group sizes.
+#define KVS_FOR_G(X, D) \
+  X(D, 1)               \
+  X(D, 2)               \
+  X(D, 4)               \
+  X(D, 7)               \
+  X(D, 8)
+
+}  // namespace
+}  // namespace kvs

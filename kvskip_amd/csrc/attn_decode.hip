@@ -1,0 +1,255 @@
+// Split-K decode attention: dense or over block lists, with optional per-block statistics,
+// stats-only (K only) and fp16 P. Both QK engines (MFMA, VALU dot2); see attn_common.hpp.
+#include "attn_common.hpp"
+
+namespace kvs {
+namespace {
+
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF>
+__global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
+  constexpr int GP = gpad<G>();
+  __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
+  __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
+
+  int split, h, b;
+  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int r8 = lane >> 3, sub = lane & 7;
+
+  int n_items;
+  const int* list = nullptr;
+  if constexpr (MASKED) {
+    n_items = min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
+    list = p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks;
+  } else {
+    n_items = p.nb;
+  }
+  const int per = (n_items + p.num_splits - 1) / p.num_splits;
+  const int i0 = min(n_items, split * per);
+  const int n = min(n_items, i0 + per) - i0;
+  const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
+
+  const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(p.T, p.k_st, D));
+  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, LOAD_V ? head_bytes(p.T, p.v_st, D) : 0);
+  const uint32_t voff = static_cast<uint32_t>((lane / Lay<D>::VLPR) * p.v_st * 2 + 16 * (lane % Lay<D>::VLPR));
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  float* sPw = sP[wave];
+
+  // Block of this wavefront's k-th item; out-of-range list entries read block 0 and are masked.
+  auto block_of = [&](int k) -> int {
+    const int blk = MASKED ? list[i0 + wave + NWAVE * k] : i0 + wave + NWAVE * k;
+    return (blk >= 0 && blk < p.nb) ? blk : -1;
+  };
+  auto accumulate = [&](const u32x4 (&vr)[Lay<D>::VN], const float (&alpha)[G]) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= alpha[g];
+    pv_block<D, G>(acc, vr, sPw, lane);
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  float m[G], l[G];
+  if constexpr (MF) {
+    // ---- MFMA engine: K(j) and V(j) both prefetched one block ahead.
+    constexpr int KS = MLay<D>::KS;
+    constexpr int NI = G < 4 ? G : 4;               // score rows i in use per lane group
+    const int j4 = lane >> 4, c16 = lane & 15;
+    const uint32_t koffm = static_cast<uint32_t>(c16 * p.k_st * 2 + 16 * j4);
+    u32x4 qa[KS];
+    load_q_mf<D, G>(qa, p, b, h, lane);
+    float mr[4], lr[4];                             // running (m, l) of head 4 j4 + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mr[i] = NEG_INF;
+      lr[i] = 0.f;
+    }
+    auto process = [&](int blk, const u32x4 (&kr)[4][KS], float (&alpha)[G]) {
+      const int t0 = blk >= 0 ? blk * BLK : 0;
+      float s[4][4];
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, blk >= 0 ? p.T : 0, lane);
+      float pv[4][4], ar[4];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int g = 4 * j4 + i;
+        const float mt = row16_max(fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i])));
+        const float mtu = mt == NEG_INF ? 0.f : mt;
+        float e[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) e[nt] = fexp2(s[nt][i] - mtu);
+        const float st = row16_sum((e[0] + e[1]) + (e[2] + e[3]));
+        const float m_new = fmaxf(mr[i], mt);
+        const float mu = m_new == NEG_INF ? 0.f : m_new;
+        ar[i] = fexp2(mr[i] - mu);
+        const float cf = mt == NEG_INF ? 0.f : fexp2(mt - mu);
+        lr[i] = lr[i] * ar[i] + st * cf;
+        mr[i] = m_new;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) pv[nt][i] = e[nt] * cf;
+        if constexpr (STATS) {
+          if (blk >= 0 && g < G) {
+            const int64_t hq = hq0 + g;
+            if (c16 == 0) {
+              p.blk_max[hq * p.nb + blk] = mt * LN2;
+              p.blk_sum[hq * p.nb + blk] = st;
+            }
+            if (p.p_out != nullptr) {
+#pragma unroll
+              for (int nt = 0; nt < 4; ++nt) p.p_out[hq * p.t_pad + t0 + 16 * nt + c16] = f2h(e[nt]);
+            }
+          }
+        }
+      }
+      if constexpr (LOAD_V) {
+        if (4 * j4 < GP) {
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+            *reinterpret_cast<float4*>(sPw + (16 * nt + c16) * GP + 4 * j4) =
+                make_float4(pv[nt][0], NI > 1 ? pv[nt][1] : 0.f, NI > 2 ? pv[nt][2] : 0.f, NI > 3 ? pv[nt][3] : 0.f);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) alpha[g] = lane_value(ar[g % 4], 16 * (g / 4));
+    };
+    if (nw > 0) {
+      u32x4 kr[4][KS];
+      u32x4 vr[Lay<D>::VN];
+      int blk = block_of(0);
+      load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk, 0) * BLK);
+      if constexpr (LOAD_V) load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+      for (int k = 0; k + 1 < nw; ++k) {
+        const int blk_n = block_of(k + 1);
+        float alpha[G];
+        process(blk, kr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk_n, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) {
+          accumulate(vr, alpha);
+          __builtin_amdgcn_sched_barrier(0);
+          load_v_block<D>(vr, rv, voff, p.v_st, max(blk_n, 0) * BLK);
+        }
+        blk = blk_n;
+      }
+      float alpha[G];
+      process(blk, kr, alpha);
+      if constexpr (LOAD_V) accumulate(vr, alpha);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = lane_value(mr[g % 4], 16 * (g / 4));
+      l[g] = lane_value(lr[g % 4], 16 * (g / 4));
+    }
+  } else {
+    // ---- VALU engine: V(j) issued after QK(j), together with K(j+1) (register budget).
+    const uint32_t koff = static_cast<uint32_t>(r8 * p.k_st * 2 + 16 * sub);
+    u32x4 qv[G][Lay<D>::KC];
+    load_q<D, G>(qv, p, b, h, lane);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = NEG_INF;
+      l[g] = 0.f;
+    }
+    auto process = [&](int blk, const u32x4 (&kr)[8][Lay<D>::KC], float (&alpha)[G]) {
+      const int t0 = blk >= 0 ? blk * BLK : 0;
+      float s[8][G];
+      qk_block<D, G>(s, kr, qv, p.scale_log2, t0, blk >= 0 ? p.T : 0, lane);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float e[8], mt, st, c;
+        block_softmax<G>(s, g, m[g], l[g], e, mt, st, alpha[g], c);
+        if constexpr (STATS) {
+          if (blk >= 0) {
+            const int64_t hq = hq0 + g;
+            if (lane == 0) {
+              p.blk_max[hq * p.nb + blk] = mt * LN2;
+              p.blk_sum[hq * p.nb + blk] = st;
+            }
+            if (p.p_out != nullptr && sub == g) {
+#pragma unroll
+              for (int rg = 0; rg < 8; ++rg) p.p_out[hq * p.t_pad + t0 + 8 * rg + r8] = f2h(e[rg]);
+            }
+          }
+        }
+        if constexpr (LOAD_V) {
+          if (sub == 0) {
+#pragma unroll
+            for (int rg = 0; rg < 8; ++rg) sPw[(8 * rg + r8) * GP + g] = e[rg] * c;
+          }
+        }
+      }
+    };
+    if (nw > 0) {
+      u32x4 kr[8][Lay<D>::KC];
+      u32x4 vr[Lay<D>::VN];
+      int blk = block_of(0);
+      load_k_block<D>(kr, rk, koff, p.k_st, max(blk, 0) * BLK);
+      for (int k = 0; k + 1 < nw; ++k) {
+        const int blk_n = block_of(k + 1);
+        float alpha[G];
+        process(blk, kr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+        load_k_block<D>(kr, rk, koff, p.k_st, max(blk_n, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) accumulate(vr, alpha);
+        blk = blk_n;
+      }
+      float alpha[G];
+      process(blk, kr, alpha);
+      if constexpr (LOAD_V) {
+        load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+        accumulate(vr, alpha);
+      }
+    }
+  }
+  finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
+}
+
+template <int D, int G, bool M, bool ST, bool LV>
+hipError_t launch_decode_t(const AttnP& p, bool mf, hipStream_t s) {
+  if (mf)
+    hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true>), attn_grid(p), dim3(NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false>), attn_grid(p), dim3(NT), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.num_splits > 1 && p.ticket == nullptr) {
+    hipLaunchKernelGGL((combine_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+template <int D, int G>
+hipError_t dispatch_flags(const AttnP& p, bool masked, bool stats, bool load_v, bool mf, hipStream_t s) {
+  if (!masked && !stats && load_v) return launch_decode_t<D, G, false, false, true>(p, mf, s);
+  if (!masked && stats && load_v) return launch_decode_t<D, G, false, true, true>(p, mf, s);
+  if (!masked && stats && !load_v) return launch_decode_t<D, G, false, true, false>(p, mf, s);
+  if (masked && !stats && load_v) return launch_decode_t<D, G, true, false, true>(p, mf, s);
+  if (masked && stats && load_v) return launch_decode_t<D, G, true, true, true>(p, mf, s);
+  if (masked && stats && !load_v) return launch_decode_t<D, G, true, true, false>(p, mf, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_decode(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, hipStream_t s) {
+  const bool mf = qk_use_mfma();
+#define KVS_CASE(DD, GG) \
+  if (D == DD && G == GG) return dispatch_flags<DD, GG>(p, masked, stats, load_v, mf, s);
+  KVS_FOR_G(KVS_CASE, 64)
+  KVS_FOR_G(KVS_CASE, 128)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace kvs

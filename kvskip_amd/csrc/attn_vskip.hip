@@ -1,0 +1,380 @@
+// Single-pass V-skip (both QK engines), two-pass V-skip pass 2, and the streaming read
+// ceiling; see attn_common.hpp for the shared decomposition and layouts.
+#include "attn_common.hpp"
+
+namespace kvs {
+namespace {
+
+// Single-pass V-skip. Per block: QK -> block log-sum-exp per head (log2 units) -> the
+// group's vote -> only then the V loads of that block; the next block's K loads are issued
+// right after, so V(i) overlaps QK(i+1)'s loads. The softmax update and P of a block are
+// computed as if the block were kept and committed only if the group keeps it.
+template <int D, int G, bool MF>
+__global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
+  constexpr int GP = gpad<G>();
+  __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
+  __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
+  __shared__ float sLse0[G];
+  __shared__ int sLoaded[NWAVE];
+
+  int split, h, b;
+  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int r8 = lane >> 3, sub = lane & 7;
+  const int nb = p.nb;
+  const int per = (nb + p.num_splits - 1) / p.num_splits;
+  const int i0 = min(nb, split * per);
+  const int n = min(nb, i0 + per) - i0;
+  const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;
+  const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(p.T, p.k_st, D));
+  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, head_bytes(p.T, p.v_st, D));
+  const uint32_t voff = static_cast<uint32_t>((lane / Lay<D>::VLPR) * p.v_st * 2 + 16 * (lane % Lay<D>::VLPR));
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  float* sPw = sP[wave];
+  int loaded = 0;
+  float m[G], l[G];
+  u32x4 vr[Lay<D>::VN];
+  auto pv = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    pv_block<D, G>(acc, vr, sPw, lane);
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  if constexpr (MF) {
+    constexpr int KS = MLay<D>::KS;
+    constexpr int NI = G < 4 ? G : 4;
+    const int j4 = lane >> 4, c16 = lane & 15;
+    const uint32_t koffm = static_cast<uint32_t>(c16 * p.k_st * 2 + 16 * j4);
+    u32x4 qa[KS];
+    load_q_mf<D, G>(qa, p, b, h, lane);
+    u32x4 kr[4][KS];
+    // normaliser estimate (log2 units) per head: lse_prev, or the block-0 log-sum-exp
+    if (p.lse_prev != nullptr) {
+      if (tid < G) sLse0[tid] = p.lse_prev[hq0 + tid] * LOG2E;
+    } else if (wave == 0) {
+      load_k_block_mf<D>(kr, rk, koffm, p.k_st, 0);
+      float s[4][4];
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, 0, p.T, lane);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float mt = row16_max(fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i])));
+        float sum = 0.f;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) sum += fexp2(s[nt][i] - mt);
+        const float lse0 = mt + flog2(row16_sum(sum));
+        const int g = 4 * j4 + i;
+        if (c16 == 0 && g < G) sLse0[g] = lse0;
+      }
+    }
+    __syncthreads();
+    float lse0r[4], mr[4], lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int g = 4 * j4 + i;
+      lse0r[i] = g < G ? sLse0[g] : 0.f;
+      mr[i] = NEG_INF;
+      lr[i] = 0.f;
+    }
+    if (nw > 0) load_k_block_mf<D>(kr, rk, koffm, p.k_st, (i0 + wave) * BLK);
+    for (int k = 0; k < nw; ++k) {
+      const int blk = i0 + wave + NWAVE * k;
+      const int t0 = blk * BLK;
+      const bool more = k + 1 < nw;
+      float s[4][4];
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, p.T, lane);
+      float tm[4], tl[4], ta[4], pv4[4][4];
+      bool vote = false;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int g = 4 * j4 + i;
+        const float mt = row16_max(fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i])));
+        const float mtu = mt == NEG_INF ? 0.f : mt;
+        float e[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) e[nt] = fexp2(s[nt][i] - mtu);
+        const float st = row16_sum((e[0] + e[1]) + (e[2] + e[3]));
+        vote = vote || (g < G && mtu + flog2(st) - lse0r[i] >= p.log2_tau);
+        const float m_new = fmaxf(mr[i], mt);
+        const float mu = m_new == NEG_INF ? 0.f : m_new;
+        ta[i] = fexp2(mr[i] - mu);
+        const float cf = mt == NEG_INF ? 0.f : fexp2(mt - mu);
+        tl[i] = lr[i] * ta[i] + st * cf;
+        tm[i] = m_new;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) pv4[nt][i] = e[nt] * cf;
+      }
+      // P as if kept (unused otherwise), before any load is issued
+      if (4 * j4 < GP) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          *reinterpret_cast<float4*>(sPw + (16 * nt + c16) * GP + 4 * j4) = make_float4(
+              pv4[nt][0], NI > 1 ? pv4[nt][1] : 0.f, NI > 2 ? pv4[nt][2] : 0.f, NI > 3 ? pv4[nt][3] : 0.f);
+      }
+      const bool need = blk == 0 || blk >= nb - p.local || __ballot(vote) != 0;
+      __builtin_amdgcn_sched_barrier(0);
+      if (need) {
+        ++loaded;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          mr[i] = i < NI ? tm[i] : mr[i];
+          lr[i] = i < NI ? tl[i] : lr[i];
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float a = lane_value(ta[g % 4], 16 * (g / 4));
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[g][u] *= a;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_v_block<D>(vr, rv, voff, p.v_st, t0);
+        if (more) load_k_block_mf<D>(kr, rk, koffm, p.k_st, (blk + NWAVE) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        pv();
+      } else if (more) {
+        load_k_block_mf<D>(kr, rk, koffm, p.k_st, (blk + NWAVE) * BLK);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = lane_value(mr[g % 4], 16 * (g / 4));
+      l[g] = lane_value(lr[g % 4], 16 * (g / 4));
+    }
+  } else {
+    const uint32_t koff = static_cast<uint32_t>(r8 * p.k_st * 2 + 16 * sub);
+    u32x4 qv[G][Lay<D>::KC];
+    load_q<D, G>(qv, p, b, h, lane);
+    u32x4 kr[8][Lay<D>::KC];
+    if (p.lse_prev != nullptr) {
+      if (tid < G) sLse0[tid] = p.lse_prev[hq0 + tid] * LOG2E;
+    } else if (wave == 0) {
+      load_k_block<D>(kr, rk, koff, p.k_st, 0);
+      float s[8][G];
+      qk_block<D, G>(s, kr, qv, p.scale_log2, 0, p.T, lane);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float x = s[0][g];
+#pragma unroll
+        for (int rg = 1; rg < 8; ++rg) x = fmaxf(x, s[rg][g]);
+        const float mt = max_rows8(x);
+        float sum = 0.f;
+#pragma unroll
+        for (int rg = 0; rg < 8; ++rg) sum += fexp2(s[rg][g] - mt);
+        const float lse0 = mt + flog2(sum_rows8(sum));
+        if (lane == 0) sLse0[g] = lse0;
+      }
+    }
+    __syncthreads();
+    float lse0[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      lse0[g] = sLse0[g];
+      m[g] = NEG_INF;
+      l[g] = 0.f;
+    }
+    if (nw > 0) load_k_block<D>(kr, rk, koff, p.k_st, (i0 + wave) * BLK);
+    for (int k = 0; k < nw; ++k) {
+      const int blk = i0 + wave + NWAVE * k;
+      const int t0 = blk * BLK;
+      const bool more = k + 1 < nw;
+      float s[8][G];
+      qk_block<D, G>(s, kr, qv, p.scale_log2, t0, p.T, lane);
+      float tm[G], tl[G], ta[G];
+      bool need = blk == 0 || blk >= nb - p.local;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float x = s[0][g];
+#pragma unroll
+        for (int rg = 1; rg < 8; ++rg) x = fmaxf(x, s[rg][g]);
+        const float mt = max_rows8(x);
+        const float mtu = mt == NEG_INF ? 0.f : mt;
+        float e[8], sum = 0.f;
+#pragma unroll
+        for (int rg = 0; rg < 8; ++rg) {
+          e[rg] = fexp2(s[rg][g] - mtu);
+          sum += e[rg];
+        }
+        const float st = sum_rows8(sum);
+        need = need || (mtu + flog2(st) - lse0[g] >= p.log2_tau);
+        const float m_new = fmaxf(m[g], mt);
+        const float mu = m_new == NEG_INF ? 0.f : m_new;
+        ta[g] = fexp2(m[g] - mu);
+        const float c = mt == NEG_INF ? 0.f : fexp2(mt - mu);
+        tl[g] = l[g] * ta[g] + st * c;
+        tm[g] = m_new;
+        if (sub == 0) {
+#pragma unroll
+          for (int rg = 0; rg < 8; ++rg) sPw[(8 * rg + r8) * GP + g] = e[rg] * c;
+        }
+      }
+      if (need) {
+        ++loaded;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          m[g] = tm[g];
+          l[g] = tl[g];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[g][u] *= ta[g];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_v_block<D>(vr, rv, voff, p.v_st, t0);
+        if (more) load_k_block<D>(kr, rk, koff, p.k_st, (blk + NWAVE) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        pv();
+      } else if (more) {
+        load_k_block<D>(kr, rk, koff, p.k_st, (blk + NWAVE) * BLK);
+      }
+    }
+  }
+  if (lane == 0) sLoaded[wave] = loaded;
+  finish<D, G, true>(p, m, l, acc, b, h, split, sL, false);
+  if (tid == 0 && p.vcount != nullptr) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) tot += sLoaded[w];
+    atomicAdd(p.vcount + b * p.Hkv + h, tot);
+  }
+}
+
+// Two-pass V-skip, pass 2: acc = sum over listed blocks of (blk_scale * P) . V; the weights
+// are normalised already, so no softmax and the splits simply add up.
+template <int D, int G>
+__global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
+  constexpr int GP = gpad<G>();
+  __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
+  __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
+
+  int split, h, b;
+  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int n_items = min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
+  const int* list = p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks;
+  const int per = (n_items + p.num_splits - 1) / p.num_splits;
+  const int i0 = min(n_items, split * per);
+  const int n = min(n_items, i0 + per) - i0;
+  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, head_bytes(p.T, p.v_st, D));
+  const uint32_t voff = static_cast<uint32_t>((lane / Lay<D>::VLPR) * p.v_st * 2 + 16 * (lane % Lay<D>::VLPR));
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = 0.f;
+    l[g] = 1.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+  u32x4 vr[Lay<D>::VN];
+  float* sPw = sP[wave];
+  const int pg = lane >> 3, ppart = lane & 7;  // P staging: head pg, tokens 8*ppart .. +8
+  for (int j = wave; j < n; j += NWAVE) {
+    const int blk = list[i0 + j];
+    if (blk < 0 || blk >= p.nb) continue;
+    const int t0 = blk * BLK;
+    load_v_block<D>(vr, rv, voff, p.v_st, t0);
+    if (pg < G) {
+      const float f = p.blk_scale[((static_cast<int64_t>(b) * p.Hkv + h) * p.nb + blk) * G + pg];
+      const u32x4 raw = ld16(p.p_in + (hq0 + pg) * p.t_pad + t0 + 8 * ppart);
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sPw[(8 * ppart + 2 * u) * GP + pg] = h2f(static_cast<uint16_t>(w[u] & 0xffffu)) * f;
+        sPw[(8 * ppart + 2 * u + 1) * GP + pg] = h2f(static_cast<uint16_t>(w[u] >> 16)) * f;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    pv_block<D, G>(acc, vr, sPw, lane);
+    __builtin_amdgcn_wave_barrier();
+  }
+  finish<D, G, true>(p, m, l, acc, b, h, split, sL, true);
+}
+
+// Streaming read: workgroup i reads the i-th contiguous chunk of n 16-byte words, each thread
+// keeping 8 loads in flight, XOR-folded so the loads stay live.
+__global__ void __launch_bounds__(256) read_kernel(const u32x4* __restrict__ x, int64_t n, uint32_t* out) {
+  constexpr int U = 8;
+  const int64_t chunk = ((n + gridDim.x - 1) / gridDim.x + 256 * U - 1) / (256 * U) * (256 * U);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t end = min(n, base + chunk);
+  uint32_t a = 0;
+  int64_t i = base + threadIdx.x;
+  for (; i + (U - 1) * 256 < end; i += U * 256) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = ld16_nt(x + i + u * 256);
+#pragma unroll
+    for (int u = 0; u < U; ++u) a ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < end; i += 256) {
+    const u32x4 v = ld16_nt(x + i);
+    a ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (a == 0x9e3779b9u) out[0] = a;
+}
+
+template <int D, int G>
+hipError_t launch_vskip1_t(const AttnP& p, bool mf, hipStream_t s) {
+  if (mf)
+    hipLaunchKernelGGL((vskip1_kernel<D, G, true>), attn_grid(p), dim3(NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((vskip1_kernel<D, G, false>), attn_grid(p), dim3(NT), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.num_splits > 1 && p.ticket == nullptr) {
+    hipLaunchKernelGGL((combine_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+template <int D, int G>
+hipError_t launch_pv_t(const AttnP& p, hipStream_t s) {
+  hipLaunchKernelGGL((pv_kernel<D, G>), attn_grid(p), dim3(NT), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.num_splits > 1 && p.ticket == nullptr) {
+    hipLaunchKernelGGL((combine_sum_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+}  // namespace
+
+bool attn_supported(int D, int G) {
+  return (D == 64 || D == 128) && (G == 1 || G == 2 || G == 4 || G == 7 || G == 8);
+}
+
+hipError_t launch_vskip1(const AttnP& p, int D, int G, hipStream_t s) {
+  const bool mf = qk_use_mfma();
+#define KVS_CASE(DD, GG) \
+  if (D == DD && G == GG) return launch_vskip1_t<DD, GG>(p, mf, s);
+  KVS_FOR_G(KVS_CASE, 64)
+  KVS_FOR_G(KVS_CASE, 128)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_pv(const AttnP& p, int D, int G, hipStream_t s) {
+#define KVS_CASE(DD, GG) \
+  if (D == DD && G == GG) return launch_pv_t<DD, GG>(p, s);
+  KVS_FOR_G(KVS_CASE, 64)
+  KVS_FOR_G(KVS_CASE, 128)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, hipStream_t s) {
+  hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const u32x4*>(x), bytes / 16,
+                     out);
+  return hipGetLastError();
+}
+
+}  // namespace kvs

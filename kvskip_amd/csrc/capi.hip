@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "internal.hpp"
@@ -57,6 +58,7 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   if (need_k && (rc = check_kv(a->k, a->k_sb, a->k_sh, a->k_st, "k")) != KVSKIP_OK) return rc;
   if (need_v && (rc = check_kv(a->v, a->v_sb, a->v_sh, a->v_st, "v")) != KVSKIP_OK) return rc;
   if (a->num_splits < 1) return fail(KVSKIP_E_INVALID, "num_splits >= 1");
+  if (a->num_splits > kvs::MAX_SPLITS) return fail(KVSKIP_E_INVALID, "num_splits <= %d", kvs::MAX_SPLITS);
   if (a->num_splits > 1 && a->part_ml == nullptr)
     return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
   std::memset(p, 0, sizeof(*p));
@@ -87,10 +89,18 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->local = a->local;
   p->vcount = a->vcount;
   p->lse_prev = a->lse_prev;
+  p->ticket = a->split_ticket;
   return KVSKIP_OK;
 }
 
 }  // namespace
+
+namespace kvs {
+bool qk_use_mfma() {
+  const char* e = std::getenv("KVSKIP_AMD_QK");
+  return !(e != nullptr && std::strcmp(e, "valu") == 0);
+}
+}  // namespace kvs
 
 extern "C" {
 

@@ -38,7 +38,13 @@ struct AttnP {
   int local;
   int* vcount;
   const float* lse_prev;
+  int* ticket;
 };
+
+constexpr int MAX_SPLITS = 256;
+
+// QK engine of the attention kernels: MFMA (default) unless KVSKIP_AMD_QK=valu.
+bool qk_use_mfma();
 
 // Head dims / group sizes with instantiated attention kernels.
 bool attn_supported(int D, int G);

@@ -49,7 +49,7 @@ def decode(q, k, v, scale, keep=None, dtype=torch.float64):
     if keep is not None:
         s = s.masked_fill(~heads(token_mask(keep, T), G), NEG_INF)
     lse = torch.logsumexp(s, -1)
-    p = torch.exp(s - lse[..., None].clamp_min(-1e300))
+    p = torch.exp(s - lse[..., None].clamp_min(torch.finfo(s.dtype).min))
     p = torch.where(torch.isfinite(lse)[..., None], p, torch.zeros_like(p))
     out = torch.einsum("bkgt,bktd->bkgd", p.reshape(B, Hkv, G, T), v.to(dtype)).reshape(B, Hq, D)
     return out, lse
@@ -67,7 +67,7 @@ def block_stats(q, k, scale, keep=None, dtype=torch.float64):
     s = scores(q, k, scale, dtype)
     s = torch.nn.functional.pad(s, (0, nb * BLOCK - T), value=NEG_INF).reshape(B, Hq, nb, BLOCK)
     M = s.amax(-1)
-    S = torch.exp(s - M[..., None].clamp_min(-1e300)).sum(-1)
+    S = torch.exp(s - M[..., None].clamp_min(torch.finfo(s.dtype).min)).sum(-1)
     S = torch.where(torch.isfinite(M), S, torch.zeros_like(S))
     if keep is not None:
         kh = heads(keep, G)

@@ -207,3 +207,43 @@ def test_read_bw(gpu):
     K.ext().read_bw(x, o, 1024)
     torch.cuda.synchronize()
     assert int(o.item()) == 0
+
+
+@pytest.mark.parametrize("engine", ["valu", "mfma"])
+def test_qk_engines(gpu, engine, monkeypatch):
+    """Both QK engines (v_dot2 VALU, MFMA) against the oracle: dense / masked + stats / stats-only /
+    vskip1, D 64 and 128, G 4 and 7, with and without split tickets (NULL -> separate merge)."""
+    monkeypatch.setenv("KVSKIP_AMD_QK", engine)
+    from kvskip_amd import ext as E
+    for D, G in ((128, 4), (64, 4), (128, 7)):
+        q, k, v = rand_qkv(1, 4 * G, 4, 1200, D, seed=100 + D + G, sink_gap=True)
+        gq, gk, gv = to_gpu(q, k, v)
+        scale = D ** -0.5
+        check_decode(q, k, v, scale, gq, gk, gv, num_splits=6, label=f"{engine} D{D} G{G}")
+        keep = W.random_block_list(1, 4, O.nblocks(1200), 0.5, seed=D + G)
+        r = check_decode(q, k, v, scale, gq, gk, gv, keep=keep, num_splits=4, label=f"{engine} D{D} G{G} masked")
+        rs = K.decode(gq, gk, gv, scale, plan=K.make_plan(keep.cuda()), stats=True, num_splits=4)
+        M, S = O.block_stats(q, k, scale, keep=keep)
+        x_dev = O.block_logw(rs["blk_max"].cpu().double(), rs["blk_sum"].cpu().double())
+        fin = torch.isfinite(O.block_logw(M, S))
+        assert torch.equal(torch.isfinite(x_dev), fin)
+        assert (x_dev - O.block_logw(M, S))[fin].abs().max().item() <= LSE_TOL
+        so = K.decode(gq, gk, gv, scale, stats=True, load_v=False, num_splits=3)
+        assert torch.equal(torch.isfinite(so["blk_max"]).cpu(), torch.ones_like(fin))
+        r1 = K.vskip_one_pass(gq, gk, gv, scale, tau=1e-3, out_f32=True, count=True, num_splits=5)
+        keep1, z = O.vskip1_keep(q, k, scale, 1e-3, 2)
+        ref1, _ = O.decode(q, k, v, scale, keep=keep1)
+        assert O.rel_err(r1["out_f32"].cpu(), ref1) <= F32_TOL
+    # the ticket-less path (separate merge kernel) through the raw operator
+    q, k, v = rand_qkv(1, 32, 8, 2000, 128, seed=77)
+    gq, gk, gv = to_gpu(q, k, v)
+    import kvskip_amd.ext as ext_mod
+    saved = ext_mod._tickets
+    try:
+        ext_mod._tickets = lambda dev, n: type("Null", (), {"data_ptr": lambda self: None})()
+        out, lse = E.decode(gq, gk, gv, 128 ** -0.5, num_splits=9, want_f32=True)[:2]
+    finally:
+        ext_mod._tickets = saved
+    ref, lref = O.decode(q, k, v, 128 ** -0.5)
+    assert O.rel_err(out.cpu(), ref) <= BF16_TOL
+    assert (lse.cpu().double() - lref).abs().max().item() <= LSE_TOL
