@@ -76,12 +76,6 @@ typedef struct kvskip_attn_args {
   int32_t local;               /* newest blocks always kept (block 0 always kept too) */
   int32_t* vcount;             /* optional [B, Hkv] V blocks loaded (atomically added) */
   const float* lse_prev;       /* optional [B, Hq] natural-log normaliser estimate; NULL: block-0 bound */
-
-  /* optional [B, Hkv] int32 split tickets, all zero before a launch and left zero after it:
-   * with num_splits > 1 the last workgroup of each KV head to finish merges the splits inside
-   * the same kernel (no second launch). NULL: a separate merge kernel runs. Launches that share
-   * one ticket array must not overlap in time (same stream, or synchronised). */
-  int32_t* split_ticket;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block

@@ -2,18 +2,19 @@
 // block-list, per-block statistics, stats-only, fp16 P; attn_vskip.hip: single-pass V-skip,
 // two-pass V-skip pass 2, read ceiling).
 //
-// Work decomposition. num_splits * Hkv * B workgroups of 4 wavefronts; a workgroup owns one
+// Work decomposition. num_splits * Hkv * B workgroups of NWAVE wavefronts; a workgroup owns one
 // contiguous range of "items" (64-token blocks, or entries of a block list) of one KV head
 // and serves all G query heads of that head, so each K/V byte is read once. Workgroups are
 // dispatched round-robin over the 8 XCDs; the launch index is remapped so that consecutive
-// work items (the splits of one KV head) land on the same XCD and share its L2.
-// Inside the workgroup the 4 wavefronts are independent streams: wavefront w takes items w,
-// w+4, ... and keeps its own online-softmax state for the G heads, so the main loop has no
+// work items (the splits of one KV head) land on the same XCD.
+// Inside the workgroup the wavefronts are independent streams: wavefront w takes items w,
+// w+NWAVE, ... and keeps its own online-softmax state for the G heads, so the main loop has no
 // workgroup barrier. A wavefront processes a whole 64-token block at a time, so the
 // per-block statistics fall out of its own registers. The 4 states are merged once, in LDS,
-// at the end. With num_splits > 1 each workgroup writes its partial state; the last
-// workgroup of a KV head to arrive (a self-resetting ticket counter) merges all partials in
-// the same kernel.
+// at the end. With num_splits > 1 each workgroup writes its partial state and a second,
+// short kernel merges the splits (8 split classes x 32 dims per workgroup). A merge inside the
+// same kernel (last-arriving workgroup) needs device-scope fences, which on gfx950 write back
+// and invalidate the whole XCD L2 per workgroup: measured 2x slower at 2 workgroups per CU.
 //
 // Pipeline per wavefront: K(j) and V(j) are in flight when block j starts; after QK(j) the K
 // loads of block j+1 are issued, after PV(j) its V loads. The last block is peeled off the
@@ -45,7 +46,10 @@
 namespace kvs {
 namespace {
 
-constexpr int NWAVE = 4;
+#ifndef KVS_NWAVE
+#define KVS_NWAVE 4
+#endif
+constexpr int NWAVE = KVS_NWAVE;  // wavefronts per attention workgroup
 constexpr int NT = NWAVE * WAVE;
 
 template <int D>
@@ -188,87 +192,10 @@ template <int D, int G>
 struct MergeLds {
   float acc[NWAVE * G * D];            // per-wavefront accumulators
   float ml[NWAVE * G * 2];             // per-wavefront (m, l)
-  float w[G * MAX_SPLITS];             // split weights 2^(m_s - M) (last workgroup)
-  float red[NT * 4];                   // partial sums of the split merge
-  float gml[G * 2];                    // merged (M, L) per head
-  int last;
 };
 
-// Last workgroup of a KV head: merge the num_splits partials of its G heads and write the
-// outputs. plain: the partials simply add up (two-pass pass 2).
-template <int D, int G, bool LOAD_V>
-__device__ __forceinline__ void merge_splits(const AttnP& p, int64_t hq0, MergeLds<D, G>& L, bool plain) {
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
-  const int S = p.num_splits;
-  for (int g = wave; g < G; g += NWAVE) {
-    const float* ml = p.part_ml + (hq0 + g) * S * 2;
-    float mx = NEG_INF;
-    if (!plain)
-      for (int s = lane; s < S; s += WAVE) mx = fmaxf(mx, ml[2 * s]);
-    mx = wave_max(mx);
-    const float mu = mx == NEG_INF ? 0.f : mx;
-    float ls = 0.f;
-    for (int s = lane; s < S; s += WAVE) {
-      const float w = plain ? 1.f : fexp2(ml[2 * s] - mu);
-      L.w[g * MAX_SPLITS + s] = w;
-      if (!plain) ls += ml[2 * s + 1] * w;
-    }
-    ls = wave_sum(ls);
-    if (lane == 0) {
-      L.gml[2 * g] = mx;
-      L.gml[2 * g + 1] = plain ? 1.f : ls;
-    }
-  }
-  __syncthreads();
-  if constexpr (LOAD_V) {
-    constexpr int NQ = G * D / 4;            // output quads
-    constexpr int TPQ = NT / NQ;             // threads per quad (>= 1)
-    if (tid < NQ * TPQ) {
-      const int qd = tid % NQ, part = tid / NQ;
-      const int g = qd / (D / 4), d4 = qd % (D / 4);
-      const float* pa = p.part_acc + (hq0 + g) * S * D + 4 * d4;
-      const float* w = L.w + g * MAX_SPLITS;
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-      for (int s = part; s < S; s += TPQ) {
-        const float4 v = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(s) * D);
-        const float f = w[s];
-        a.x = fmaf(v.x, f, a.x);
-        a.y = fmaf(v.y, f, a.y);
-        a.z = fmaf(v.z, f, a.z);
-        a.w = fmaf(v.w, f, a.w);
-      }
-      *reinterpret_cast<float4*>(L.red + 4 * (part * NQ + qd)) = a;
-    }
-    __syncthreads();
-    if (tid < NQ) {
-      const int qd = tid, g = qd / (D / 4), d4 = qd % (D / 4);
-      float4 a = *reinterpret_cast<const float4*>(L.red + 4 * qd);
-      for (int t = 1; t < TPQ; ++t) {
-        const float4 b4 = *reinterpret_cast<const float4*>(L.red + 4 * (t * NQ + qd));
-        a.x += b4.x;
-        a.y += b4.y;
-        a.z += b4.z;
-        a.w += b4.w;
-      }
-      const float l = L.gml[2 * g + 1];
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      const float o[4] = {a.x * inv, a.y * inv, a.z * inv, a.w * inv};
-      const int64_t base = (hq0 + g) * D + 4 * d4;
-      const uint32_t lo = static_cast<uint32_t>(f2bf(o[0])) | (static_cast<uint32_t>(f2bf(o[1])) << 16);
-      const uint32_t hi = static_cast<uint32_t>(f2bf(o[2])) | (static_cast<uint32_t>(f2bf(o[3])) << 16);
-      *reinterpret_cast<uint2*>(p.out + base) = make_uint2(lo, hi);
-      if (p.out_f32) *reinterpret_cast<float4*>(p.out_f32 + base) = make_float4(o[0], o[1], o[2], o[3]);
-    }
-  }
-  if (!plain && tid < G && p.lse) {
-    const float M = L.gml[2 * tid], l = L.gml[2 * tid + 1];
-    p.lse[hq0 + tid] = l > 0.f ? (M + flog2(l)) * LN2 : NEG_INF;
-  }
-}
-
-// Workgroup epilogue: merge the 4 wavefront states (m, l in log2 units, acc un-normalised),
-// then write out/out_f32/lse (one split) or the split partials (+ the in-kernel split merge).
+// Workgroup epilogue: merge the wavefront states (m, l in log2 units, acc un-normalised), then
+// write out/out_f32/lse (one split) or the split partials.
 template <int D, int G, bool LOAD_V>
 __device__ __forceinline__ void finish(const AttnP& p, float (&m)[G], float (&l)[G], float (&acc)[G][8], int b,
                                        int h, int split, MergeLds<D, G>& L, bool plain) {
@@ -339,17 +266,6 @@ __device__ __forceinline__ void finish(const AttnP& p, float (&m)[G], float (&l)
       p.part_ml[(hq * S + split) * 2 + 1] = Ls;
     }
   }
-  if (S == 1 || p.ticket == nullptr) return;
-  // Publish this partial, take a ticket; the last arrival merges.
-  __threadfence();
-  __syncthreads();
-  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
-  if (tid == 0) L.last = atomicAdd(p.ticket + bh, 1) == S - 1;
-  __syncthreads();
-  if (!L.last) return;
-  __threadfence();
-  merge_splits<D, G, LOAD_V>(p, hq0, L, plain);
-  if (tid == 0) p.ticket[bh] = 0;
 }
 
 template <int D, int G>
@@ -460,42 +376,77 @@ __device__ __forceinline__ void qk_block_mf(float (&s)[4][4], const u32x4 (&kr)[
   }
 }
 
-// Log-sum-exp merge of the split partials when no ticket array is given; one workgroup per
-// (b, query head), one thread per dim. With out == nullptr (stats-only) only lse is produced.
+// Split merge: workgroup (b*Hq + hq, 32-dim slice), 256 threads = 8 split classes x 32 dims.
+// Thread (cls, d) loads the partials of splits s = cls (mod 8) in one round trip, the classes
+// agree on the max through LDS, then weight (2^(m_s - M), log-sum-exp mode; 1, plain mode for
+// the two-pass pass 2) and add in LDS. With out == nullptr (stats-only) only lse is produced.
 template <int D>
-__global__ void __launch_bounds__(D) combine_kernel(const AttnP p) {
+__global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
+  constexpr int NC = 8, U = MAX_SPLITS / NC;
   const int64_t hq = blockIdx.x;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x, cls = tid / 32, dl = tid % 32;
+  const int d = blockIdx.y * 32 + dl;
   const int S = p.num_splits;
   const float* ml = p.part_ml + hq * S * 2;
-  float M = NEG_INF;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
-  const float mu = M == NEG_INF ? 0.f : M;
-  float L = 0.f, A = 0.f;
   const bool with_v = p.out != nullptr;
-  for (int s = 0; s < S; ++s) {
-    const float w = fexp2(ml[2 * s] - mu);
-    L += ml[2 * s + 1] * w;
-    if (with_v) A += p.part_acc[(hq * S + s) * D + d] * w;
+  __shared__ float rA[NC][32], rL[NC], rM[NC];
+  float ms[U], ls[U], as[U];
+  float mloc = NEG_INF;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int s = cls + NC * u;
+    if (s < S) {
+      const float2 t = *reinterpret_cast<const float2*>(ml + 2 * s);
+      ms[u] = t.x;
+      ls[u] = t.y;
+      as[u] = with_v ? p.part_acc[(hq * S + s) * D + d] : 0.f;
+      mloc = fmaxf(mloc, t.x);
+    }
   }
-  if (with_v) {
-    const float o = L > 0.f ? A / L : 0.f;
-    p.out[hq * D + d] = f2bf(o);
-    if (p.out_f32) p.out_f32[hq * D + d] = o;
+  if (dl == 0) rM[cls] = mloc;
+  __syncthreads();
+  float M = NEG_INF;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) M = fmaxf(M, rM[c]);
+  const float mu = M == NEG_INF ? 0.f : M;
+  float A = 0.f, L = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int s = cls + NC * u;
+    if (s < S) {
+      const float w = plain ? 1.f : fexp2(ms[u] - mu);
+      L += ls[u] * w;
+      A += as[u] * w;
+    }
   }
-  if (d == 0 && p.lse) p.lse[hq] = L > 0.f ? (M + flog2(L)) * LN2 : NEG_INF;
+  rA[cls][dl] = A;
+  if (dl == 0) rL[cls] = L;
+  __syncthreads();
+  if (tid < 32) {
+    float a = 0.f, l = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      a += rA[c][tid];
+      l += rL[c];
+    }
+    if (plain) l = 1.f;
+    if (with_v) {
+      const float o = l > 0.f ? a / l : 0.f;
+      p.out[hq * D + d] = f2bf(o);
+      if (p.out_f32) p.out_f32[hq * D + d] = o;
+    }
+    if (!plain && tid == 0 && blockIdx.y == 0 && p.lse) p.lse[hq] = l > 0.f ? (M + flog2(l)) * LN2 : NEG_INF;
+  }
 }
 
-template <int D>
-__global__ void __launch_bounds__(D) combine_sum_kernel(const AttnP p) {
-  const int64_t hq = blockIdx.x;
-  const int d = threadIdx.x;
-  float A = 0.f;
-  for (int s = 0; s < p.num_splits; ++s) A += p.part_acc[(hq * p.num_splits + s) * D + d];
-  p.out[hq * D + d] = f2bf(A);
-  if (p.out_f32) p.out_f32[hq * D + d] = A;
+inline hipError_t launch_combine(const AttnP& p, int D, bool plain, hipStream_t s) {
+  const dim3 grid(p.B * p.Hq, p.out != nullptr ? D / 32 : 1);
+  if (D == 128)
+    hipLaunchKernelGGL((combine_kernel<128>), grid, dim3(256), 0, s, p, plain ? 1 : 0);
+  else
+    hipLaunchKernelGGL((combine_kernel<64>), grid, dim3(256), 0, s, p, plain ? 1 : 0);
+  return hipGetLastError();
 }
-
 
 inline dim3 attn_grid(const AttnP& p) { return dim3(p.num_splits * p.Hkv * p.B); }
 

@@ -222,10 +222,7 @@ hipError_t launch_decode_t(const AttnP& p, bool mf, hipStream_t s) {
     hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false>), attn_grid(p), dim3(NT), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (p.num_splits > 1 && p.ticket == nullptr) {
-    hipLaunchKernelGGL((combine_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
-    e = hipGetLastError();
-  }
+  if (p.num_splits > 1) e = launch_combine(p, D, false, s);
   return e;
 }
 

@@ -327,10 +327,7 @@ hipError_t launch_vskip1_t(const AttnP& p, bool mf, hipStream_t s) {
     hipLaunchKernelGGL((vskip1_kernel<D, G, false>), attn_grid(p), dim3(NT), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (p.num_splits > 1 && p.ticket == nullptr) {
-    hipLaunchKernelGGL((combine_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
-    e = hipGetLastError();
-  }
+  if (p.num_splits > 1) e = launch_combine(p, D, false, s);
   return e;
 }
 
@@ -339,10 +336,7 @@ hipError_t launch_pv_t(const AttnP& p, hipStream_t s) {
   hipLaunchKernelGGL((pv_kernel<D, G>), attn_grid(p), dim3(NT), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (p.num_splits > 1 && p.ticket == nullptr) {
-    hipLaunchKernelGGL((combine_sum_kernel<D>), dim3(p.B * p.Hq), dim3(D), 0, s, p);
-    e = hipGetLastError();
-  }
+  if (p.num_splits > 1) e = launch_combine(p, D, true, s);
   return e;
 }
 

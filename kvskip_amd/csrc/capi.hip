@@ -89,7 +89,6 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->local = a->local;
   p->vcount = a->vcount;
   p->lse_prev = a->lse_prev;
-  p->ticket = a->split_ticket;
   return KVSKIP_OK;
 }
 

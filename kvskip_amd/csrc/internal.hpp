@@ -38,7 +38,6 @@ struct AttnP {
   int local;
   int* vcount;
   const float* lse_prev;
-  int* ticket;
 };
 
 constexpr int MAX_SPLITS = 256;

@@ -39,20 +39,6 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
-_TICKETS: dict = {}
-
-
-def _tickets(dev: torch.device, n: int) -> torch.Tensor:
-    """Zeroed int32 split-ticket array of >= n entries for the current stream of `dev` (the kernels
-    leave it zero again, so it is allocated once per stream and reused)."""
-    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
-    t = _TICKETS.get(key)
-    if t is None or t.numel() < n:
-        t = torch.zeros(max(n, 64), dtype=torch.int32, device=dev)
-        _TICKETS[key] = t
-    return t
-
-
 def check_kv(t: torch.Tensor, name: str):
     """kernels/kvskip_ext.cpp:12-19."""
     _require(t.is_cuda and t.dtype == torch.bfloat16, f"{name} must be a CUDA bf16 tensor")
@@ -139,8 +125,6 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     a.out, a.out_f32, a.lse = _ptr(out), _ptr(out32), lse.data_ptr()
     a.blk_max, a.blk_sum = _ptr(bmax), _ptr(bsum)
     a.p_out = _ptr(pbuf)
-    if num_splits > 1:
-        a.split_ticket = _tickets(dev, B * Hkv).data_ptr()
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode(ctypes.byref(a), int(bool(stats)), int(bool(load_v)), _stream(dev)))
     return [out, lse, bmax, bsum, out32, pbuf]
@@ -176,8 +160,6 @@ def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
     a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
     a.out, a.out_f32 = out.data_ptr(), _ptr(out32)
     a.p_in, a.blk_scale = P.data_ptr(), blk_scale.data_ptr()
-    if num_splits > 1:
-        a.split_ticket = _tickets(dev, B * Hkv).data_ptr()
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_pv(ctypes.byref(a), _stream(dev)))
     return [out, out32]
@@ -213,8 +195,6 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
         _require(lse_prev.is_cuda and lse_prev.dtype == torch.float32 and lse_prev.is_contiguous()
                  and lse_prev.numel() == B * Hq, "lse_prev: contiguous fp32 [B, Hq]")
         a.lse_prev = lse_prev.data_ptr()
-    if num_splits > 1:
-        a.split_ticket = _tickets(dev, B * Hkv).data_ptr()
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_vskip1(ctypes.byref(a), _stream(dev)))
     return [out, lse, out32, vcount]

@@ -21,7 +21,7 @@ import torch
 from . import ext as _ext_mod
 
 TILE = 64
-WG_PER_CU = 2          # attention workgroups (4 wavefronts each) resident per CU
+WG_PER_CU = 1          # attention workgroups (4 wavefronts each) per CU in the split heuristic
 
 
 def ext():

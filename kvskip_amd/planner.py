@@ -1,0 +1,204 @@
+"""Device-side refresh planner loop of one attention layer: the reference's "refresh_fused" mode
+(src/kvskip_attn.py:399-478) on the kvskip_amd kernels, with the first step initialised on the
+device too (the reference runs its Python planner for it, src/kvskip_attn.py:445-450).
+
+Per decode step: plan (estimate, refresh decision, block list) -> masked + block-statistics
+attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
+Three kernel launches (+ two fills of the statistics outputs) per layer-step, all on the current
+stream, no host synchronisation.
+
+The policy fields follow KvskipConfig (src/kvskip_attn.py:116-147) for one layer.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import ext as E
+from . import kvskip as K
+
+TILE = 64
+MARGIN = 64                      # spare block capacity of the state (src/kvskip_attn.py:399)
+KINDS = {"logit": 0, "add": 1, "peak": 2}
+
+
+@dataclass
+class Policy:
+    delta: float = 0.05
+    max_age: int = 32
+    level: float = 0.99
+    local: int = 2
+    calib: float | None = None          # rate of the online correction of the estimate (None: off)
+    calib_kind: str = "logit"           # "logit" | "add" | "peak"
+    calib_hold: int = 0                 # decode steps before the correction is applied
+    calib_warm: tuple = ()              # (W, A): max age A during the first W decode steps
+    calib_free: bool = False            # allow negative corrections
+    calib_auto_ix: float | None = None  # heads whose correction exceeds this join the token index
+    dense_heads: tuple = ()             # KV heads refreshed (= exact) on every step
+    index_heads: tuple = ()             # KV heads on the token index
+    index_union: bool = False           # index blocks join the attended set instead of replacing it
+
+    def flags(self, Hkv: int) -> list[int]:
+        """src/kvskip_attn.py:413-419."""
+        f = [0] * Hkv
+        for h in self.dense_heads:
+            f[h] = 1
+        for h in self.index_heads:
+            f[h] = 4 if self.index_union else 2
+        return f
+
+    def max_age_at(self, t: int) -> int:
+        """src/kvskip_attn.py:295-299."""
+        if self.calib_warm and t < self.calib_warm[0]:
+            return min(self.max_age, self.calib_warm[1])
+        return self.max_age
+
+    @property
+    def needs_index(self) -> bool:
+        return bool(self.index_heads) or self.calib_auto_ix is not None
+
+
+class FusedPlanner:
+    """Planner state of one layer in device memory (the fields of src/kvskip_attn.py:420-432) and
+    its step. Usage: out = p.first(q, k, v, scale) on the first decode step, then
+    out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
+
+    def __init__(self, policy: Policy):
+        self.policy = policy
+        self.state = None
+        self.t = 0
+        self.T = 0
+        self.counters = {}
+
+    # -- state
+    def _alloc(self, q, k, NBC):
+        B, Hq, D = q.shape
+        Hkv = k.shape[1]
+        dev = q.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.NBC = NBC
+        self.state = dict(
+            csum=torch.zeros(B, Hkv, NBC, D, **f32),
+            lse_ref=torch.full((B, Hq, NBC), -math.inf, **f32),
+            cs_ref=torch.zeros(B, Hq, NBC, **f32),
+            keep=torch.zeros(B, Hkv, NBC, dtype=torch.uint8, device=dev),
+            lse_att=torch.zeros(B, Hq, **f32),
+            age=torch.zeros(B, Hkv, dtype=torch.int32, device=dev),
+            flags=torch.tensor(self.policy.flags(Hkv), dtype=torch.int32, device=dev),
+            cs_now=torch.zeros(B, Hq, NBC, **f32),
+            trig=torch.zeros(B, Hkv, dtype=torch.uint8, device=dev),
+            block_idx=torch.zeros(B, Hkv, NBC, dtype=torch.int32, device=dev),
+            block_cnt=torch.zeros(B, Hkv, dtype=torch.int32, device=dev),
+            calib=torch.zeros(B, Hkv, **f32),
+            est=torch.zeros(B, Hkv, **f32),
+            aix=torch.zeros(B, Hkv, dtype=torch.uint8, device=dev),
+            idx=torch.zeros(B, NBC, dtype=torch.uint8, device=dev),
+        )
+
+    def _grow(self, NBC):
+        """src/kvskip_attn.py:435-442."""
+        fills = dict(keep=0, lse_ref=-math.inf, cs_ref=0.0, csum=0.0, cs_now=0.0, block_idx=0)
+        for key, fill in fills.items():
+            x = self.state[key]
+            out = torch.full((*x.shape[:2], NBC, *x.shape[3:]), fill, dtype=x.dtype, device=x.device)
+            out[:, :, :x.shape[2]] = x
+            self.state[key] = out
+        idx = torch.zeros(self.state["idx"].shape[0], NBC, dtype=torch.uint8, device=self.state["idx"].device)
+        self.state["idx"] = idx
+        self.NBC = NBC
+
+    def _count(self, key, value):
+        self.counters[key] = self.counters.get(key, 0) + value
+
+    def _set_idx(self, idx, ids, T):
+        """This step's token-index blocks into state['idx'] ([B, NBC] uint8): from idx (bool / uint8
+        [B, >= nb]) or from token ids [B, >= T] int32 with the device token-index kernel."""
+        s = self.state
+        nb = math.ceil(T / TILE)
+        if ids is not None:
+            E.token_index(ids, T, self.NBC, out=s["idx"])
+        elif idx is not None:
+            s["idx"].zero_()
+            s["idx"][:, :nb] = idx[:, :nb].to(torch.uint8)
+        else:
+            raise RuntimeError("this policy needs the token index: pass idx or ids")
+        return s["idx"]
+
+    # -- steps
+    def first(self, q, k, v, scale):
+        """First decode step: dense + block statistics and the state initialisation
+        (src/kvskip_attn.py:339-354), on the device: per-block key sums of the prefix, a plan that
+        refreshes every head, the attention pass, and an update without calibration."""
+        if q.dim() == 4:
+            q = q.squeeze(2)
+        B, Hq, D = q.shape
+        Hkv, T = k.shape[1], k.shape[2]
+        nb = math.ceil(T / TILE)
+        self._alloc(q, k, nb + MARGIN)
+        s = self.state
+        E.block_sums(k, self.NBC, out=s["csum"])
+        every = torch.ones(Hkv, dtype=torch.int32, device=q.device)      # refresh all, no index heads
+        pol = self.policy
+        E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
+               s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
+               int(pol.local), False)
+        r = K.decode(q, k, v, scale, plan=K.Plan(s["block_idx"], s["block_cnt"], nb, nb), stats=True)
+        E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
+                 s["lse_att"], T, float(pol.level), int(pol.local))
+        self.t, self.T = 0, T
+        self._count("dense_heads", B * Hkv)
+        self._count("blocks_read", B * Hkv * nb)
+        self._count("blocks_total", B * Hkv * nb)
+        return r["out"]
+
+    def step(self, q, k, v, scale, idx=None, ids=None):
+        """One later decode step (src/kvskip_attn.py:451-478): plan -> masked + stats attention ->
+        update. idx: this step's token-index blocks (bool [B, >= nb]) or ids: token ids [B, >= T] int32
+        (index heads / auto index only)."""
+        if self.state is None:
+            return self.first(q, k, v, scale)
+        if q.dim() == 4:
+            q = q.squeeze(2)
+        B, Hq, D = q.shape
+        Hkv, T = k.shape[1], k.shape[2]
+        nb = math.ceil(T / TILE)
+        if nb > self.NBC:
+            self._grow(nb + MARGIN)
+        s = self.state
+        pol = self.policy
+        add_token = T == self.T + 1
+        if not add_token and T != self.T:
+            E.block_sums(k, self.NBC, out=s["csum"])                  # several tokens appended: resum
+        self.t += 1
+        self.T = T
+        ix = self._set_idx(idx, ids, T) if pol.needs_index else None
+        cal = pol.calib is not None
+        kind = KINDS[pol.calib_kind]
+        E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"], s["cs_now"],
+               s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
+               int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
+               cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None)
+        r = K.decode(q, k, v, scale, plan=K.Plan(s["block_idx"], s["block_cnt"], nb, nb), stats=True)
+        E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
+                 s["lse_att"], T, float(pol.level), int(pol.local), s["flags"], ix, s["est"],
+                 s["calib"] if cal else None, float(pol.calib or 0.0), bool(pol.calib_free), kind,
+                 s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0))
+        self._count("blocks_read", s["block_cnt"].sum())
+        self._count("blocks_total", B * Hkv * nb)
+        self._count("masked_heads", B * Hkv)
+        self._count("dense_heads", s["trig"].sum())
+        return r["out"]
+
+    def read_mask(self, nb):
+        """Blocks read this step per (b, KV head): bool [B, Hkv, nb] (host-side view for checks)."""
+        s = self.state
+        bi, bc = s["block_idx"], s["block_cnt"]
+        B, H, n = bi.shape
+        ar = torch.arange(n, device=bi.device)
+        valid = ar[None, None, :] < bc[..., None]
+        m = torch.zeros(B, H, n + 1, dtype=torch.bool, device=bi.device)
+        m.scatter_(-1, torch.where(valid, bi.long(), n), True)
+        return m[..., :nb]

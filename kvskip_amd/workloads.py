@@ -145,3 +145,102 @@ def perturbed_lse(lse_exact: torch.Tensor, seed: int, rel: float = 0.05) -> torc
     g = _gen("cpu", seed)
     u = (torch.rand(lse_exact.shape, generator=g, dtype=torch.float64) * 2 - 1) * rel
     return (lse_exact.double().cpu() + torch.log1p(u)).float().to(lse_exact.device)
+
+
+@dataclass
+class PlannerRun:
+    """Synthetic decode run for the planner loop (BASELINE configs 4 and 5): per layer a KV cache
+    with capacity T0 + steps (the first T0 tokens filled), planted hot-block sets, and a query
+    process; token ids with planted repeats for the token index."""
+    k: list                 # per layer [B, Hkv, T0 + steps, D] bf16 (capacity)
+    v: list
+    dirs: list              # per layer [B, Hkv, n_sets, D] unit directions of the planted sets
+    q0: list                # per layer [B, Hq, D] float32 initial queries
+    aim: list               # per layer [B, Hq] int64 planted set each query head points at
+    ids: torch.Tensor       # [B, T0 + steps] int32
+    T0: list                # per batch element prefix length (ragged batches)
+    steps: int
+    scale: float
+    seed: int
+    alpha: float
+
+
+def planner_run(layers=32, B=1, Hq=32, Hkv=8, D=128, T0=32768, steps=128, seed=4, n_sets=6, hot=3,
+                hot_shift=6.0, vocab=128256, ragged=None, device="cpu") -> PlannerRun:
+    """Keys / values N(0, 1); per (layer, b, KV head) n_sets planted sets of `hot` blocks whose keys
+    get += hot_shift * u_j (u_j a seeded unit direction), plus a sink on block 0 holding ~0.5 of
+    the group's mass at the start. hot_shift 6 (a +12-nat boost for an aimed query) makes a
+    minority of blocks hold 99% of the mass, as in real decode attention; at 2 the attention is
+    so flat that top-p 0.99 keeps every block and the planner has nothing to skip. Query head h starts aimed at a random set: q = alpha u_j + N(0,1)
+    with alpha = 2 sqrt(D). ragged: optional list of per-batch prefix lengths (<= T0); the cache of
+    element b then holds T0[b] valid tokens."""
+    g = _gen(device, seed)
+    G = Hq // Hkv
+    T0s = list(ragged) if ragged is not None else [T0] * B
+    Tcap = max(T0s) + steps
+    alpha = 2.0 * math.sqrt(D)
+    ks, vs, dirs, q0s, aims = [], [], [], [], []
+    for layer in range(layers):
+        k = _randn((B, Hkv, Tcap, D), g, device)
+        v = _randn((B, Hkv, Tcap, D), g, device)
+        u = _randn((B, Hkv, n_sets, D), g, device)
+        u = u / u.norm(dim=-1, keepdim=True)
+        aim = torch.randint(0, n_sets, (B, Hq), generator=g, device=device)
+        q = _randn((B, Hq, D), g, device) + alpha * torch.gather(
+            u.repeat_interleave(G, dim=1), 2, aim[..., None, None].expand(B, Hq, 1, D))[:, :, 0]
+        for b in range(B):
+            nb = (T0s[b] + BLOCK - 1) // BLOCK
+            for h in range(Hkv):
+                if nb > hot * n_sets + 3:
+                    blocks = torch.randperm(nb - 3, generator=g, device=device)[:hot * n_sets] + 1
+                    for j in range(n_sets):
+                        for blk in blocks[j * hot:(j + 1) * hot].tolist():
+                            k[b, h, blk * BLOCK:min(T0s[b], (blk + 1) * BLOCK)] += hot_shift * u[b, h, j]
+                qg = q[b, h * G:(h + 1) * G].double()
+                qhat = qg.mean(0)
+                qhat = (qhat / qhat.norm()).float()
+                s = (qg @ k[b, h, :T0s[b]].double().T) / math.sqrt(D)
+                c = (qg @ qhat.double()) / math.sqrt(D)
+                t1 = min(T0s[b], BLOCK)
+                rest = torch.logsumexp(s[:, t1:], -1) if T0s[b] > t1 else torch.full((G,), -math.inf, dtype=torch.float64)
+                beta = _solve_bias(rest.cpu(), s[:, :t1].cpu(), c.cpu(), 0.5)
+                k[b, h, :t1] += beta * qhat
+        ks.append(k.to(torch.bfloat16))
+        vs.append(v.to(torch.bfloat16))
+        dirs.append(u)
+        q0s.append(q)
+        aims.append(aim)
+    ids = torch.randint(0, vocab, (B, Tcap), generator=g, device=device, dtype=torch.int64)
+    # planted repeats: a third of the decode-step tokens copy an earlier token
+    for b in range(B):
+        for t in range(T0s[b], T0s[b] + steps):
+            if torch.rand((), generator=g, device=device).item() < 1 / 3:
+                src = int(torch.randint(0, t, (), generator=g, device=device).item())
+                ids[b, t] = ids[b, src]
+    return PlannerRun(ks, vs, dirs, q0s, aims, ids.to(torch.int32), T0s, steps, 1.0 / math.sqrt(D), seed, alpha)
+
+
+class QueryProcess:
+    """q_t = 0.97 q_{t-1} + 0.25 N(0, 1); with probability p_jump per query head and step the head
+    re-aims at another planted set: q = alpha u_new + 0.25 N(0, 1). Seeded, on the CPU."""
+
+    def __init__(self, run: PlannerRun, layer: int, p_jump=0.03, seed=None):
+        self.run, self.layer, self.p = run, layer, p_jump
+        self.g = torch.Generator().manual_seed(run.seed * 1000 + layer if seed is None else seed)
+        self.q = run.q0[layer].detach().float().cpu().clone()
+        self.aim = run.aim[layer].cpu().clone()
+        self.u = run.dirs[layer].float().cpu()
+
+    def next(self) -> torch.Tensor:
+        B, Hq, D = self.q.shape
+        Hkv, n_sets = self.u.shape[1], self.u.shape[2]
+        G = Hq // Hkv
+        eps = torch.randn(B, Hq, D, generator=self.g)
+        self.q = 0.97 * self.q + 0.25 * eps
+        jump = torch.rand(B, Hq, generator=self.g) < self.p
+        if bool(jump.any()):
+            new = (self.aim + 1 + torch.randint(0, n_sets - 1, (B, Hq), generator=self.g)) % n_sets
+            self.aim = torch.where(jump, new, self.aim)
+            uu = torch.gather(self.u.repeat_interleave(G, dim=1), 2, self.aim[..., None, None].expand(B, Hq, 1, D))[:, :, 0]
+            self.q = torch.where(jump[..., None], self.run.alpha * uu + 0.25 * eps, self.q)
+        return self.q.to(torch.bfloat16)

@@ -1,0 +1,196 @@
+"""GPU parity of the device-side refresh planner (plan / update kernels, the fused loop, the
+device initialisation, block key sums, token index) against the fp64 CPU oracle of the
+reference's Python planner (refresh_pre_step, src/kvskip_attn.py:328-396).
+
+Decisions (refresh triggers, block lists, stored sets, token-index hits, index latches) must be
+identical on every head-step; a difference is tolerated only where the oracle's deciding
+quantity lies within 1e-5 of its threshold (float32 summation order), and every such case is
+counted and printed. Continuous state (estimates, centroid scores, references, attended
+log-sum-exp, calibration) within 1e-4 absolute; outputs within 2e-3 relative (bf16).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kvskip_amd import ext as E
+from kvskip_amd import kvskip as K
+from kvskip_amd import workloads as W
+from kvskip_amd.planner import FusedPlanner, Policy as DPolicy
+from oracle import attention as O
+from oracle import planner as OP
+
+pytestmark = pytest.mark.gpu
+
+BORDER = 1e-5
+
+
+def dpolicy(p: OP.Policy) -> DPolicy:
+    return DPolicy(**p.__dict__)
+
+
+def test_block_sums_and_token_index(gpu):
+    g = torch.Generator().manual_seed(11)
+    k = torch.randn(2, 3, 1000, 128, generator=g).to(torch.bfloat16)
+    cs = E.block_sums(k.cuda(), 20).cpu()
+    ref = OP.centroid_sums(k)
+    assert (cs[:, :, :16].double() - ref).abs().max().item() <= 1e-4 * ref.abs().max().item()
+    assert (cs[:, :, 16:] == 0).all()
+    ids = torch.randint(0, 50, (3, 3000), generator=g, dtype=torch.int32)
+    for T in (1, 2, 63, 64, 65, 1000, 2999, 3000):
+        dev = E.token_index(ids.cuda(), T, 50).cpu().numpy().astype(bool)
+        ref = OP.index_blocks(ids.numpy(), T)
+        nb = ref.shape[1]
+        assert (dev[:, :nb] == ref).all(), T
+        assert not dev[:, nb:].any()
+
+
+def _state_to_oracle(p: FusedPlanner, G, scale, T, nb_ref=None) -> OP.State:
+    """Oracle state built from the device state (fp32 -> fp64), so one kernel can be checked on
+    exactly the inputs the device saw."""
+    s = p.state
+    nb = O.nblocks(T)
+    nbr = nb if nb_ref is None else nb_ref
+    return OP.State(scale=scale, G=G, T=T, csum=s["csum"][:, :, :nb].double().cpu(),
+                    keep=s["keep"][:, :, :nbr].bool().cpu(), lse_ref=s["lse_ref"][:, :, :nbr].double().cpu(),
+                    cs_ref=s["cs_ref"][:, :, :nbr].double().cpu(), lse_att=s["lse_att"].double().cpu(),
+                    age=s["age"].long().cpu(), t=p.t, calib=s["calib"].double().cpu(), aix=s["aix"].bool().cpu())
+
+
+def _agree(dev, ref, margin, what):
+    """dev / ref bool tensors of the same shape (per head leading dims); margin per head."""
+    diff = dev != ref
+    while diff.dim() > margin.dim():
+        diff = diff.any(-1)
+    bad = diff & (margin >= BORDER)
+    n_border = int((diff & (margin < BORDER)).sum())
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())} head(s) differ away from the threshold"
+    return n_border
+
+
+@pytest.mark.parametrize("G,D", [(4, 128), (7, 128), (4, 64)])
+def test_plan_update_kernels(gpu, G, D):
+    """One plan and one update launch each on identical inputs, after a device initialisation."""
+    run = W.planner_run(layers=1, B=2, Hq=4 * G, Hkv=4, D=D, T0=3000, steps=8, seed=21 + G)
+    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), dense_heads=(3,))
+    qp = W.QueryProcess(run, 0, p_jump=0.3)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    fp = FusedPlanner(dpolicy(pol))
+    T = run.T0[0] + 1
+    fp.first(qp.next().cuda(), k[:, :, :T], v[:, :, :T], run.scale)
+    for step in range(1, 6):
+        T += 1
+        q = qp.next()
+        nb = O.nblocks(T)
+        st = _state_to_oracle(fp, G, run.scale, T - 1)
+        st.csum = st.csum[:, :, :O.nblocks(T - 1)]
+        pr = OP.plan(st, q, k[:, :, :T].cpu(), pol)
+        s = fp.state
+        qd = q.cuda()
+        E.plan(qd, k[:, :, :T], s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"],
+               s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], run.scale, pol.delta, OP.max_age_at(pol, step),
+               pol.local, True, None, s["calib"], s["est"], True, OP.KINDS[pol.calib_kind], None)
+        fp.t, fp.T = step, T
+        trig = s["trig"].bool().cpu()
+        nbord = _agree(trig, pr["trig"], pr["margin"], "refresh decision")
+        assert torch.equal(fp.read_mask(nb).cpu()[trig == pr["trig"]], pr["read"][trig == pr["trig"]])
+        assert (s["est"].double().cpu() - pr["miss"]).abs().max().item() <= 1e-4
+        assert (s["cs_now"][:, :, :nb].double().cpu() - pr["cs"]).abs().max().item() <= 1e-4
+        assert (s["csum"][:, :, :nb].double().cpu() - st.csum).abs().max().item() <= 1e-3
+        # update on the stats of the device's own pass
+        r = K.decode(qd, k[:, :, :T], v[:, :, :T], run.scale, plan=K.Plan(s["block_idx"], s["block_cnt"], nb, nb),
+                     stats=True)
+        logw = O.block_logw(r["blk_max"].double().cpu(), r["blk_sum"].double().cpu())
+        st_u = _state_to_oracle(fp, G, run.scale, T, nb_ref=O.nblocks(T))
+        pr_u = dict(pr, trig=trig)
+        E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
+                 s["lse_att"], T, pol.level, pol.local, s["flags"], None, s["est"], s["calib"], pol.calib,
+                 pol.calib_free, OP.KINDS[pol.calib_kind], None, 0.0)
+        pr_u["miss"] = s["est"].double().cpu()
+        pr_u["cs"] = s["cs_now"][:, :, :nb].double().cpu()
+        OP.update(st_u, pr_u, logw, pol)
+        keep_dev = s["keep"][:, :, :nb].bool().cpu()
+        kb = _agree(keep_dev, st_u.keep, torch.full(trig.shape, st_u.topp_margin, dtype=torch.float64), "stored set")
+        assert (s["lse_att"].double().cpu() - st_u.lse_att).abs().max().item() <= 1e-4
+        assert (s["calib"].double().cpu() - st_u.calib).abs().max().item() <= 1e-4
+        fin = torch.isfinite(st_u.lse_ref)
+        assert torch.equal(torch.isfinite(s["lse_ref"][:, :, :nb].cpu()), fin)
+        assert (s["lse_ref"][:, :, :nb].double().cpu() - st_u.lse_ref)[fin].abs().max().item() <= 1e-4
+        print(f"G{G} D{D} step {step}: T {T}, refreshing {int(trig.sum())}/{trig.numel()}, borderline "
+              f"decisions {nbord}, stored-set borderline {kb}", flush=True)
+
+
+def _run_loop(pol: OP.Policy, G=4, D=128, B=1, Hkv=8, T0=4096, steps=40, seed=4, p_jump=0.03):
+    run = W.planner_run(layers=1, B=B, Hq=G * Hkv, Hkv=Hkv, D=D, T0=T0, steps=steps, seed=seed)
+    qp = W.QueryProcess(run, 0, p_jump=p_jump)
+    k_cpu, v_cpu = run.k[0], run.v[0]
+    k, v = k_cpu.cuda(), v_cpu.cuda()
+    ids = run.ids.cuda()
+    fp = FusedPlanner(dpolicy(pol))
+    st = None
+    stats = dict(head_steps=0, same=0, border=0, refresh_dev=0, refresh_ref=0, read=0, total=0, max_err=0.0)
+    for t in range(steps):
+        T = T0 + t + 1
+        q = qp.next()
+        nb = O.nblocks(T)
+        idx_ref = torch.from_numpy(OP.index_blocks(run.ids.numpy(), T))
+        if t == 0:
+            out_d = fp.first(q.cuda(), k[:, :, :T], v[:, :, :T], run.scale)
+            st, out_r = OP.init(q, k_cpu[:, :, :T], v_cpu[:, :, :T], run.scale, pol)
+            read_r = torch.ones(B, Hkv, nb, dtype=torch.bool)
+            read_d = fp.read_mask(nb).cpu()
+            margin = torch.full((B, Hkv), math.inf, dtype=torch.float64)
+        else:
+            needs_index = bool(pol.index_heads) or pol.calib_auto_ix is not None
+            out_d = fp.step(q.cuda(), k[:, :, :T], v[:, :, :T], run.scale, ids=ids if needs_index else None)
+            out_r, pr = OP.step(st, q, k_cpu[:, :, :T], v_cpu[:, :, :T], pol, idx=idx_ref)
+            read_r, margin = pr["read"], pr["margin"]
+            read_d = fp.read_mask(nb).cpu()
+            stats["refresh_dev"] += int(fp.state["trig"].sum())
+            stats["refresh_ref"] += int(pr["trig"].sum())
+        same = (read_d == read_r).all(-1)
+        stats["head_steps"] += same.numel()
+        stats["same"] += int(same.sum())
+        stats["border"] += _agree(read_d, read_r, margin, f"read set at step {t}")
+        stats["read"] += int(read_r.sum())
+        stats["total"] += read_r.numel()
+        hq = same.repeat_interleave(G, 1)
+        num = (out_d.float().cpu().double() - out_r).norm(dim=-1)
+        den = out_r.norm(dim=-1).clamp_min(1e-12)
+        stats["max_err"] = max(stats["max_err"], float((num / den)[hq].max()) if bool(hq.any()) else 0.0)
+        if pol.calib is not None:
+            assert (fp.state["calib"].double().cpu() - st.calib).abs().max().item() <= 1e-4
+        if pol.calib_auto_ix is not None:
+            assert torch.equal(fp.state["aix"].bool().cpu(), st.aix)
+    print(f"{pol}: identical read sets on {stats['same']}/{stats['head_steps']} head-steps "
+          f"(borderline {stats['border']}), refreshes device {stats['refresh_dev']} / oracle {stats['refresh_ref']}, "
+          f"blocks read {stats['read'] / stats['total']:.3f}, max rel. output err {stats['max_err']:.2e}, "
+          f"min top-p margin {st.topp_margin:.1e}", flush=True)
+    assert stats["max_err"] <= 2e-3
+    return stats
+
+
+POLICIES = {
+    "stage3": OP.Policy(dense_heads=(6,)),
+    "stage4": OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1),
+    "logit": OP.Policy(calib=0.3, calib_kind="logit", calib_warm=(32, 8)),
+    "add": OP.Policy(calib=0.3, calib_kind="add", calib_warm=(32, 8)),
+    "index_union": OP.Policy(index_heads=(2,), index_union=True, dense_heads=(6,)),
+    "index_only": OP.Policy(index_heads=(2,), index_union=False),
+    "auto_index": OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.001),
+}
+
+
+@pytest.mark.parametrize("name", list(POLICIES))
+def test_planner_loop(gpu, name):
+    """The fused loop (plan -> masked + stats attention -> update, device initialisation) against
+    the oracle's refresh_pre_step, free-running for 40 decode steps with query drift and jumps
+    (bench/test_planner.py:71-133, with the pass bar raised from 97% agreement to 100%)."""
+    _run_loop(POLICIES[name], p_jump=0.05)
+
+
+def test_planner_loop_gqa7_batch(gpu):
+    """Config 5 shape (28 / 4 heads, G 7) at batch 3 with the stage-4 policy."""
+    _run_loop(POLICIES["stage4"], G=7, Hkv=4, B=3, T0=2500, steps=30, seed=5, p_jump=0.05)

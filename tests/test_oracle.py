@@ -1,0 +1,260 @@
+"""Pins the CPU oracle (oracle/) without trusting its own formulas: against a library routine
+(torch's scaled_dot_product_attention), brute-force loops on tiny inputs, and closed-form
+invariants chosen so that a dropped term, a sign or index error or a transposed operand fails.
+The reference ships no golden vectors for this path (its tests read model dumps that are not in
+the repository), so these checks are what fix the oracle; tests/golden/ holds fixtures made by
+the pinned oracle for the GPU tests to reuse."""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as O
+from oracle import planner as OP
+
+
+def rnd(*shape, seed=0, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=dtype)
+
+
+def brute_decode(q, k, v, scale, keep=None):
+    """Pure-Python loops: softmax attention of each query head over its KV head's kept tokens."""
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    out = torch.zeros(B, Hq, D, dtype=torch.float64)
+    lse = torch.full((B, Hq), -math.inf, dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // G
+            toks = [t for t in range(T) if keep is None or bool(keep[b, kh, t // 64])]
+            if not toks:
+                continue
+            s = [scale * sum(float(q[b, h, d]) * float(k[b, kh, t, d]) for d in range(D)) for t in toks]
+            m = max(s)
+            w = [math.exp(x - m) for x in s]
+            z = sum(w)
+            lse[b, h] = m + math.log(z)
+            for d in range(D):
+                out[b, h, d] = sum(wi * float(v[b, kh, t, d]) for wi, t in zip(w, toks)) / z
+    return out, lse
+
+
+def test_decode_vs_sdpa():
+    for (B, Hq, Hkv, T, D) in ((2, 8, 2, 300, 16), (1, 28, 4, 129, 32), (3, 4, 4, 64, 8)):
+        q, k, v = rnd(B, Hq, D, seed=1), rnd(B, Hkv, T, D, seed=2), rnd(B, Hkv, T, D, seed=3)
+        out, lse = O.decode(q, k, v, 0.37)
+        ref = F.scaled_dot_product_attention(q[:, :, None], k, v, scale=0.37, enable_gqa=True)[:, :, 0]
+        assert torch.allclose(out, ref, atol=1e-12, rtol=1e-10)
+        s = torch.einsum("bhd,bhtd->bht", q, k.repeat_interleave(Hq // Hkv, 1)) * 0.37
+        assert torch.allclose(lse, torch.logsumexp(s, -1), atol=1e-12)
+
+
+def test_decode_masked_vs_brute_and_gather():
+    B, Hq, Hkv, T, D = 2, 4, 2, 150, 3
+    q, k, v = rnd(B, Hq, D, seed=4), rnd(B, Hkv, T, D, seed=5), rnd(B, Hkv, T, D, seed=6)
+    keep = torch.tensor([[[1, 0, 1], [0, 1, 0]], [[0, 0, 1], [1, 1, 1]]], dtype=torch.bool)
+    out, lse = O.decode(q, k, v, 0.5, keep=keep)
+    bo, bl = brute_decode(q, k, v, 0.5, keep)
+    assert torch.allclose(out, bo, atol=1e-12) and torch.allclose(lse, bl, atol=1e-12)
+    # masked == SDPA on the gathered kept tokens, per (b, kv head)
+    for b in range(B):
+        for h in range(Hkv):
+            toks = torch.nonzero(O.token_mask(keep[b, h], T)).flatten()
+            ref = F.scaled_dot_product_attention(q[b:b + 1, 2 * h:2 * h + 2, None], k[b:b + 1, h:h + 1, toks],
+                                                 v[b:b + 1, h:h + 1, toks], scale=0.5)[0, :, 0]
+            assert torch.allclose(out[b, 2 * h:2 * h + 2], ref, atol=1e-12)
+    # empty kept set: out 0, lse -inf (what a kernel that reads nothing returns)
+    out, lse = O.decode(q, k, v, 0.5, keep=torch.zeros_like(keep))
+    assert (out == 0).all() and torch.isinf(lse).all()
+
+
+def test_block_stats_invariants():
+    B, Hq, Hkv, T, D = 1, 6, 3, 200, 8
+    q, k = rnd(B, Hq, D, seed=7), rnd(B, Hkv, T, D, seed=8)
+    M, S = O.block_stats(q, k, 0.3)
+    s = O.scores(q, k, 0.3)
+    # the block log-weights merge to the full log-sum-exp; each block max is attained
+    assert torch.allclose(torch.logsumexp(O.block_logw(M, S), -1), torch.logsumexp(s, -1), atol=1e-12)
+    for blk in range(O.nblocks(T)):
+        seg = s[..., blk * 64:min(T, blk * 64 + 64)]
+        assert torch.equal(M[..., blk], seg.amax(-1))
+        assert torch.allclose(S[..., blk], torch.exp(seg - seg.amax(-1, keepdim=True)).sum(-1), atol=1e-12)
+    # P: exp(s - block max) reproduces exp(s) after scaling back, 1 at the block max, 0 past T
+    P = O.p_values(q, k, 0.3)
+    assert torch.allclose(P[..., :T] * torch.exp(M.repeat_interleave(64, -1)[..., :T]), torch.exp(s), rtol=1e-12)
+    assert (P[..., T:] == 0).all() and torch.allclose(P.reshape(B, Hq, -1, 64).amax(-1), torch.ones_like(M))
+    keep = torch.zeros(B, Hkv, O.nblocks(T), dtype=torch.bool)
+    keep[..., 1] = True
+    Mk, Sk = O.block_stats(q, k, 0.3, keep=keep)
+    assert torch.isinf(Mk[..., 0]).all() and (Sk[..., 0] == 0).all() and torch.equal(Mk[..., 1], M[..., 1])
+
+
+def brute_topp(w, level):
+    """Fewest blocks whose weights reach `level` (all subsets); ties at the cut kept."""
+    n = len(w)
+    for size in range(1, n + 1):
+        best = max(itertools.combinations(range(n), size), key=lambda c: sum(w[i] for i in c))
+        if sum(w[i] for i in best) >= level:
+            thr = min(w[i] for i in best)
+            return {i for i in range(n) if w[i] >= thr}
+    return set(range(n))
+
+
+def test_topp_vs_brute_force():
+    g = torch.Generator().manual_seed(9)
+    for trial in range(200):
+        nb = int(torch.randint(1, 9, (1,), generator=g))
+        logw = torch.randn(1, 1, nb, generator=g, dtype=torch.float64) * 3
+        level = float(torch.rand((), generator=g)) * 0.5 + 0.5
+        keep_h, _ = O.topp_heads(logw, level)
+        w = torch.softmax(logw[0, 0], -1).tolist()
+        assert set(torch.nonzero(keep_h[0, 0]).flatten().tolist()) == brute_topp(w, level), (logw, level)
+    # GQA union + sink + local, rule tau
+    logw = rnd(1, 4, 10, seed=10) * 2
+    keep = O.select_blocks(logw, 2, "tau", 0.1, local=2)
+    W = torch.softmax(logw, -1)
+    for h in range(2):
+        for blk in range(10):
+            expect = blk == 0 or blk >= 8 or bool((W[0, 2 * h:2 * h + 2, blk] >= 0.1).any())
+            assert bool(keep[0, h, blk]) == expect
+
+
+def test_vskip1_rule_vs_brute():
+    B, Hq, Hkv, T, D = 1, 4, 2, 64 * 6 + 5, 4
+    q, k = rnd(B, Hq, D, seed=11) * 2, rnd(B, Hkv, T, D, seed=12)
+    for lp in (None, torch.tensor([[3.0, 4.0, 5.0, 6.0]], dtype=torch.float64)):
+        keep, z = O.vskip1_keep(q, k, 0.5, 1e-2, 1, lse_prev=lp)
+        s = O.scores(q, k, 0.5)
+        for h in range(Hkv):
+            for blk in range(7):
+                lse_b = [float(torch.logsumexp(s[0, g, blk * 64:min(T, blk * 64 + 64)], -1)) for g in (2 * h, 2 * h + 1)]
+                lse0 = [float(torch.logsumexp(s[0, g, :64], -1)) if lp is None else float(lp[0, g]) for g in (2 * h, 2 * h + 1)]
+                vote = any(a - b >= math.log(1e-2) for a, b in zip(lse_b, lse0))
+                assert bool(keep[0, h, blk]) == (blk == 0 or blk == 6 or vote)
+
+
+def test_two_pass_identity():
+    """pass 2 with blk_scale = exp(blk_max - lse_kept) on the pass-1 P is exact attention over the
+    kept set (kernels/kvskip.py:157-179)."""
+    B, Hq, Hkv, T, D = 1, 4, 2, 300, 8
+    q, k, v = rnd(B, Hq, D, seed=13), rnd(B, Hkv, T, D, seed=14), rnd(B, Hkv, T, D, seed=15)
+    M, S = O.block_stats(q, k, 0.4)
+    logw = O.block_logw(M, S)
+    keep = O.select_blocks(logw, 2, "topp", 0.9, local=1)
+    kh = O.heads(keep, 2)
+    lse_kept = logw.masked_fill(~kh, -math.inf).logsumexp(-1, keepdim=True)
+    scale_b = torch.exp(M - lse_kept).masked_fill(~kh, 0.0).reshape(B, Hkv, 2, -1).transpose(2, 3)
+    out = O.pv(O.p_values(q, k, 0.4), v, scale_b, keep)
+    ref, _ = O.decode(q, k, v, 0.4, keep=keep)
+    assert torch.allclose(out, ref, atol=1e-12)
+
+
+def test_split_ranges():
+    for n in (0, 1, 7, 64, 65):
+        for S in (1, 3, 8, 70):
+            r = O.split_ranges(n, S)
+            assert len(r) == S and r[0][0] == 0 and r[-1][1] == n
+            assert all(a[1] == b[0] for a, b in zip(r, r[1:]))
+
+
+def test_centroids_vs_loops():
+    B, Hq, Hkv, T, D = 1, 4, 2, 130, 3
+    q, k = rnd(B, Hq, D, seed=16), rnd(B, Hkv, T, D, seed=17)
+    cs = OP.centroid_sums(k)
+    sc = OP.centroid_scores(q, cs, T, 0.7)
+    for h in range(Hq):
+        for blk in range(3):
+            rows = range(blk * 64, min(T, blk * 64 + 64))
+            c = [sum(float(k[0, h // 2, t, d]) for t in rows) / len(rows) for d in range(D)]
+            assert abs(float(sc[0, h, blk]) - 0.7 * sum(float(q[0, h, d]) * c[d] for d in range(D))) < 1e-12
+
+
+def _layer(T=2000, G=4, Hkv=2, D=16, seed=18):
+    q = rnd(1, G * Hkv, D, seed=seed) * 1.5
+    k = rnd(1, Hkv, T, D, seed=seed + 1)
+    k[:, :, 0:64] += 2.0 * q.reshape(1, Hkv, G, D).mean(2)[:, :, None] / D ** 0.5
+    return q, k, rnd(1, Hkv, T, D, seed=seed + 2)
+
+
+def test_estimate_is_exact_at_refresh():
+    """Right after a refresh, with the same query and no new token, every centroid score equals its
+    reference, so the estimate is the block log-sum-exp over the blocks outside the attended set:
+    miss = that set's true missed softmax mass (brute force), which top-p 0.99 keeps <= 0.01."""
+    q, k, v = _layer()
+    pol = OP.Policy(level=0.99)
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    pr = OP.plan(st, q, k, pol)
+    p = torch.softmax(O.scores(q, k, 1.0), -1)                                      # [1, Hq, T]
+    att = O.heads(O.token_mask(st.keep | O.always_keep(O.nblocks(k.shape[2]), pol.local), k.shape[2]), 4)
+    missed = (p * ~att).sum(-1).reshape(1, 2, 4).amax(-1)
+    assert torch.allclose(pr["miss"], missed, atol=1e-12)
+    assert (missed > 0).all() and (missed <= 1 - pol.level + 1e-12).all() and not pr["trig"].any()
+    assert not st.keep.all()
+
+
+def test_estimate_tracks_drift_and_triggers():
+    """Moving the query onto keys outside the stored set raises the estimate past delta (refresh);
+    the age limit and forced heads refresh regardless; the warm-up shortens the age limit."""
+    q, k, v = _layer(seed=30)
+    pol = OP.Policy(delta=0.05, max_age=3, dense_heads=(1,))
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    # query head 0 turns to the mean key of a block outside its group's stored set
+    outside = int(torch.nonzero(~(st.keep[0, 0] | O.always_keep(st.keep.shape[-1], 2)))[0])
+    c = k[0, 0, outside * 64:outside * 64 + 64].mean(0)
+    q2 = q.clone()
+    q2[0, 0] = 40.0 * c / c.norm()
+    pr = OP.plan(st, q2, k, pol)
+    assert bool(pr["trig"][0, 0]) and pr["dec"][0, 0] > pol.delta and bool(pr["trig"][0, 1])
+    assert bool(pr["read"][0, 0].all())
+    # the unchanged query of the same state does not trigger; the age limit then does
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    for t in range(1, 4):
+        pr = OP.plan(st, q, k, pol)
+        assert bool(pr["trig"][0, 0]) == (t == 3) and bool(pr["trig"][0, 1])
+    warm = OP.Policy(max_age=3, calib_warm=(2, 1))
+    assert OP.max_age_at(warm, 1) == 1 and OP.max_age_at(warm, 2) == 3
+
+
+def test_calibration_peak_bounds_the_residual():
+    """kind "peak" keeps c >= real - estimate on every refresh (decaying maximum); with rate 0 it is
+    exactly the largest residual seen; real = the attended set's true missed mass."""
+    q, k, v = _layer(seed=40)
+    pol = OP.Policy(calib=0.0, calib_kind="peak", dense_heads=(0, 1))
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    q2 = q + 0.8 * rnd(*q.shape, seed=41)
+    out, pr = OP.step(st, q2, k, v, pol)
+    assert (pr["miss"] > 0).all()
+    p = torch.softmax(O.scores(q2, k, 1.0), -1)
+    att = O.heads(O.token_mask(pr["sel"], k.shape[2]), 4)
+    real = (p * ~att).sum(-1).reshape(1, 2, 4).amax(-1)
+    assert (real > 0).all()
+    assert torch.allclose(st.calib, torch.clamp(real - pr["miss"], min=0.0), atol=1e-12)
+
+
+def test_token_index_vs_loops():
+    g = np.random.default_rng(3)
+    ids = g.integers(0, 7, size=(2, 300))
+    for T in (1, 2, 64, 65, 200, 300):
+        got = OP.index_blocks(ids, T)
+        for b in range(2):
+            cur = ids[b, T - 1]
+            for blk in range(O.nblocks(T)):
+                hit = False
+                for j in range(blk * 64, min(T, blk * 64 + 64)):
+                    same = j < T - 1 and ids[b, j] == cur
+                    after = j >= 1 and j - 1 < T - 1 and ids[b, j - 1] == cur
+                    hit = hit or same or after
+                assert got[b, blk] == hit
+
+
+def test_attended_lse_all_blocks_is_full_lse():
+    q, k, v = _layer(seed=50)
+    M, S = O.block_stats(q, k, 0.25)
+    full = OP.attended_lse(O.block_logw(M, S), torch.ones(1, 2, M.shape[-1], dtype=torch.bool), 4)
+    assert torch.allclose(full, torch.logsumexp(O.scores(q, k, 0.25), -1), atol=1e-12)
