@@ -121,6 +121,9 @@ def main():
     ap.add_argument("--splits", type=int, default=None, help="override the split count of the dense op")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--events", type=int, default=64, help="event-timed calls per path")
+    ap.add_argument("--no-planner", action="store_true", help="skip the config-4 planner loop")
+    ap.add_argument("--planner-layers", type=int, default=32)
+    ap.add_argument("--planner-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -241,6 +244,11 @@ def main():
     del x
     log(f"cfg1: {us1:.1f} us; read ceiling {best:.0f} GB/s")
 
+    # ---- config 4: 32-layer decode loop with the device-side planner (stage-4 policy, layer 0 dense)
+    if not args.no_planner:
+        res["planner_cfg4"] = bench_planner(dev, layers=args.planner_layers, T0=32768, steps=args.planner_steps)
+        torch.cuda.empty_cache()
+
     roof = {"bound": "hbm", "achieved": res["dense"]["GBs_event_median"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": res["dense"]["GBs_event_median"] / PEAK_GBS, "traffic": None,
             "kernel": "decode_kernel<128,4,dense> at config 2 (split merge in-kernel), HIP events per launch "
@@ -263,6 +271,102 @@ def main():
         "paths": res, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
+    """Config 4: `layers` Llama-3.1-8B attention layers, `steps` decode steps from T0 (one token
+    appended per step), query drift + jumps, stage-4 policy (delta 0.05, max age 32, calibration
+    0.05 peak, warm-up (32, 8), token-index latch at 0.1; reproduce/04-tails.sh:16,63-69), layer 0
+    dense. One eager pass with counters gives the read fraction and refresh rate; the timed passes
+    replay HIP graphs of `chunk` steps x all layers (decisions still made on the device) for the
+    planner loop and for dense decode of every layer."""
+    import torch
+
+    from kvskip_amd import ext as E
+    from kvskip_amd import kvskip as K
+    from kvskip_amd import workloads as W
+    from kvskip_amd.planner import FusedPlanner, Policy
+
+    t_gen = time.perf_counter()
+    run = W.planner_run(layers=layers, T0=T0, steps=steps, seed=4, device=dev)
+    B, Hkv, _, D = run.k[0].shape
+    Hq = run.q0[0].shape[1]
+    qps = [W.QueryProcess(run, l) for l in range(layers)]
+    qs = torch.stack([torch.stack([qps[l].next() for l in range(layers)]) for _ in range(steps)]).to(dev)
+    NBC = math.ceil((T0 + 1) / 64) + 64
+    idx_all = torch.zeros(steps, B, NBC, dtype=torch.uint8, device=dev)
+    ids = run.ids.to(dev)
+    for t in range(steps):
+        E.token_index(ids, T0 + t + 1, NBC, out=idx_all[t])
+    pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    log(f"cfg4: {layers} layers x {steps} steps from T {T0} generated in {time.perf_counter() - t_gen:.1f} s")
+
+    def kv(l, T):
+        return run.k[l][:, :, :T], run.v[l][:, :, :T]
+
+    def dense_layer(l, t):
+        k, v = kv(l, T0 + t + 1)
+        return K.decode(qs[t, l], k, v, run.scale)["out"]
+
+    def planner_pass(planners, t):
+        for l in range(layers):
+            if l == 0:
+                dense_layer(0, t)
+                continue
+            k, v = kv(l, T0 + t + 1)
+            if t == 0:
+                planners[l].first(qs[t, l], k, v, run.scale)
+            else:
+                planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t])
+
+    # eager pass with counters
+    planners = [None] + [FusedPlanner(pol) for _ in range(1, layers)]
+    for t in range(steps):
+        planner_pass(planners, t)
+    torch.cuda.synchronize()
+    read = sum(float(p.counters["blocks_read"]) for p in planners[1:])
+    total = sum(float(p.counters["blocks_total"]) for p in planners[1:])
+    refresh = sum(float(p.counters.get("dense_heads", 0)) for p in planners[1:]) - (layers - 1) * B * Hkv
+    head_steps = (layers - 1) * (steps - 1) * B * Hkv
+    log(f"cfg4 eager: blocks read {read / total:.3f}, refresh rate {refresh / head_steps:.3f}")
+
+    def capture(fn_step, t0, t1):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for t in range(t0, t1):
+                fn_step(t)
+        return g
+
+    def timed(fn_step, init=None):
+        if init is not None:
+            init()
+        torch.cuda.synchronize()
+        graphs = [capture(fn_step, t0, min(steps, t0 + chunk)) for t0 in range(1, steps, chunk)]
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for g in graphs:
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3          # us for steps 1 .. steps-1, all layers
+
+    planners = [None] + [FusedPlanner(pol, count=False) for _ in range(1, layers)]
+    us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
+    us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
+    n = (steps - 1) * layers
+    out = {"layers": layers, "steps": steps, "T0": T0, "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, "
+           "warm (32, 8), auto index 0.1), layer 0 dense", "blocks_read_frac": read / total,
+           "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
+           "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
+           "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
+           "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
+    log(f"cfg4: policy {us_plan / n:.2f} us/layer-step vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), "
+        f"{us_plan / (steps - 1) / 1e3:.3f} ms per 32-layer step")
+    del planners, run, qs
+    return out
 
 
 def cpu_baseline(q, k, v, scale, nbytes, budget_s=12.0):

@@ -152,6 +152,9 @@ typedef struct kvskip_update_args {
   float calib_rate, aix_thr, level;
   int32_t calib_free, calib_kind;
   int32_t B, Hq, Hkv, T, NBC, local;
+  int32_t list_stats;          /* 0: blk_max / blk_sum cover every block (the reference's contract);
+                                  1: they hold values only for the blocks of this step's plan (the
+                                  rest is uninitialised and ignored), so they need no fill */
 } kvskip_update_args;
 
 int kvskip_update(const kvskip_update_args* p, void* stream);

@@ -57,6 +57,7 @@ class UpdateArgs(ctypes.Structure):
         ("calib_rate", c_float), ("aix_thr", c_float), ("level", c_float),
         ("calib_free", c_int32), ("calib_kind", c_int32),
         ("B", c_int32), ("Hq", c_int32), ("Hkv", c_int32), ("T", c_int32), ("NBC", c_int32), ("local", c_int32),
+        ("list_stats", c_int32),
     ]
 
 

@@ -328,11 +328,6 @@ __device__ __forceinline__ float row16_max(float v) {
   return fmaxf(v, dpp<DPP_MIRROR>(v));
 }
 
-// Lane value of another lane as a uniform (scalar) value.
-__device__ __forceinline__ float lane_value(float v, int src) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
-}
-
 // B operand (K^T) of one 64-token block: kr[nt][kk] = 16 bytes of row t0 + 16 nt + lane%16 at
 // 16-byte chunk 4 kk + lane/16. koffm = (lane % 16) * k_st * 2 + 16 * (lane / 16).
 template <int D>

@@ -192,6 +192,8 @@ int kvskip_plan(const kvskip_plan_args* p, void* stream) {
   if (!aligned16(p->csum)) return fail(KVSKIP_E_INVALID, "csum must be 16-byte aligned");
   const int nb = (p->T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK;
   if (nb > p->NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
+  if (nb > kvs::planner_max_blocks(G))
+    return fail(KVSKIP_E_UNSUPPORTED, "plan: %d blocks exceed the planner capacity (%d)", nb, kvs::planner_max_blocks(G));
   if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
   if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
   return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
@@ -211,12 +213,13 @@ int kvskip_update(const kvskip_update_args* p, void* stream) {
   const int nb = (p->T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK;
   if (nb > p->NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
   if (nb > kvs::planner_max_blocks(G))
-    return fail(KVSKIP_E_UNSUPPORTED, "update: %d blocks exceed the LDS capacity (%d)", nb, kvs::planner_max_blocks(G));
+    return fail(KVSKIP_E_UNSUPPORTED, "update: %d blocks exceed the planner capacity (%d)", nb, kvs::planner_max_blocks(G));
   if (p->calib != nullptr) {
     if (p->flags == nullptr || p->est == nullptr) return fail(KVSKIP_E_INVALID, "calibration needs flags and est");
     if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
   }
   if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
+  if (p->list_stats && p->flags == nullptr) return fail(KVSKIP_E_INVALID, "list_stats needs flags");
   return launched(kvs::launch_update(*p, static_cast<hipStream_t>(stream)), "kvskip_update");
 }
 

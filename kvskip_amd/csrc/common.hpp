@@ -72,39 +72,38 @@ __device__ __forceinline__ float sum8(float v) {
 
 __device__ __forceinline__ float xshfl(float v, int mask) { return __shfl_xor(v, mask, WAVE); }
 
-// Reductions over lane bits 3..5 (the 8 row slots of the K layout; values are equal
-// within each aligned group of 8 lanes).
-__device__ __forceinline__ float max_rows8(float v) {
-  v = fmaxf(v, dpp<DPP_ROR8>(v));
-  v = fmaxf(v, xshfl(v, 16));
-  return fmaxf(v, xshfl(v, 32));
-}
-__device__ __forceinline__ float sum_rows8(float v) {
-  v += dpp<DPP_ROR8>(v);
-  v += xshfl(v, 16);
-  return v + xshfl(v, 32);
+// Value of lane `src` as a wavefront-uniform (scalar) value.
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
-// Whole-wave reductions.
+// Combine the four 16-lane rows of a row-reduced value (uniform result, fixed order).
+__device__ __forceinline__ float rows4_sum(float v) {
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float rows4_max(float v) {
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// Reductions over lane bits 3..5 (the 8 row slots of the K layout; values are equal within each
+// aligned group of 8 lanes); the result is wavefront-uniform.
+__device__ __forceinline__ float max_rows8(float v) { return rows4_max(fmaxf(v, dpp<DPP_ROR8>(v))); }
+__device__ __forceinline__ float sum_rows8(float v) { return rows4_sum(v + dpp<DPP_ROR8>(v)); }
+
+// Whole-wavefront reductions (uniform result): DPP inside the 16-lane rows, then the 4 rows.
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<DPP_XOR1>(v);
   v += dpp<DPP_XOR2>(v);
   v += dpp<DPP_HALF_MIRROR>(v);
   v += dpp<DPP_MIRROR>(v);
-  v += xshfl(v, 16);
-  return v + xshfl(v, 32);
+  return rows4_sum(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_XOR1>(v));
   v = fmaxf(v, dpp<DPP_XOR2>(v));
   v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
   v = fmaxf(v, dpp<DPP_MIRROR>(v));
-  v = fmaxf(v, xshfl(v, 16));
-  return fmaxf(v, xshfl(v, 32));
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-  for (int o = 1; o < WAVE; o <<= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+  return rows4_max(v);
 }
 
 // 16-byte loads: plain and streaming (non-temporal).

@@ -11,14 +11,17 @@
 // head refreshes: it reads every block this step, and update rebuilds its set from the block
 // statistics of that same pass (each query head's top-p blocks, union over the group).
 //
-// plan:   workgroup of 4 wavefronts per (b, KV head). Centroid scores with 16 lanes per block
-//         row (fp32 key sums, 4 block rows per wavefront step); the drift estimate is folded
-//         into the same pass (lane 16 r + g keeps head g's running log-sum-exp), so no LDS
-//         copy of the scores is needed; the block list is compacted in ascending order by
-//         wavefront ballots.
-// update: one wavefront per query head of the group (G wavefronts). Top-p by an exact
-//         bitwise search for the largest score key whose upper set holds >= level of the mass
-//         (the fewest blocks reaching level; ties at the threshold are all kept).
+// plan:   one workgroup of 16 wavefronts per (b, KV head). Centroid scores with 16 lanes per
+//         block row (fp32 key sums, 16 block rows in flight per wavefront); the drift estimate is
+//         folded into the same pass (lane 16 r + g keeps head g's running log-sum-exp), so no
+//         LDS copy of the scores is needed; every load of a step (key sums, references, set
+//         flags, the appended key) is issued before any use; the block list is compacted in
+//         ascending order by ballots of the whole workgroup.
+// update: one wavefront per query head of the group (G wavefronts), the head's blocks held in
+//         registers (64 per register slot). Top-p by an exact bitwise search for the largest
+//         score key whose upper set holds >= level of the mass (the fewest blocks reaching
+//         level; ties at the threshold are all kept), on weights computed once; wavefront sums
+//         stay in DPP rows + readlane; the group's union goes through LDS as ballot masks.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -48,42 +51,48 @@ __device__ __forceinline__ void lse_merge(float& m1, float& s1, float m2, float 
   }
 }
 
-// Wavefront merge of (m, s) pairs over the lanes selected by xor masks 16 and 32.
-__device__ __forceinline__ void lse_merge_rows(float& m, float& s) {
-#pragma unroll
-  for (int o = 16; o < WAVE; o <<= 1) {
-    const float m2 = __shfl_xor(m, o, WAVE), s2 = __shfl_xor(s, o, WAVE);
-    lse_merge(m, s, m2, s2);
-  }
-}
-__device__ __forceinline__ void lse_merge_wave(float& m, float& s) {
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const float m2 = __shfl_xor(m, o, WAVE), s2 = __shfl_xor(s, o, WAVE);
-    lse_merge(m, s, m2, s2);
-  }
+// Whole-wavefront log-sum-exp of per-lane (m, s) pairs: max, then rescaled sums (uniform result).
+__device__ __forceinline__ void lse_wave(float& m, float& s) {
+  const float M = wave_max(s > 0.f ? m : NEG_INF);
+  const float S = wave_sum(s > 0.f ? s * __expf(m - M) : 0.f);
+  m = M;
+  s = S;
 }
 
-// Ascending compaction of {blk < nb : pred(blk)} into out[], by one wavefront; returns the count.
-template <typename Pred>
-__device__ __forceinline__ int compact_wave(int nb, int lane, int* out, Pred pred) {
+constexpr int PW = 16;         // plan workgroup: 16 wavefronts
+constexpr int PNT = PW * WAVE;
+constexpr int MAX_NB = 4096;   // planner block capacity: update holds a head's blocks in registers
+
+// Ascending compaction of {i < nb : sF[i] != 0} into out[] by the whole plan workgroup (chunks of
+// PNT blocks, wavefront w taking the chunk's w-th 64); returns the count (uniform).
+__device__ int compact_wg(const uint8_t* sF, int nb, int* out, int* sCnt) {
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   int base = 0;
-  for (int c0 = 0; c0 < nb; c0 += WAVE) {
-    const int blk = c0 + lane;
-    const bool f = blk < nb && pred(blk);
-    const uint64_t mask = __ballot(f);
-    const int off = __popcll(mask & ((uint64_t(1) << lane) - 1));
-    if (f) out[base + off] = blk;
-    base += __popcll(mask);
+  for (int c0 = 0; c0 < nb; c0 += PNT) {
+    const int i = c0 + tid;
+    const bool f = i < nb && sF[i] != 0;
+    const uint64_t m = __ballot(f);
+    if (lane == 0) sCnt[wave] = __popcll(m);
+    __syncthreads();
+    int off = base, tot = 0;
+#pragma unroll
+    for (int w = 0; w < PW; ++w) {
+      const int c = sCnt[w];
+      off += w < wave ? c : 0;
+      tot += c;
+    }
+    if (f) out[off + __popcll(m & ((uint64_t(1) << lane) - 1))] = i;
+    base += tot;
+    __syncthreads();
   }
   return base;
 }
 
-constexpr int PNT = 256;  // plan workgroup
-
 template <int D, int G>
 __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
-  constexpr int DL = D / 16;  // dims per lane in the centroid pass
+  constexpr int DL = D / 16;                         // dims per lane: {64 w + 4 c16 + j}
+  constexpr int DW = DL / 4;
+  constexpr int PU = (D == 128 && G >= 7) ? 2 : 4;  // block-row groups (4 rows each) in flight, 128 VGPRs
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int nb = (p.T + BLK - 1) / BLK;
@@ -93,34 +102,33 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   const uint8_t* keep = p.keep + bh * p.NBC;
   int* bi = p.block_idx + bh * p.NBC;
   const int fl = p.flags[h];
-  __shared__ float sM[PNT / WAVE][G], sS[PNT / WAVE][G];
+  __shared__ uint8_t sF[MAX_NB];  // attended set of this step (block flags)
+  __shared__ float sM[PW][G], sS[PW][G];
+  __shared__ int sCnt[PW];
   __shared__ int sTrig;
 
   if (fl & 2) {  // token-index head: index blocks + sink + local, never refreshes
     const uint8_t* idx = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : nullptr;
-    if (wave == 0) {
-      const int cnt = compact_wave(nb, lane, bi, [&](int i) { return (idx != nullptr && idx[i] != 0) || always_block(i, nb, p.local); });
-      if (lane == 0) {
-        p.block_cnt[bh] = cnt;
-        p.trig[bh] = 0;
-      }
+    for (int i = tid; i < nb; i += PNT)
+      sF[i] = ((idx != nullptr && idx[i] != 0) || always_block(i, nb, p.local)) ? 1 : 0;
+    __syncthreads();
+    const int cnt = compact_wg(sF, nb, bi, sCnt);
+    if (tid == 0) {
+      p.block_cnt[bh] = cnt;
+      p.trig[bh] = 0;
     }
     return;
   }
   const bool uni = p.idx != nullptr && ((fl & 4) || (p.aix != nullptr && p.aix[bh] != 0));
-  const uint8_t* idx = uni ? p.idx + static_cast<int64_t>(b) * p.NBC : nullptr;
-  auto attended = [&](int i) { return keep[i] != 0 || always_block(i, nb, p.local) || (uni && idx[i] != 0); };
+  const uint8_t* ixp = uni ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
+  // decision inputs, in flight during the pass
+  const int age0 = p.age[bh];
+  const float cal0 = (p.calib != nullptr && p.calib_on) ? p.calib[bh] : 0.f;
+  const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + min(lane, G - 1)];
 
-  if (p.add_token && tid < D) {  // the key appended by this step joins its block's sum
-    const int t = p.T - 1;
-    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
-                         static_cast<int64_t>(t) * p.k_st;
-    csum[static_cast<int64_t>(t / BLK) * D + tid] += __uint_as_float(static_cast<uint32_t>(kr[tid]) << 16);
-  }
-  __syncthreads();
-
-  // Centroid scores + drift estimate. Lane (rs = lane/16, c16 = lane%16): block row rs of
-  // each step, dims {4*c16 + j, 64 + 4*c16 + j} (D = 128) or {4*c16 + j} (D = 64).
+  // Lane (rs = lane/16, c16 = lane%16) of a wavefront step: block row 4u + rs of row group u,
+  // dims {64 w + 4 c16 + j}; lane c16 = g also keeps query head g's running log-sum-exp of
+  // lse_ref + cs - cs_ref over the unattended blocks.
   const int rs = lane >> 4, c16 = lane & 15;
   float qf[G][DL];
   {
@@ -129,178 +137,289 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
     for (int g = 0; g < G; ++g) {
       const uint16_t* qp = q + b * p.q_sb + (static_cast<int64_t>(h) * G + g) * p.q_sh;
 #pragma unroll
-      for (int u = 0; u < DL / 4; ++u)
+      for (int w = 0; w < DW; ++w)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          qf[g][4 * u + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * u + 4 * c16 + j]) << 16) * p.scale;
+          qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
     }
   }
-  float em = NEG_INF, es = 0.f;  // head g = c16 (if < G): running log-sum-exp of est over unattended blocks
-  for (int base = 4 * wave; base < nb; base += 4 * (PNT / WAVE)) {
-    const int blk = base + rs;
-    const bool ok = blk < nb;
-    float cv[DL];
-    if (ok) {
-      const float* cp = csum + static_cast<int64_t>(blk) * D;
+  // The key appended by this step (row T-1, block nb-1) joins its block's sum, in registers.
+  const bool add = p.add_token != 0;
+  uint2 kx[DW];
+  if (add) {
+    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
+                         static_cast<int64_t>(p.T - 1) * p.k_st;
 #pragma unroll
-      for (int u = 0; u < DL / 4; ++u) {
-        const float4 t = *reinterpret_cast<const float4*>(cp + 64 * u + 4 * c16);
-        cv[4 * u] = t.x;
-        cv[4 * u + 1] = t.y;
-        cv[4 * u + 2] = t.z;
-        cv[4 * u + 3] = t.w;
+    for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
+  }
+  const int gl = min(c16, G - 1);
+  float em = NEG_INF, es = 0.f;
+  for (int base = 4 * PU * wave; base < nb; base += 4 * PU * PW) {
+    float cv[PU][DL];
+    float lr[PU], cr[PU];
+    bool at[PU];
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {  // every load of the step first
+      const int rc = min(base + 4 * u + rs, nb - 1);
+      const float* cp = csum + static_cast<int64_t>(rc) * D;
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const float4 t = *reinterpret_cast<const float4*>(cp + 64 * w + 4 * c16);
+        cv[u][4 * w] = t.x;
+        cv[u][4 * w + 1] = t.y;
+        cv[u][4 * w + 2] = t.z;
+        cv[u][4 * w + 3] = t.w;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < DL; ++j) cv[j] = 0.f;
+      const int64_t r = row0 + static_cast<int64_t>(gl) * p.NBC + rc;
+      lr[u] = p.lse_ref[r];
+      cr[u] = p.cs_ref[r];
+      at[u] = (static_cast<uint32_t>(keep[rc]) | static_cast<uint32_t>(ixp[rc])) != 0;
     }
-    const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? p.T - blk * BLK : BLK);
-    float mine = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float d = 0.f;
+    for (int u = 0; u < PU; ++u) {
+      const int blk = base + 4 * u + rs;
+      if (add && blk == nb - 1) {
 #pragma unroll
-      for (int j = 0; j < DL; ++j) d = fmaf(qf[g][j], cv[j], d);
-      d += dpp<DPP_XOR1>(d);
-      d += dpp<DPP_XOR2>(d);
-      d += dpp<DPP_HALF_MIRROR>(d);
-      d += dpp<DPP_MIRROR>(d);
-      if (c16 == g) mine = d * inv_n;
-    }
-    if (ok && c16 < G) {
-      p.cs_now[row0 + static_cast<int64_t>(c16) * p.NBC + blk] = mine;
-      if (!attended(blk)) {
-        const int64_t r = row0 + static_cast<int64_t>(c16) * p.NBC + blk;
-        lse_push(em, es, p.lse_ref[r] + mine - p.cs_ref[r]);
+        for (int w = 0; w < DW; ++w) {
+          cv[u][4 * w] += bf_lo(kx[w].x);
+          cv[u][4 * w + 1] += bf_hi(kx[w].x);
+          cv[u][4 * w + 2] += bf_lo(kx[w].y);
+          cv[u][4 * w + 3] += bf_hi(kx[w].y);
+          *reinterpret_cast<float4*>(csum + static_cast<int64_t>(blk) * D + 64 * w + 4 * c16) =
+              make_float4(cv[u][4 * w], cv[u][4 * w + 1], cv[u][4 * w + 2], cv[u][4 * w + 3]);
+        }
+      }
+      const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? p.T - blk * BLK : BLK);
+      float mine = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < DL; ++j) d = fmaf(qf[g][j], cv[u][j], d);
+        d += dpp<DPP_XOR1>(d);
+        d += dpp<DPP_XOR2>(d);
+        d += dpp<DPP_HALF_MIRROR>(d);
+        d += dpp<DPP_MIRROR>(d);
+        if (c16 == g) mine = d * inv_n;
+      }
+      if (blk < nb) {
+        const bool a = at[u] || always_block(blk, nb, p.local);
+        if (c16 == 0) sF[blk] = a ? 1 : 0;
+        if (c16 < G) {
+          p.cs_now[row0 + static_cast<int64_t>(c16) * p.NBC + blk] = mine;
+          if (!a) lse_push(em, es, lr[u] + mine - cr[u]);
+        }
       }
     }
   }
-  lse_merge_rows(em, es);
+  // merge the 4 block-row slots of each head (lanes c16, 16 + c16, 32 + c16, 48 + c16)
+#pragma unroll
+  for (int o = 16; o < WAVE; o <<= 1) {
+    const float m2 = __shfl_xor(em, o, WAVE), s2 = __shfl_xor(es, o, WAVE);
+    lse_merge(em, es, m2, s2);
+  }
   if (rs == 0 && c16 < G) {
     sM[wave][c16] = em;
     sS[wave][c16] = es;
   }
   __syncthreads();
 
-  if (tid == 0) {
+  if (wave == 0) {  // decision: miss = max over the group of sigma(est - lse_att)
     float miss = 0.f;
+#pragma unroll
     for (int g = 0; g < G; ++g) {
-      float M = NEG_INF, S = 0.f;
-      for (int w = 0; w < PNT / WAVE; ++w) lse_merge(M, S, sM[w][g], sS[w][g]);
-      if (S > 0.f) {
-        const float est = M + __logf(S);
-        const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + g];
-        miss = fmaxf(miss, 1.f / (1.f + __expf(la - est)));
+      float m = lane < PW ? sM[lane][g] : NEG_INF, sv = lane < PW ? sS[lane][g] : 0.f;
+      lse_wave(m, sv);
+      if (sv > 0.f) {
+        const float est = m + __logf(sv);
+        miss = fmaxf(miss, 1.f / (1.f + __expf(lane_value(la, g) - est)));
       }
     }
-    if (p.est != nullptr) p.est[bh] = miss;
-    float dec = miss;
-    if (p.calib != nullptr && p.calib_on)
-      dec = p.calib_kind ? miss + p.calib[bh] : 1.f / (1.f + __expf(-(clamped_logit(miss) + p.calib[bh])));
-    const int a = p.age[bh] + 1;
-    const bool tr = dec > p.delta || a >= p.max_age || (fl & 1);
-    p.age[bh] = tr ? 0 : a;
-    p.trig[bh] = tr ? 1 : 0;
-    sTrig = tr;
+    if (lane == 0) {
+      if (p.est != nullptr) p.est[bh] = miss;
+      float dec = miss;
+      if (p.calib != nullptr && p.calib_on)
+        dec = p.calib_kind ? miss + cal0 : 1.f / (1.f + __expf(-(clamped_logit(miss) + cal0)));
+      const int a = age0 + 1;
+      const bool tr = dec > p.delta || a >= p.max_age || (fl & 1);
+      p.age[bh] = tr ? 0 : a;
+      p.trig[bh] = tr ? 1 : 0;
+      sTrig = tr;
+    }
   }
   __syncthreads();
 
-  if (wave == 0) {
-    const bool tr = sTrig != 0;
-    const int cnt = compact_wave(nb, lane, bi, [&](int i) { return tr || attended(i); });
-    if (lane == 0) p.block_cnt[bh] = cnt;
+  if (sTrig != 0) {  // refresh: every block
+    for (int i = tid; i < nb; i += PNT) bi[i] = i;
+    if (tid == 0) p.block_cnt[bh] = nb;
+  } else {
+    const int cnt = compact_wg(sF, nb, bi, sCnt);
+    if (tid == 0) p.block_cnt[bh] = cnt;
   }
 }
 
-template <int G>
-__global__ void update_kernel(const kvskip_update_args p) {
-  extern __shared__ float smem[];
+// Order-preserving key of a float (larger float -> larger key).
+__device__ __forceinline__ uint32_t fkey(float y) {
+  const uint32_t u = __float_as_uint(y);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One wavefront per query head g of the group; lane holds blocks i = lane + 64 r, r < R (nb <= 64 R).
+template <int G, int R>
+__global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_args p) {
+  constexpr int RC = R < 16 ? R : 16;  // register slots whose loads are in flight together
   const int h = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;  // wave = query head g
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int nb = (p.T + BLK - 1) / BLK;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t hrow = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + wave;
-  float* x = smem + static_cast<int64_t>(wave) * nb;                           // [G][nb] block log-weights
-  uint8_t* skeep = reinterpret_cast<uint8_t*>(smem + static_cast<int64_t>(G) * nb);  // [nb]
+  __shared__ uint64_t sKm[G][R];  // each query head's top-p blocks (lane bits of r)
   __shared__ float sReal[G];
   uint8_t* keep = p.keep + bh * p.NBC;
+  const uint8_t* ixp = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
   const bool tr = p.trig[bh] != 0;
   const int fl = p.flags != nullptr ? p.flags[h] : 0;
+  const bool uni = p.idx != nullptr && ((fl & 4) || (p.aix != nullptr && p.aix[bh] != 0));
+  const bool ixh = (fl & 2) != 0;  // token-index head: read index + sink + local (list_stats)
+  const float est0 = p.calib != nullptr ? p.est[bh] : 0.f;
+  const float cal0 = p.calib != nullptr ? p.calib[bh] : 0.f;
 
-  float mx = NEG_INF;
-  for (int i = lane; i < nb; i += WAVE) {
-    const float v = p.blk_max[hrow * nb + i] + __logf(p.blk_sum[hrow * nb + i]);  // -inf where not read
-    x[i] = v;
-    mx = fmaxf(mx, v);
-  }
-  for (int i = tid; i < nb; i += G * WAVE) skeep[i] = 0;
-  mx = wave_max(mx);
-  __syncthreads();
-
-  if (tr && p.calib != nullptr) {  // the mass the attended set missed (this head read every block)
-    const bool uni = p.idx != nullptr && ((fl & 4) || (p.aix != nullptr && p.aix[bh] != 0));
-    const uint8_t* idx = uni ? p.idx + static_cast<int64_t>(b) * p.NBC : nullptr;
-    float mi = NEG_INF, si = 0.f, mo = NEG_INF, so = 0.f;
-    for (int i = lane; i < nb; i += WAVE) {
-      if (keep[i] != 0 || always_block(i, nb, p.local) || (uni && idx[i] != 0))
-        lse_push(mi, si, x[i]);
-      else
-        lse_push(mo, so, x[i]);
+  float x[R];          // block log-weights blk_max + log blk_sum (-inf where not read / past nb)
+  uint64_t kp = 0;     // bit r: block in the stored set before this update
+  uint64_t att = 0;    // bit r: block attended this step (stored set + sink + local + index union)
+#pragma unroll
+  for (int c = 0; c < R; c += RC) {
+    float bm[RC], bs[RC];
+    uint32_t kb[RC], ib[RC];
+#pragma unroll
+    for (int r = 0; r < RC; ++r) {  // loads of the chunk first, clamped in range
+      const int ic = min(lane + WAVE * (c + r), nb - 1);
+      bm[r] = p.blk_max[hrow * nb + ic];
+      bs[r] = p.blk_sum[hrow * nb + ic];
+      kb[r] = keep[ic];
+      ib[r] = ixp[ic];
     }
-    lse_merge_wave(mi, si);
-    lse_merge_wave(mo, so);
-    if (lane == 0) sReal[wave] = so > 0.f ? 1.f / (1.f + __expf((mi + __logf(si)) - (mo + __logf(so)))) : 0.f;
+#pragma unroll
+    for (int r = 0; r < RC; ++r) {
+      const int i = lane + WAVE * (c + r);
+      const bool in = i < nb;
+      const bool al = always_block(i, nb, p.local);
+      const bool k = in && kb[r] != 0;
+      const bool a = in && (k || al || (uni && ib[r] != 0));
+      const bool rd = in && (!p.list_stats || tr || (ixh ? (p.idx != nullptr && ib[r] != 0) || al : a));
+      x[c + r] = rd ? bm[r] + __logf(bs[r]) : NEG_INF;
+      kp |= static_cast<uint64_t>(k) << (c + r);
+      att |= static_cast<uint64_t>(a) << (c + r);
+    }
   }
+
   if (tr) {
+    float cn[R <= 16 ? R : 1];  // cs_now of the refresh, in flight during the search
+    if constexpr (R <= 16) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) cn[r] = p.cs_now[hrow * p.NBC + min(lane + WAVE * r, nb - 1)];
+    }
+    float mx = NEG_INF;
+#pragma unroll
+    for (int r = 0; r < R; ++r) mx = fmaxf(mx, x[r]);
+    mx = wave_max(mx);
     float se = 0.f;
-    for (int i = lane; i < nb; i += WAVE) se += __expf(x[i] - mx);
+#pragma unroll
+    for (int r = 0; r < R; ++r) se += __expf(x[r] - mx);
     const float lse = mx + __logf(wave_sum(se));
-    // Largest key theta (order-preserving bits of y = x - lse) whose upper set {key >= theta}
-    // holds >= level of the mass; keep exactly that upper set.
-    auto key_of = [](float y) -> uint32_t {
-      const uint32_t u = __float_as_uint(y);
-      return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    };
+    float w[R];
+    uint32_t key[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float y = x[r] - lse;
+      w[r] = __expf(y);
+      key[r] = fkey(y);
+    }
+    // Largest key theta of y = x - lse whose upper set {key >= theta} holds >= level of the
+    // mass: the fewest blocks reaching level (ties at the cut kept); exact, 32 bit steps.
     uint32_t theta = 0;
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t cand = theta | (1u << bit);
-      float acc = 0.f;
-      for (int i = lane; i < nb; i += WAVE) {
-        const float y = x[i] - lse;
-        if (key_of(y) >= cand) acc += __expf(y);
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; r += 2) {
+        acc0 += key[r] >= cand ? w[r] : 0.f;
+        if (r + 1 < R) acc1 += key[r + 1] >= cand ? w[r + 1] : 0.f;
       }
-      if (wave_sum(acc) >= p.level) theta = cand;
+      if (wave_sum(acc0 + acc1) >= p.level) theta = cand;
     }
-    for (int i = lane; i < nb; i += WAVE)
-      if (key_of(x[i] - lse) >= theta) skeep[i] = 1;
-    for (int i = lane; i < p.NBC; i += WAVE) {
-      p.lse_ref[hrow * p.NBC + i] = i < nb ? x[i] : NEG_INF;
-      p.cs_ref[hrow * p.NBC + i] = i < nb ? p.cs_now[hrow * p.NBC + i] : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t m = __ballot(lane + WAVE * r < nb && key[r] >= theta);
+      if (lane == 0) sKm[wave][r] = m;
+    }
+    if (p.calib != nullptr) {  // the mass the attended set missed (this head read every block)
+      float mi = NEG_INF, si = 0.f, mo = NEG_INF, so = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if ((att >> r) & 1)
+          lse_push(mi, si, x[r]);
+        else
+          lse_push(mo, so, x[r]);
+      }
+      lse_wave(mi, si);
+      lse_wave(mo, so);
+      if (lane == 0) sReal[wave] = so > 0.f ? 1.f / (1.f + __expf((mi + __logf(si)) - (mo + __logf(so)))) : 0.f;
+    }
+    // references of the refresh: lse_ref <- x, cs_ref <- cs_now (capacity tail: -inf / 0)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = lane + WAVE * r;
+      if (i < p.NBC) {
+        float c;
+        if constexpr (R <= 16)
+          c = cn[r];
+        else
+          c = p.cs_now[hrow * p.NBC + min(i, nb - 1)];
+        p.lse_ref[hrow * p.NBC + i] = x[r];
+        p.cs_ref[hrow * p.NBC + i] = i < nb ? c : 0.f;
+      }
+    }
+    for (int i = WAVE * R + lane; i < p.NBC; i += WAVE) {
+      p.lse_ref[hrow * p.NBC + i] = NEG_INF;
+      p.cs_ref[hrow * p.NBC + i] = 0.f;
     }
   }
-  __syncthreads();
+  __syncthreads();  // every read of the old stored set is done; sKm / sReal complete
+
   if (tr && p.calib != nullptr && tid == 0) {
     float real = 0.f;
     for (int g = 0; g < G; ++g) real = fmaxf(real, sReal[g]);
-    const float est = p.est[bh];
-    const float resid = p.calib_kind ? real - est : clamped_logit(real) - clamped_logit(est);
-    float c = p.calib_kind == 2 ? fmaxf((1.f - p.calib_rate) * p.calib[bh], resid)
-                                : (1.f - p.calib_rate) * p.calib[bh] + p.calib_rate * resid;
+    const float resid = p.calib_kind ? real - est0 : clamped_logit(real) - clamped_logit(est0);
+    float c = p.calib_kind == 2 ? fmaxf((1.f - p.calib_rate) * cal0, resid)
+                                : (1.f - p.calib_rate) * cal0 + p.calib_rate * resid;
     if (!p.calib_free) c = fmaxf(c, 0.f);
     p.calib[bh] = c;
     if (p.aix != nullptr && c > p.aix_thr) p.aix[bh] = 1;
   }
+  uint64_t kn = kp;  // bit r: block in the stored set after this update
   if (tr) {
-    for (int i = tid; i < p.NBC; i += G * WAVE)
-      keep[i] = (i < nb && (skeep[i] != 0 || always_block(i, nb, p.local))) ? 1 : 0;
+    kn = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint64_t u = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) u |= sKm[g][r];
+      const int i = lane + WAVE * r;
+      const bool k = i < nb && (((u >> lane) & 1) || always_block(i, nb, p.local));
+      kn |= static_cast<uint64_t>(k) << r;
+      if (wave == r % G && i < p.NBC) keep[i] = k ? 1 : 0;
+    }
+    for (int i = WAVE * R + tid; i < p.NBC; i += G * WAVE) keep[i] = 0;
   }
-  // Attended log-sum-exp for the next step (every head), over the (new) stored set + always.
+  // Attended log-sum-exp for the next step (every head): the stored set + sink + local.
   float m2 = NEG_INF, s2 = 0.f;
-  for (int i = lane; i < nb; i += WAVE) {
-    const bool k = tr ? (skeep[i] != 0) : (keep[i] != 0);
-    if (k || always_block(i, nb, p.local)) lse_push(m2, s2, x[i]);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = lane + WAVE * r;
+    if (i < nb && (((kn >> r) & 1) || always_block(i, nb, p.local))) lse_push(m2, s2, x[r]);
   }
-  lse_merge_wave(m2, s2);
+  lse_wave(m2, s2);
   if (lane == 0) p.lse_att[hrow] = s2 > 0.f ? m2 + __logf(s2) : NEG_INF;
 }
 
@@ -347,15 +466,21 @@ hipError_t launch_plan_t(const kvskip_plan_args& p, hipStream_t s) {
 template <int G>
 hipError_t launch_update_t(const kvskip_update_args& p, hipStream_t s) {
   const int nb = (p.T + BLK - 1) / BLK;
-  const size_t smem = static_cast<size_t>(G) * nb * sizeof(float) + nb;
-  hipLaunchKernelGGL((update_kernel<G>), dim3(p.Hkv, p.B), dim3(G * WAVE), smem, s, p);
+  const dim3 grid(p.Hkv, p.B), blk(G * WAVE);
+  if (nb <= 2 * WAVE) hipLaunchKernelGGL((update_kernel<G, 2>), grid, blk, 0, s, p);
+  else if (nb <= 4 * WAVE) hipLaunchKernelGGL((update_kernel<G, 4>), grid, blk, 0, s, p);
+  else if (nb <= 8 * WAVE) hipLaunchKernelGGL((update_kernel<G, 8>), grid, blk, 0, s, p);
+  else if (nb <= 16 * WAVE) hipLaunchKernelGGL((update_kernel<G, 16>), grid, blk, 0, s, p);
+  else if (nb <= 32 * WAVE) hipLaunchKernelGGL((update_kernel<G, 32>), grid, blk, 0, s, p);
+  else if (nb <= 64 * WAVE) hipLaunchKernelGGL((update_kernel<G, 64>), grid, blk, 0, s, p);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 }  // namespace
 
-// LDS of update: G * nb floats + nb bytes, within 64 KiB.
-int planner_max_blocks(int G) { return (64 * 1024) / (4 * G + 1); }
+// Blocks per head the planner kernels hold (plan: LDS flags; update: registers), any G.
+int planner_max_blocks(int) { return MAX_NB; }
 
 hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s) {
   const int G = p.Hq / p.Hkv;

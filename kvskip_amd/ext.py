@@ -5,8 +5,8 @@ kernels/kvskip_ext.cpp:327-351 (decode, pv, vskip1, plan, update, read_bw). Outp
 with torch on the inputs' device; launches go to torch's current stream; nothing synchronises.
 Absent outputs are returned as None (the reference returns undefined tensors).
 
-Two extra operators (block_sums, token_index) expose the device-side planner initialisation and
-token index; they have no counterpart in kvskip_ext.
+Extra operators with no counterpart in kvskip_ext: block_sums and token_index (the device-side
+planner initialisation and token index) and decode_into (decode into caller-owned buffers).
 """
 
 from __future__ import annotations
@@ -95,7 +95,6 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     _require(load_v or stats, "load_v=false only makes sense with stats=true")
     _require(not write_p or stats, "write_p needs stats=true")
     _require(stages in (2, 3), "kvskip: unsupported head dim / stages")
-    masked = block_idx is not None
     nb = (T + TILE - 1) // TILE
     dev = q.device
     f32 = dict(dtype=torch.float32, device=dev)
@@ -111,8 +110,47 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     if num_splits > 1:
         part_acc = torch.empty(B, Hq, num_splits, D, **f32) if load_v else None
         part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
+    _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
+                   pbuf, part_acc, part_ml)
+    return [out, lse, bmax, bsum, out32, pbuf]
+
+
+def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1):
+    """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
+    out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
+    [B, Hq, nb] over the blocks read only: no -inf / 0 fill) and part_acc / part_ml fp32
+    (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way."""
+    check_q(q)
+    check_kv(k, "k")
+    check_kv(v, "v")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    _require(1 <= num_splits <= 256, "num_splits in 1..256")
+    nb = (T + TILE - 1) // TILE
+    out, lse = bufs["out"], bufs["lse"]
+    _require(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() >= B * Hq * D, "bufs: out")
+    _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() >= B * Hq, "bufs: lse")
+    bmax = bsum = part_acc = part_ml = None
+    if stats:
+        bmax, bsum = bufs["blk_max"], bufs["blk_sum"]
+        for t in (bmax, bsum):
+            _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= B * Hq * nb, "bufs: stats")
+    if num_splits > 1:
+        part_acc, part_ml = bufs["part_acc"], bufs["part_ml"]
+        _require(part_acc.dtype == torch.float32 and part_acc.is_contiguous()
+                 and part_acc.numel() >= B * Hq * num_splits * D, "bufs: part_acc")
+        _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
+                 and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
+    _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
+                   part_acc, part_ml)
+
+
+def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
+                   pbuf, part_acc, part_ml):
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
-    if masked:
+    if block_idx is not None:
         _require(block_cnt is not None, "block_cnt is required with block_idx")
         bi, bc = block_idx, block_cnt
         _require(bi.is_cuda and bi.dtype == torch.int32 and bi.dim() == 3 and bi.is_contiguous()
@@ -125,9 +163,9 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     a.out, a.out_f32, a.lse = _ptr(out), _ptr(out32), lse.data_ptr()
     a.blk_max, a.blk_sum = _ptr(bmax), _ptr(bsum)
     a.p_out = _ptr(pbuf)
+    dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode(ctypes.byref(a), int(bool(stats)), int(bool(load_v)), _stream(dev)))
-    return [out, lse, bmax, bsum, out32, pbuf]
 
 
 def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
@@ -252,8 +290,13 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
 
 
 def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
-           est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0):
-    """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place."""
+           est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0,
+           list_stats=False):
+    """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place.
+
+    list_stats (not in the reference): blk_max / blk_sum hold values only for the blocks of this
+    step's plan (the masked pass ran on unfilled buffers); the kernel derives the read set from
+    trig, keep, flags and idx and ignores the rest. Needs flags (and idx if the plan had one)."""
     check_f32(blk_max, "blk_max")
     check_f32(blk_sum, "blk_sum")
     B, Hkv, NBC = keep.shape
@@ -265,6 +308,15 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
     p.keep, p.lse_ref, p.cs_ref, p.lse_att = keep.data_ptr(), lse_ref.data_ptr(), cs_ref.data_ptr(), lse_att.data_ptr()
     p.B, p.Hq, p.Hkv, p.T, p.NBC, p.local = B, Hq, Hkv, int(T), NBC, int(local)
     p.level = float(level)
+
+    def set_flags_idx():
+        _require(flags.is_cuda and flags.dtype == torch.int32 and flags.numel() == Hkv, "flags: int32 [Hkv]")
+        p.flags = flags.data_ptr()
+        if idx is not None:
+            _require(idx.is_cuda and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[0] == B
+                     and idx.shape[1] == NBC, "idx: contiguous uint8 [B, NBC]")
+            p.idx = idx.data_ptr()
+
     if calib is not None:
         _require(flags is not None and est is not None, "calibration needs flags and est")
         _require(flags.is_cuda and flags.dtype == torch.int32 and flags.numel() == Hkv, "flags: int32 [Hkv]")
@@ -278,10 +330,11 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
                      "aix: contiguous uint8 [B, Hkv]")
             _require(idx is not None, "aix needs idx")
             p.aix, p.aix_thr = aix.data_ptr(), float(aix_thr)
-        if idx is not None:
-            _require(idx.is_cuda and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[0] == B
-                     and idx.shape[1] == NBC, "idx: contiguous uint8 [B, NBC]")
-            p.idx = idx.data_ptr()
+        set_flags_idx()
+    if list_stats:
+        _require(flags is not None, "list_stats needs flags")
+        set_flags_idx()
+        p.list_stats = 1
     dev = keep.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_update(ctypes.byref(p), _stream(dev)))

@@ -4,8 +4,10 @@ device too (the reference runs its Python planner for it, src/kvskip_attn.py:445
 
 Per decode step: plan (estimate, refresh decision, block list) -> masked + block-statistics
 attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
-Three kernel launches (+ two fills of the statistics outputs) per layer-step, all on the current
-stream, no host synchronisation.
+Three kernel launches per layer-step (four with the split merge), all on the current stream, no
+host synchronisation, no allocation after the first step of a capacity: the pass writes into
+buffers the planner owns, and its statistics need no -inf / 0 fill because update reads only
+the blocks the plan listed (list_stats).
 
 The policy fields follow KvskipConfig (src/kvskip_attn.py:116-147) for one layer.
 """
@@ -66,12 +68,14 @@ class FusedPlanner:
     its step. Usage: out = p.first(q, k, v, scale) on the first decode step, then
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
-    def __init__(self, policy: Policy):
+    def __init__(self, policy: Policy, count: bool = True):
         self.policy = policy
         self.state = None
         self.t = 0
         self.T = 0
+        self.count = count          # per-step counters as device tensors (off under graph capture)
         self.counters = {}
+        self.bufs = None
 
     # -- state
     def _alloc(self, q, k, NBC):
@@ -110,8 +114,29 @@ class FusedPlanner:
         self.state["idx"] = idx
         self.NBC = NBC
 
+    def _attend(self, q, k, v, scale, nb):
+        """Masked + statistics pass over the plan's lists into the planner's buffers. Returns
+        out [B, Hq, D] (valid until the next step) and the [B, Hq, nb] statistics views."""
+        B, Hq, D = q.shape
+        Hkv = k.shape[1]
+        S = K.num_splits_for(B * Hkv, nb)
+        n_st, n_part = B * Hq * self.NBC, B * Hq * S * D
+        b = self.bufs
+        if b is None or b["blk_max"].numel() < n_st or b["part_acc"].numel() < n_part or b["out"].shape != q.shape:
+            dev = q.device
+            f32 = dict(dtype=torch.float32, device=dev)
+            b = self.bufs = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
+                                 lse=torch.empty(B, Hq, **f32), blk_max=torch.empty(n_st, **f32),
+                                 blk_sum=torch.empty(n_st, **f32), part_acc=torch.empty(n_part, **f32),
+                                 part_ml=torch.empty(B * Hq * S * 2, **f32))
+        s = self.state
+        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S)
+        n = B * Hq * nb
+        return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
+
     def _count(self, key, value):
-        self.counters[key] = self.counters.get(key, 0) + value
+        if self.count:
+            self.counters[key] = self.counters.get(key, 0) + value
 
     def _set_idx(self, idx, ids, T):
         """This step's token-index blocks into state['idx'] ([B, NBC] uint8): from idx (bool / uint8
@@ -120,6 +145,8 @@ class FusedPlanner:
         nb = math.ceil(T / TILE)
         if ids is not None:
             E.token_index(ids, T, self.NBC, out=s["idx"])
+        elif idx is not None and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[1] == self.NBC:
+            return idx                                               # a ready [B, NBC] device buffer
         elif idx is not None:
             s["idx"].zero_()
             s["idx"][:, :nb] = idx[:, :nb].to(torch.uint8)
@@ -145,19 +172,19 @@ class FusedPlanner:
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
                int(pol.local), False)
-        r = K.decode(q, k, v, scale, plan=K.Plan(s["block_idx"], s["block_cnt"], nb, nb), stats=True)
-        E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
-                 s["lse_att"], T, float(pol.level), int(pol.local))
+        out, bmax, bsum = self._attend(q, k, v, scale, nb)
+        E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
+                 float(pol.level), int(pol.local), every, list_stats=True)
         self.t, self.T = 0, T
         self._count("dense_heads", B * Hkv)
         self._count("blocks_read", B * Hkv * nb)
         self._count("blocks_total", B * Hkv * nb)
-        return r["out"]
+        return out
 
     def step(self, q, k, v, scale, idx=None, ids=None):
         """One later decode step (src/kvskip_attn.py:451-478): plan -> masked + stats attention ->
-        update. idx: this step's token-index blocks (bool [B, >= nb]) or ids: token ids [B, >= T] int32
-        (index heads / auto index only)."""
+        update. idx: this step's token-index blocks (bool [B, >= nb], or a uint8 [B, NBC] device
+        buffer used as is) or ids: token ids [B, >= T] int32 (index heads / auto index only)."""
         if self.state is None:
             return self.first(q, k, v, scale)
         if q.dim() == 4:
@@ -181,16 +208,17 @@ class FusedPlanner:
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
                int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
                cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None)
-        r = K.decode(q, k, v, scale, plan=K.Plan(s["block_idx"], s["block_cnt"], nb, nb), stats=True)
-        E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
-                 s["lse_att"], T, float(pol.level), int(pol.local), s["flags"], ix, s["est"],
-                 s["calib"] if cal else None, float(pol.calib or 0.0), bool(pol.calib_free), kind,
-                 s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0))
+        out, bmax, bsum = self._attend(q, k, v, scale, nb)
+        E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
+                 float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
+                 float(pol.calib or 0.0), bool(pol.calib_free), kind,
+                 s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0),
+                 list_stats=True)
         self._count("blocks_read", s["block_cnt"].sum())
         self._count("blocks_total", B * Hkv * nb)
         self._count("masked_heads", B * Hkv)
         self._count("dense_heads", s["trig"].sum())
-        return r["out"]
+        return out
 
     def read_mask(self, nb):
         """Blocks read this step per (b, KV head): bool [B, Hkv, nb] (host-side view for checks)."""

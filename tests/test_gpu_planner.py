@@ -70,11 +70,14 @@ def _agree(dev, ref, margin, what):
     return n_border
 
 
-@pytest.mark.parametrize("G,D", [(4, 128), (7, 128), (4, 64)])
-def test_plan_update_kernels(gpu, G, D):
-    """One plan and one update launch each on identical inputs, after a device initialisation."""
-    run = W.planner_run(layers=1, B=2, Hq=4 * G, Hkv=4, D=D, T0=3000, steps=8, seed=21 + G)
-    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), dense_heads=(3,))
+@pytest.mark.parametrize("G,D,B,Hkv,T0", [(4, 128, 2, 4, 3000), (7, 128, 2, 4, 3000), (4, 64, 2, 4, 3000),
+                                          (2, 64, 1, 4, 10000), (1, 128, 1, 4, 20000), (7, 128, 1, 2, 40000),
+                                          (4, 128, 1, 2, 70000), (8, 64, 1, 2, 140000)])
+def test_plan_update_kernels(gpu, G, D, B, Hkv, T0):
+    """One plan and one update launch each on identical inputs, after a device initialisation
+    (contexts from 4 to 2189 blocks: every register tiling of update)."""
+    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=T0, steps=8, seed=21 + G)
+    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), dense_heads=(Hkv - 1,))
     qp = W.QueryProcess(run, 0, p_jump=0.3)
     k, v = run.k[0].cuda(), run.v[0].cuda()
     fp = FusedPlanner(dpolicy(pol))
@@ -105,9 +108,21 @@ def test_plan_update_kernels(gpu, G, D):
         logw = O.block_logw(r["blk_max"].double().cpu(), r["blk_sum"].double().cpu())
         st_u = _state_to_oracle(fp, G, run.scale, T, nb_ref=O.nblocks(T))
         pr_u = dict(pr, trig=trig)
+        # list_stats: the same update on stats that hold NaN wherever the pass read nothing must
+        # leave bit-identical state (the fused loop skips the -inf / 0 fill this way)
+        mut = ("keep", "lse_ref", "cs_ref", "lse_att", "calib")
+        alt = {key: s[key].clone() for key in mut}
+        unread = r["blk_sum"] == 0
+        bmax_nan = r["blk_max"].masked_fill(unread, math.nan)
+        bsum_nan = r["blk_sum"].masked_fill(unread, math.nan)
+        E.update(bmax_nan, bsum_nan, s["trig"], s["cs_now"], alt["keep"], alt["lse_ref"], alt["cs_ref"],
+                 alt["lse_att"], T, pol.level, pol.local, s["flags"], None, s["est"], alt["calib"], pol.calib,
+                 pol.calib_free, OP.KINDS[pol.calib_kind], None, 0.0, list_stats=True)
         E.update(r["blk_max"], r["blk_sum"], s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"],
                  s["lse_att"], T, pol.level, pol.local, s["flags"], None, s["est"], s["calib"], pol.calib,
                  pol.calib_free, OP.KINDS[pol.calib_kind], None, 0.0)
+        for key in mut:
+            assert torch.equal(alt[key], s[key]), f"list_stats changed {key}"
         pr_u["miss"] = s["est"].double().cpu()
         pr_u["cs"] = s["cs_now"][:, :, :nb].double().cpu()
         OP.update(st_u, pr_u, logw, pol)
@@ -157,11 +172,13 @@ def _run_loop(pol: OP.Policy, G=4, D=128, B=1, Hkv=8, T0=4096, steps=40, seed=4,
         stats["read"] += int(read_r.sum())
         stats["total"] += read_r.numel()
         hq = same.repeat_interleave(G, 1)
-        num = (out_d.float().cpu().double() - out_r).norm(dim=-1)
-        den = out_r.norm(dim=-1).clamp_min(1e-12)
-        stats["max_err"] = max(stats["max_err"], float((num / den)[hq].max()) if bool(hq.any()) else 0.0)
+        if bool(hq.any()):       # rel. L2 error over the heads whose read sets agree (bench/harness.py:134)
+            stats["max_err"] = max(stats["max_err"], O.rel_err(out_d.float().cpu()[hq], out_r[hq]))
         if pol.calib is not None:
-            assert (fp.state["calib"].double().cpu() - st.calib).abs().max().item() <= 1e-4
+            # the log-odds kind differentiates logit() near its clamp, where fp32 estimates of a
+            # ~1e-4 mass move it by ~1e-3 (the reference's own bar is 0.05, bench/test_planner.py:122)
+            tol = 2e-3 if pol.calib_kind == "logit" else 1e-4
+            assert (fp.state["calib"].double().cpu() - st.calib).abs().max().item() <= tol
         if pol.calib_auto_ix is not None:
             assert torch.equal(fp.state["aix"].bool().cpu(), st.aix)
     print(f"{pol}: identical read sets on {stats['same']}/{stats['head_steps']} head-steps "
