@@ -247,6 +247,11 @@ def main():
     # ---- config 4: 32-layer decode loop with the device-side planner (stage-4 policy, layer 0 dense)
     if not args.no_planner:
         res["planner_cfg4"] = bench_planner(dev, layers=args.planner_layers, T0=32768, steps=args.planner_steps)
+        # the same loop with queries that revert to their planted direction between jumps:
+        # attention stays on the planted blocks, so the policy skips most of the cache
+        res["planner_cfg4_focused"] = bench_planner(dev, layers=args.planner_layers, T0=32768,
+                                                    steps=min(args.planner_steps, 64), revert=True,
+                                                    tag="cfg4-focused")
         torch.cuda.empty_cache()
 
     roof = {"bound": "hbm", "achieved": res["dense"]["GBs_event_median"], "peak": PEAK_GBS, "unit": "GB/s",
@@ -273,7 +278,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
+def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4"):
     """Config 4: `layers` Llama-3.1-8B attention layers, `steps` decode steps from T0 (one token
     appended per step), query drift + jumps, stage-4 policy (delta 0.05, max age 32, calibration
     0.05 peak, warm-up (32, 8), token-index latch at 0.1; reproduce/04-tails.sh:16,63-69), layer 0
@@ -291,7 +296,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
     run = W.planner_run(layers=layers, T0=T0, steps=steps, seed=4, device=dev)
     B, Hkv, _, D = run.k[0].shape
     Hq = run.q0[0].shape[1]
-    qps = [W.QueryProcess(run, l) for l in range(layers)]
+    qps = [W.QueryProcess(run, l, noise=noise, revert=revert) for l in range(layers)]
     qs = torch.stack([torch.stack([qps[l].next() for l in range(layers)]) for _ in range(steps)]).to(dev)
     NBC = math.ceil((T0 + 1) / 64) + 64
     idx_all = torch.zeros(steps, B, NBC, dtype=torch.uint8, device=dev)
@@ -299,7 +304,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
     for t in range(steps):
         E.token_index(ids, T0 + t + 1, NBC, out=idx_all[t])
     pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
-    log(f"cfg4: {layers} layers x {steps} steps from T {T0} generated in {time.perf_counter() - t_gen:.1f} s")
+    log(f"{tag}: {layers} layers x {steps} steps from T {T0} generated in {time.perf_counter() - t_gen:.1f} s")
 
     def kv(l, T):
         return run.k[l][:, :, :T], run.v[l][:, :, :T]
@@ -328,7 +333,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
     total = sum(float(p.counters["blocks_total"]) for p in planners[1:])
     refresh = sum(float(p.counters.get("dense_heads", 0)) for p in planners[1:]) - (layers - 1) * B * Hkv
     head_steps = (layers - 1) * (steps - 1) * B * Hkv
-    log(f"cfg4 eager: blocks read {read / total:.3f}, refresh rate {refresh / head_steps:.3f}")
+    log(f"{tag} eager: blocks read {read / total:.3f}, refresh rate {refresh / head_steps:.3f}")
 
     def capture(fn_step, t0, t1):
         s = torch.cuda.Stream()
@@ -357,13 +362,13 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16):
     us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
-    out = {"layers": layers, "steps": steps, "T0": T0, "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, "
+    out = {"layers": layers, "steps": steps, "T0": T0, "query_noise": noise, "query_revert": revert, "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, "
            "warm (32, 8), auto index 0.1), layer 0 dense", "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
-    log(f"cfg4: policy {us_plan / n:.2f} us/layer-step vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), "
+    log(f"{tag}: policy {us_plan / n:.2f} us/layer-step vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), "
         f"{us_plan / (steps - 1) / 1e3:.3f} ms per 32-layer step")
     del planners, run, qs
     return out

@@ -128,9 +128,17 @@ typedef struct kvskip_plan_args {
   int32_t* block_cnt;          /* [B, Hkv] out */
   int32_t B, Hq, Hkv, T, D, NBC, local, max_age, add_token, calib_on, calib_kind;
   float scale, delta;
+  /* Optional workspace (not in the reference): >= kvskip_plan_part_floats(B, Hq, Hkv, NBC)
+   * floats. With it the centroid pass runs on ceil(nb / 32) workgroups per head and a second
+   * launch decides and compacts; NULL: one workgroup per head, one launch. Calls sharing a
+   * workspace must not overlap. */
+  float* part;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
+
+/* Floats of kvskip_plan_args.part for a state of capacity NBC blocks. */
+int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC);
 
 /* Refresh planner, after the attention pass. Replaces kvskip::UpdateParams + launch_update
  * (kernels/kvskip.h:91-111,116, kernels/kvskip_planner.cu:229-305,314-318), reached from

@@ -45,6 +45,7 @@ class PlanArgs(ctypes.Structure):
         ("NBC", c_int32), ("local", c_int32), ("max_age", c_int32), ("add_token", c_int32),
         ("calib_on", c_int32), ("calib_kind", c_int32),
         ("scale", c_float), ("delta", c_float),
+        ("part", c_void_p),
     ]
 
 
@@ -68,6 +69,7 @@ SIGNATURES = {
     "kvskip_vskip1": ([POINTER(AttnArgs), c_void_p], c_int),
     "kvskip_read": ([c_void_p, c_int64, c_void_p, c_int32, c_void_p], c_int),
     "kvskip_plan": ([POINTER(PlanArgs), c_void_p], c_int),
+    "kvskip_plan_part_floats": ([c_int32, c_int32, c_int32, c_int32], c_int64),
     "kvskip_update": ([POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_int32, c_void_p], c_int),

@@ -386,18 +386,21 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   const bool with_v = p.out != nullptr;
   __shared__ float rA[NC][32], rL[NC], rM[NC];
   float ms[U], ls[U], as[U];
-  float mloc = NEG_INF;
+  const int nu = (S + NC - 1) / NC;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int s = cls + NC * u;
-    if (s < S) {
+  for (int u = 0; u < U; ++u) {  // every load first (clamped split), one round trip
+    if (u < nu) {
+      const int s = min(cls + NC * u, S - 1);
       const float2 t = *reinterpret_cast<const float2*>(ml + 2 * s);
       ms[u] = t.x;
       ls[u] = t.y;
       as[u] = with_v ? p.part_acc[(hq * S + s) * D + d] : 0.f;
-      mloc = fmaxf(mloc, t.x);
     }
   }
+  float mloc = NEG_INF;
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (u < nu && cls + NC * u < S) mloc = fmaxf(mloc, ms[u]);
   if (dl == 0) rM[cls] = mloc;
   __syncthreads();
   float M = NEG_INF;

@@ -199,6 +199,11 @@ int kvskip_plan(const kvskip_plan_args* p, void* stream) {
   return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
 }
 
+int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC) {
+  if (B < 1 || Hkv < 1 || Hq < 1 || NBC < 1 || Hq % Hkv != 0) return -1;
+  return kvs::plan_part_floats(B, Hq, Hkv, NBC);
+}
+
 int kvskip_update(const kvskip_update_args* p, void* stream) {
   if (p == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
   if (p->blk_max == nullptr || p->blk_sum == nullptr) return fail(KVSKIP_E_INVALID, "blk_max must be contiguous CUDA fp32");

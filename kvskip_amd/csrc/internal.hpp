@@ -63,5 +63,6 @@ hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int
 
 // Largest block count the planner kernels hold in LDS for a group of G query heads.
 int planner_max_blocks(int G);
+int64_t plan_part_floats(int B, int Hq, int Hkv, int NBC);
 
 }  // namespace kvs

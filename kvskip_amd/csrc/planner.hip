@@ -258,6 +258,225 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   }
 }
 
+// ---- Two-kernel plan (with a workspace): plan_scores spreads the centroid pass of a head over
+// ceil(nb / 32) workgroups (4 wavefronts, 8 block rows each), each publishing per query head the
+// (m, s) log-sum-exp of its unattended blocks' estimates and the 32-bit mask of its attended
+// blocks; plan_decide (one wavefront per head) merges them, decides and compacts from the masks.
+// The kernel boundary publishes the partials (a last-arriving-workgroup ticket would need an
+// agent-scope release per workgroup, an L2 write-back each, which costs more than the launch).
+constexpr int WW = 4;                // wavefronts per workgroup
+constexpr int WU = 2;                // row groups (4 rows) per wavefront
+constexpr int WCB = WW * WU * 4;     // 32 blocks per workgroup
+constexpr int WNT = WW * WAVE;
+
+__host__ __device__ constexpr int part_stride(int G) { return 2 * G + 1; }  // m[G], s[G], mask
+
+template <int D, int G>
+__global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args p) {
+  constexpr int DL = D / 16, DW = DL / 4, SP = part_stride(G);
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, C = gridDim.x;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int nb = (p.T + BLK - 1) / BLK;
+  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;
+  float* csum = p.csum + bh * p.NBC * D;
+  const uint8_t* keep = p.keep + bh * p.NBC;
+  const int fl = p.flags[h];
+  const bool ixh = (fl & 2) != 0;  // token-index head: index + sink + local, no estimate
+  const bool ax = p.aix != nullptr && p.aix[bh] != 0;
+  const bool uni = p.idx != nullptr && ((fl & 4) || ax);
+  const uint8_t* idx = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
+  const bool use_idx = p.idx != nullptr && (ixh || uni);
+  __shared__ float sM[WW][G], sS[WW][G];
+  __shared__ uint32_t sMask[WW];
+
+  // Every load is issued without waiting for the flags (an index head's extra loads are unused).
+  const int rs = lane >> 4, c16 = lane & 15, gl = min(c16, G - 1);
+  float qf[G][DL];
+  uint2 kx[DW];
+  {
+    const uint16_t* q = reinterpret_cast<const uint16_t*>(p.q);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint16_t* qp = q + b * p.q_sb + (static_cast<int64_t>(h) * G + g) * p.q_sh;
+#pragma unroll
+      for (int w = 0; w < DW; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
+    }
+    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
+                         static_cast<int64_t>(p.T - 1) * p.k_st;
+#pragma unroll
+    for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
+  }
+  const bool add = p.add_token != 0 && !ixh;
+
+  const int base = c * WCB + wave * (4 * WU);
+  float cv[WU][DL], lr[WU], cr[WU];
+  uint32_t kb[WU], ib[WU];
+#pragma unroll
+  for (int u = 0; u < WU; ++u) {  // every load of the pass first
+    const int rc = min(base + 4 * u + rs, nb - 1);
+    {
+      const float* cp = csum + static_cast<int64_t>(rc) * D;
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const float4 t = *reinterpret_cast<const float4*>(cp + 64 * w + 4 * c16);
+        cv[u][4 * w] = t.x;
+        cv[u][4 * w + 1] = t.y;
+        cv[u][4 * w + 2] = t.z;
+        cv[u][4 * w + 3] = t.w;
+      }
+      const int64_t r = row0 + static_cast<int64_t>(gl) * p.NBC + rc;
+      lr[u] = p.lse_ref[r];
+      cr[u] = p.cs_ref[r];
+    }
+    kb[u] = keep[rc];
+    ib[u] = idx[rc];
+  }
+  float em = NEG_INF, es = 0.f;
+  uint32_t wmask = 0;  // attended blocks of this wavefront: bit 4 u + rs
+#pragma unroll
+  for (int u = 0; u < WU; ++u) {
+    const int blk = base + 4 * u + rs;
+    const bool in = blk < nb, al = always_block(blk, nb, p.local);
+    const bool a = in && (ixh ? (use_idx && ib[u] != 0) || al : kb[u] != 0 || al || (uni && ib[u] != 0));
+    const uint64_t bal = __ballot(c16 == 0 && a);
+    wmask |= static_cast<uint32_t>(((bal >> 0) & 1) | (((bal >> 16) & 1) << 1) | (((bal >> 32) & 1) << 2) |
+                                   (((bal >> 48) & 1) << 3)) << (4 * u);
+    if (ixh) continue;
+    if (add && blk == nb - 1) {
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        cv[u][4 * w] += bf_lo(kx[w].x);
+        cv[u][4 * w + 1] += bf_hi(kx[w].x);
+        cv[u][4 * w + 2] += bf_lo(kx[w].y);
+        cv[u][4 * w + 3] += bf_hi(kx[w].y);
+        *reinterpret_cast<float4*>(csum + static_cast<int64_t>(blk) * D + 64 * w + 4 * c16) =
+            make_float4(cv[u][4 * w], cv[u][4 * w + 1], cv[u][4 * w + 2], cv[u][4 * w + 3]);
+      }
+    }
+    const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? p.T - blk * BLK : BLK);
+    float mine = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < DL; ++j) d = fmaf(qf[g][j], cv[u][j], d);
+      d += dpp<DPP_XOR1>(d);
+      d += dpp<DPP_XOR2>(d);
+      d += dpp<DPP_HALF_MIRROR>(d);
+      d += dpp<DPP_MIRROR>(d);
+      if (c16 == g) mine = d * inv_n;
+    }
+    if (in && c16 < G) {
+      p.cs_now[row0 + static_cast<int64_t>(c16) * p.NBC + blk] = mine;
+      if (!a) lse_push(em, es, lr[u] + mine - cr[u]);
+    }
+  }
+#pragma unroll
+  for (int o = 16; o < WAVE; o <<= 1) {
+    const float m2 = __shfl_xor(em, o, WAVE), s2 = __shfl_xor(es, o, WAVE);
+    lse_merge(em, es, m2, s2);
+  }
+  if (rs == 0 && c16 < G) {
+    sM[wave][c16] = em;
+    sS[wave][c16] = es;
+  }
+  if (lane == 0) sMask[wave] = wmask;
+  __syncthreads();
+  float* part = p.part + (bh * C + c) * SP;
+  if (wave == 0 && lane < G) {
+    float m = NEG_INF, sv = 0.f;
+#pragma unroll
+    for (int w = 0; w < WW; ++w) lse_merge(m, sv, sM[w][lane], sS[w][lane]);
+    part[lane] = m;
+    part[G + lane] = sv;
+  }
+  if (tid == 0) {
+    uint32_t mk = 0;
+#pragma unroll
+    for (int w = 0; w < WW; ++w) mk |= sMask[w] << (8 * w);
+    part[2 * G] = __uint_as_float(mk);
+  }
+}
+
+// One wavefront per (b, KV head): merge the C = ceil(nb / 32) partials (lane l: chunks l, l + 64,
+// ...), decide, and compact the list from the chunk masks (prefix over lanes, ascending).
+template <int G>
+__global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
+  constexpr int SP = part_stride(G);
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int nb = (p.T + BLK - 1) / BLK, C = (nb + WCB - 1) / WCB;
+  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  const int fl = p.flags[h];
+  const float* pb = p.part + bh * C * SP;
+  int* bi = p.block_idx + bh * p.NBC;
+  const int age0 = p.age[bh];
+  const float cal0 = (p.calib != nullptr && p.calib_on) ? p.calib[bh] : 0.f;
+  const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + min(lane, G - 1)];
+  constexpr int CL = MAX_NB / WCB / WAVE;  // chunks per lane at capacity
+  float pm[CL][G], ps[CL][G];
+  uint32_t mk[CL];
+#pragma unroll
+  for (int j = 0; j < CL; ++j) {  // every partial first
+    const int cc = min(lane + WAVE * j, C - 1);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      pm[j][g] = pb[cc * SP + g];
+      ps[j][g] = pb[cc * SP + G + g];
+    }
+    mk[j] = __float_as_uint(pb[cc * SP + 2 * G]);
+  }
+  bool tr = false;
+  if (!(fl & 2)) {
+    float miss = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float m = NEG_INF, sv = 0.f;
+#pragma unroll
+      for (int j = 0; j < CL; ++j)
+        if (lane + WAVE * j < C) lse_merge(m, sv, pm[j][g], ps[j][g]);
+      lse_wave(m, sv);
+      if (sv > 0.f) miss = fmaxf(miss, 1.f / (1.f + __expf(lane_value(la, g) - (m + __logf(sv)))));
+    }
+    float dec = miss;
+    if (p.calib != nullptr && p.calib_on)
+      dec = p.calib_kind ? miss + cal0 : 1.f / (1.f + __expf(-(clamped_logit(miss) + cal0)));
+    const int a = age0 + 1;
+    tr = dec > p.delta || a >= p.max_age || (fl & 1);
+    if (lane == 0) {
+      if (p.est != nullptr) p.est[bh] = miss;
+      p.age[bh] = tr ? 0 : a;
+    }
+  }
+  if (lane == 0) p.trig[bh] = tr ? 1 : 0;
+  if (tr) {  // refresh: every block
+    for (int i = lane; i < nb; i += WAVE) bi[i] = i;
+    if (lane == 0) p.block_cnt[bh] = nb;
+    return;
+  }
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < CL; ++j) {
+    if (WAVE * j >= C) break;
+    const int cc = lane + WAVE * j;
+    const uint32_t m0 = cc < C ? mk[j] : 0u;
+    const int n = __popc(m0);
+    int incl = n;  // inclusive prefix over lanes
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int t = __shfl_up(incl, o, WAVE);
+      if (lane >= o) incl += t;
+    }
+    int off = base + incl - n;
+    for (uint32_t m = m0; m != 0; m &= m - 1) bi[off++] = cc * WCB + __ffs(m) - 1;
+    base += __shfl(incl, WAVE - 1, WAVE);
+  }
+  if (lane == 0) p.block_cnt[bh] = base;
+}
+
 // Order-preserving key of a float (larger float -> larger key).
 __device__ __forceinline__ uint32_t fkey(float y) {
   const uint32_t u = __float_as_uint(y);
@@ -459,7 +678,13 @@ __global__ void __launch_bounds__(256) token_index_kernel(const int32_t* ids, in
 
 template <int D, int G>
 hipError_t launch_plan_t(const kvskip_plan_args& p, hipStream_t s) {
-  hipLaunchKernelGGL((plan_kernel<D, G>), dim3(p.Hkv, p.B), dim3(PNT), 0, s, p);
+  if (p.part != nullptr) {
+    const int nb = (p.T + BLK - 1) / BLK;
+    hipLaunchKernelGGL((plan_scores_kernel<D, G>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p);
+    hipLaunchKernelGGL((plan_decide_kernel<G>), dim3(p.Hkv, p.B), dim3(WAVE), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((plan_kernel<D, G>), dim3(p.Hkv, p.B), dim3(PNT), 0, s, p);
+  }
   return hipGetLastError();
 }
 
@@ -481,6 +706,11 @@ hipError_t launch_update_t(const kvskip_update_args& p, hipStream_t s) {
 
 // Blocks per head the planner kernels hold (plan: LDS flags; update: registers), any G.
 int planner_max_blocks(int) { return MAX_NB; }
+
+int64_t plan_part_floats(int B, int Hq, int Hkv, int NBC) {
+  const int G = Hq / Hkv;
+  return static_cast<int64_t>(B) * Hkv * ((NBC + WCB - 1) / WCB) * part_stride(G);
+}
 
 hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s) {
   const int G = p.Hq / p.Hkv;

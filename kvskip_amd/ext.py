@@ -239,8 +239,12 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
-         max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None):
-    """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place."""
+         max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
+         part=None):
+    """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
+
+    part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
+    centroid pass is spread over all compute units (two launches instead of one)."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
@@ -284,9 +288,18 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     p.B, p.Hq, p.Hkv, p.T, p.D, p.NBC = B, Hq, Hkv, T, D, NBC
     p.local, p.max_age, p.add_token = int(local), int(max_age), int(bool(add_token))
     p.scale, p.delta = float(scale), float(delta)
+    if part is not None:
+        check_f32(part, "part")
+        _require(part.numel() >= plan_part_floats(B, Hq, Hkv, NBC), "part: too small")
+        p.part = part.data_ptr()
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
+
+
+def plan_part_floats(B, Hq, Hkv, NBC) -> int:
+    """fp32 elements of plan()'s `part` workspace for a state of capacity NBC blocks."""
+    return int(_native.lib().kvskip_plan_part_floats(int(B), int(Hq), int(Hkv), int(NBC)))
 
 
 def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,

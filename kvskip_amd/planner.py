@@ -100,6 +100,7 @@ class FusedPlanner:
             est=torch.zeros(B, Hkv, **f32),
             aix=torch.zeros(B, Hkv, dtype=torch.uint8, device=dev),
             idx=torch.zeros(B, NBC, dtype=torch.uint8, device=dev),
+            part=torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), **f32),     # multi-workgroup plan
         )
 
     def _grow(self, NBC):
@@ -112,6 +113,9 @@ class FusedPlanner:
             self.state[key] = out
         idx = torch.zeros(self.state["idx"].shape[0], NBC, dtype=torch.uint8, device=self.state["idx"].device)
         self.state["idx"] = idx
+        B, Hq = self.state["lse_att"].shape
+        Hkv = self.state["keep"].shape[1]
+        self.state["part"] = torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), dtype=torch.float32, device=idx.device)
         self.NBC = NBC
 
     def _attend(self, q, k, v, scale, nb):
@@ -171,7 +175,7 @@ class FusedPlanner:
         pol = self.policy
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
-               int(pol.local), False)
+               int(pol.local), False, part=s["part"])
         out, bmax, bsum = self._attend(q, k, v, scale, nb)
         E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
                  float(pol.level), int(pol.local), every, list_stats=True)
@@ -207,17 +211,19 @@ class FusedPlanner:
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"], s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
                int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
-               cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None)
+               cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None,
+               part=s["part"])
         out, bmax, bsum = self._attend(q, k, v, scale, nb)
         E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
                  float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
                  float(pol.calib or 0.0), bool(pol.calib_free), kind,
                  s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0),
                  list_stats=True)
-        self._count("blocks_read", s["block_cnt"].sum())
-        self._count("blocks_total", B * Hkv * nb)
-        self._count("masked_heads", B * Hkv)
-        self._count("dense_heads", s["trig"].sum())
+        if self.count:
+            self._count("blocks_read", s["block_cnt"].sum())
+            self._count("blocks_total", B * Hkv * nb)
+            self._count("masked_heads", B * Hkv)
+            self._count("dense_heads", s["trig"].sum())
         return out
 
     def read_mask(self, nb):

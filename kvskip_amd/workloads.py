@@ -221,26 +221,36 @@ def planner_run(layers=32, B=1, Hq=32, Hkv=8, D=128, T0=32768, steps=128, seed=4
 
 
 class QueryProcess:
-    """q_t = 0.97 q_{t-1} + 0.25 N(0, 1); with probability p_jump per query head and step the head
-    re-aims at another planted set: q = alpha u_new + 0.25 N(0, 1). Seeded, on the CPU."""
+    """q_t = 0.97 q_{t-1} + noise N(0, 1) (noise 0.25: config 4); with probability p_jump per query
+    head and step the head re-aims at another planted set: q = alpha u_new + noise N(0, 1).
+    revert=True: q_t = m + 0.97 (q_{t-1} - m) + noise N(0, 1) with m = alpha u_aim, so the query
+    stays on its planted set between jumps instead of decaying towards 0 (whose flat softmax puts
+    the 99% set over most of the cache). Seeded, on the CPU."""
 
-    def __init__(self, run: PlannerRun, layer: int, p_jump=0.03, seed=None):
-        self.run, self.layer, self.p = run, layer, p_jump
+    def __init__(self, run: PlannerRun, layer: int, p_jump=0.03, seed=None, noise=0.25, revert=False):
+        self.run, self.layer, self.p, self.noise, self.revert = run, layer, p_jump, noise, revert
         self.g = torch.Generator().manual_seed(run.seed * 1000 + layer if seed is None else seed)
         self.q = run.q0[layer].detach().float().cpu().clone()
         self.aim = run.aim[layer].cpu().clone()
         self.u = run.dirs[layer].float().cpu()
+
+    def _aimed(self, G):
+        B, Hq, D = self.q.shape
+        return torch.gather(self.u.repeat_interleave(G, dim=1), 2, self.aim[..., None, None].expand(B, Hq, 1, D))[:, :, 0]
 
     def next(self) -> torch.Tensor:
         B, Hq, D = self.q.shape
         Hkv, n_sets = self.u.shape[1], self.u.shape[2]
         G = Hq // Hkv
         eps = torch.randn(B, Hq, D, generator=self.g)
-        self.q = 0.97 * self.q + 0.25 * eps
+        if self.revert:
+            m = self.run.alpha * self._aimed(G)
+            self.q = m + 0.97 * (self.q - m) + self.noise * eps
+        else:
+            self.q = 0.97 * self.q + self.noise * eps
         jump = torch.rand(B, Hq, generator=self.g) < self.p
         if bool(jump.any()):
             new = (self.aim + 1 + torch.randint(0, n_sets - 1, (B, Hq), generator=self.g)) % n_sets
             self.aim = torch.where(jump, new, self.aim)
-            uu = torch.gather(self.u.repeat_interleave(G, dim=1), 2, self.aim[..., None, None].expand(B, Hq, 1, D))[:, :, 0]
-            self.q = torch.where(jump[..., None], self.run.alpha * uu + 0.25 * eps, self.q)
+            self.q = torch.where(jump[..., None], self.run.alpha * self._aimed(G) + self.noise * eps, self.q)
         return self.q.to(torch.bfloat16)

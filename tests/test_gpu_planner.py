@@ -92,9 +92,22 @@ def test_plan_update_kernels(gpu, G, D, B, Hkv, T0):
         pr = OP.plan(st, q, k[:, :, :T].cpu(), pol)
         s = fp.state
         qd = q.cuda()
+        # the multi-workgroup plan on a copy of the state, then the one-workgroup plan on the state
+        wide = {key: s[key].clone() for key in ("csum", "age", "cs_now", "trig", "block_idx", "block_cnt", "est")}
+        E.plan(qd, k[:, :, :T], wide["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], wide["age"],
+               s["flags"], wide["cs_now"], wide["trig"], wide["block_idx"], wide["block_cnt"], run.scale, pol.delta,
+               OP.max_age_at(pol, step), pol.local, True, None, s["calib"], wide["est"], True,
+               OP.KINDS[pol.calib_kind], None, part=s["part"])
         E.plan(qd, k[:, :, :T], s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"],
                s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], run.scale, pol.delta, OP.max_age_at(pol, step),
                pol.local, True, None, s["calib"], s["est"], True, OP.KINDS[pol.calib_kind], None)
+        for key in ("csum", "cs_now", "trig", "block_cnt", "age"):       # same arithmetic per row
+            assert torch.equal(wide[key], s[key]), f"wide plan: {key}"
+        for bb in range(B):
+            for hh in range(Hkv):
+                n = int(s["block_cnt"][bb, hh])
+                assert torch.equal(wide["block_idx"][bb, hh, :n], s["block_idx"][bb, hh, :n]), "wide plan: list"
+        assert (wide["est"] - s["est"]).abs().max().item() <= 1e-6    # merge order of the partials
         fp.t, fp.T = step, T
         trig = s["trig"].bool().cpu()
         nbord = _agree(trig, pr["trig"], pr["margin"], "refresh decision")
