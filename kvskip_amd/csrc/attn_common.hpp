@@ -372,35 +372,32 @@ __device__ __forceinline__ void qk_block_mf(float (&s)[4][4], const u32x4 (&kr)[
 }
 
 // Split merge: workgroup (b*Hq + hq, 32-dim slice), 256 threads = 8 split classes x 32 dims.
-// Thread (cls, d) loads the partials of splits s = cls (mod 8) in one round trip, the classes
-// agree on the max through LDS, then weight (2^(m_s - M), log-sum-exp mode; 1, plain mode for
-// the two-pass pass 2) and add in LDS. With out == nullptr (stats-only) only lse is produced.
-template <int D>
+// Thread (cls, d) loads the partials of splits s = cls + 8 u, u < U (U = ceil(S / 8), a template
+// parameter so every load is unconditional, clamped to S - 1, and in flight together), the
+// classes agree on the max through LDS, then weight (2^(m_s - M), log-sum-exp mode; 1, plain
+// mode for the two-pass pass 2) and add in LDS. WITH_V = false (stats-only): only lse.
+template <int D, int U, bool WITH_V>
 __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
-  constexpr int NC = 8, U = MAX_SPLITS / NC;
+  constexpr int NC = 8;
   const int64_t hq = blockIdx.x;
   const int tid = threadIdx.x, cls = tid / 32, dl = tid % 32;
   const int d = blockIdx.y * 32 + dl;
   const int S = p.num_splits;
   const float* ml = p.part_ml + hq * S * 2;
-  const bool with_v = p.out != nullptr;
   __shared__ float rA[NC][32], rL[NC], rM[NC];
   float ms[U], ls[U], as[U];
-  const int nu = (S + NC - 1) / NC;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {  // every load first (clamped split), one round trip
-    if (u < nu) {
-      const int s = min(cls + NC * u, S - 1);
-      const float2 t = *reinterpret_cast<const float2*>(ml + 2 * s);
-      ms[u] = t.x;
-      ls[u] = t.y;
-      as[u] = with_v ? p.part_acc[(hq * S + s) * D + d] : 0.f;
-    }
+  for (int u = 0; u < U; ++u) {
+    const int s = min(cls + NC * u, S - 1);
+    const float2 t = *reinterpret_cast<const float2*>(ml + 2 * s);
+    ms[u] = t.x;
+    ls[u] = t.y;
+    if constexpr (WITH_V) as[u] = p.part_acc[(hq * S + s) * D + d];
   }
   float mloc = NEG_INF;
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (u < nu && cls + NC * u < S) mloc = fmaxf(mloc, ms[u]);
+    if (cls + NC * u < S) mloc = fmaxf(mloc, ms[u]);
   if (dl == 0) rM[cls] = mloc;
   __syncthreads();
   float M = NEG_INF;
@@ -410,11 +407,10 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   float A = 0.f, L = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int s = cls + NC * u;
-    if (s < S) {
+    if (cls + NC * u < S) {
       const float w = plain ? 1.f : fexp2(ms[u] - mu);
       L += ls[u] * w;
-      A += as[u] * w;
+      if constexpr (WITH_V) A += as[u] * w;
     }
   }
   rA[cls][dl] = A;
@@ -428,7 +424,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
       l += rL[c];
     }
     if (plain) l = 1.f;
-    if (with_v) {
+    if constexpr (WITH_V) {
       const float o = l > 0.f ? a / l : 0.f;
       p.out[hq * D + d] = f2bf(o);
       if (p.out_f32) p.out_f32[hq * D + d] = o;
@@ -437,12 +433,28 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   }
 }
 
+template <int D, bool WITH_V>
+inline void launch_combine_u(const AttnP& p, dim3 grid, int plain, hipStream_t s) {
+  const int u = (p.num_splits + 7) / 8;
+  if (u <= 1) hipLaunchKernelGGL((combine_kernel<D, 1, WITH_V>), grid, dim3(256), 0, s, p, plain);
+  else if (u <= 2) hipLaunchKernelGGL((combine_kernel<D, 2, WITH_V>), grid, dim3(256), 0, s, p, plain);
+  else if (u <= 4) hipLaunchKernelGGL((combine_kernel<D, 4, WITH_V>), grid, dim3(256), 0, s, p, plain);
+  else if (u <= 8) hipLaunchKernelGGL((combine_kernel<D, 8, WITH_V>), grid, dim3(256), 0, s, p, plain);
+  else if (u <= 16) hipLaunchKernelGGL((combine_kernel<D, 16, WITH_V>), grid, dim3(256), 0, s, p, plain);
+  else hipLaunchKernelGGL((combine_kernel<D, MAX_SPLITS / 8, WITH_V>), grid, dim3(256), 0, s, p, plain);
+}
+
 inline hipError_t launch_combine(const AttnP& p, int D, bool plain, hipStream_t s) {
-  const dim3 grid(p.B * p.Hq, p.out != nullptr ? D / 32 : 1);
-  if (D == 128)
-    hipLaunchKernelGGL((combine_kernel<128>), grid, dim3(256), 0, s, p, plain ? 1 : 0);
-  else
-    hipLaunchKernelGGL((combine_kernel<64>), grid, dim3(256), 0, s, p, plain ? 1 : 0);
+  const bool with_v = p.out != nullptr;
+  const dim3 grid(p.B * p.Hq, with_v ? D / 32 : 1);
+  const int pl = plain ? 1 : 0;
+  if (D == 128) {
+    if (with_v) launch_combine_u<128, true>(p, grid, pl, s);
+    else launch_combine_u<128, false>(p, grid, pl, s);
+  } else {
+    if (with_v) launch_combine_u<64, true>(p, grid, pl, s);
+    else launch_combine_u<64, false>(p, grid, pl, s);
+  }
   return hipGetLastError();
 }
 
