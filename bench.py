@@ -124,6 +124,8 @@ def main():
     ap.add_argument("--no-planner", action="store_true", help="skip the config-4 planner loop")
     ap.add_argument("--planner-layers", type=int, default=32)
     ap.add_argument("--planner-steps", type=int, default=128)
+    ap.add_argument("--pmc-target", action="store_true",
+                    help="profiling target only: 20 dense config-2 decodes + copy kernels of known size, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -159,6 +161,10 @@ def main():
     def dense(i):
         return E.decode(q, ks[i], vs[i], L.scale, None, None, False, True, S_dense, 2, False, False)
 
+    if args.pmc_target:
+        pmc_target(dense, dev)
+        return
+
     def masked(i):
         return E.decode(q, ks[i], vs[i], L.scale, bi, bc, True, True, S_mask, 2, False, False)
 
@@ -176,6 +182,15 @@ def main():
         res[name] = {"us_per_op_median": med, "us_per_op_mean": statistics.mean(us), "bytes": nbytes,
                      "GBs_event_median": nbytes / med / 1e3}
         log(f"{name}: event median {med:.1f} us -> {nbytes / med / 1e3:.0f} GB/s")
+
+    # ---- the dominant kernel on its own: the split pass of the dense op (HIP events around each
+    # launch on the current stream, after a cache flush), and the split merge after it
+    ops = [E.DecodeOp(q, ks[i], vs[i], L.scale, S_dense) for i in range(NCOPY)]
+    t_split, t_merge = split_merge_events(ops, args.events, flush)
+    bytes_split = 2 * B * Hkv * T * D * 2 + B * Hq * D * 2          # K + V + q, the split pass's reads
+    res["dense"].update(split_pass_us_median=t_split, merge_us_median=t_merge, split_pass_bytes=bytes_split)
+    log(f"dense split pass: {t_split:.2f} us ({bytes_split / t_split / 1e3:.0f} GB/s), merge {t_merge:.2f} us")
+    del ops
 
     # ---- timed steps (dense, the headline) and the masked path, from graphs
     el = timed_steps(dense, args.steps, args.warmup)
@@ -254,10 +269,13 @@ def main():
                                                     tag="cfg4-focused")
         torch.cuda.empty_cache()
 
-    roof = {"bound": "hbm", "achieved": res["dense"]["GBs_event_median"], "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": res["dense"]["GBs_event_median"] / PEAK_GBS, "traffic": None,
-            "kernel": "decode_kernel<128,4,dense> at config 2 (split merge in-kernel), HIP events per launch "
-                      "after a 512 MiB cache flush, median"}
+    achieved = bytes_split / t_split / 1e3
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4), "traffic": read_traffic(),
+            "kernel": f"decode_kernel<128,4,dense,mfma> (split pass, {S_dense} splits) at config 2: K+V+q bytes / "
+                      "median HIP-event duration of one launch after a 512 MiB cache flush",
+            "algorithmic_bytes": bytes_split, "us_per_launch": round(t_split, 3),
+            "read_ceiling_GBs": round(res["read_ceiling_GBs"], 1)}
 
     cpu = None
     if not args.no_cpu:
@@ -276,6 +294,63 @@ def main():
         "paths": res, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def split_merge_events(ops, n, flush):
+    """Median HIP-event durations (us) of the split pass and of the split merge of DecodeOps,
+    cycling the ops; a flush precedes every pair."""
+    import torch
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    for op in ops:
+        op.run()
+    torch.cuda.synchronize()
+    for i in range(n):
+        flush()
+        ev[i][0].record()
+        ops[i % len(ops)].splits()
+        ev[i][1].record()
+        ops[i % len(ops)].merge()
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    split = statistics.median(a.elapsed_time(b) * 1e3 for a, b, _ in ev)
+    merge = statistics.median(b.elapsed_time(c) * 1e3 for _, b, c in ev)
+    return split, merge
+
+
+PMC_FILE = ROOT / "profiles" / "decode_dense_cfg2_pmc.txt"
+
+
+def read_traffic():
+    """HBM bytes per launch of the dense split pass from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel factors), or None."""
+    try:
+        for line in PMC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def pmc_target(dense, dev):
+    """Profiling target for rocprofv3 --pmc: 20 dense config-2 decodes, then a 256 MiB torch copy
+    (reads and writes 256 MiB) and a 256 MiB read_bw (reads 256 MiB) 5 times each, as the known
+    sizes that scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+
+    from kvskip_amd import ext as E
+    for i in range(20):
+        dense(i % NCOPY)
+    a = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    o = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(5):
+        b.copy_(a)
+    for _ in range(5):
+        E.read_bw(a, o, 1024)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_target": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2}), flush=True)
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4"):

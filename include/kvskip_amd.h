@@ -61,7 +61,8 @@ typedef struct kvskip_attn_args {
   float* lse;                  /* optional [B, Hq] natural-log log-sum-exp of the attended scores */
 
   /* per-block statistics, [B, Hq, nb]: max score (natural units) and sum exp(s - max);
-   * blocks not read are left untouched (callers pre-fill -inf / 0) */
+   * every block is written, (-inf, 0) where the list skips it (the reference leaves those to a
+   * host-side fill, kernels/kvskip_ext.cpp:51-54; here the masked pass writes them) */
   float* blk_max;
   float* blk_sum;
 
@@ -84,6 +85,14 @@ typedef struct kvskip_attn_args {
  * Replaces kvskip::launch_decode (kernels/kvskip.h:113-114, kernels/kvskip_kernel.cu:761-769),
  * reached from kvskip_ext.decode (kernels/kvskip_ext.cpp:25-101). Any G = Hq / Hkv in 1..8. */
 int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream);
+
+/* kvskip_decode as its two launches (num_splits >= 2; same arguments, called in this order on
+ * one stream): the split pass into part_acc / part_ml (+ statistics), then the split merge into
+ * out / out_f32 / lse. Not in the reference (its launch_decode issues both,
+ * kernels/kvskip_kernel.cu:433-473): for timing each kernel on its own or scheduling other work
+ * between the two. */
+int kvskip_decode_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream);
+int kvskip_merge_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream);
 
 /* Two-pass V-skip, pass 2: out = sum over listed blocks of blk_scale * P . V (no softmax);
  * num_splits > 1 adds the plain sum of the partials.

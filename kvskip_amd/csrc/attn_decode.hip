@@ -5,6 +5,39 @@
 namespace kvs {
 namespace {
 
+// Masked statistics of the blocks the list skips: (-inf, 0), so the outputs need no fill. The
+// split holding list positions [i0, i0 + n) writes the gaps before each of its entries (from the
+// previous entry, or from block 0) and, if it holds the list's last entry, the tail up to nb;
+// an empty list is written by split 0. Every unlisted block falls to exactly one split.
+// Thread t < NT has the entries of position i0 + t and the one before it loaded (prev, cur).
+template <int G>
+__device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, int i0, int n, int split,
+                                int64_t hq0, int tid, int prev0, int cur0) {
+  auto put = [&](int blk) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
+      p.blk_sum[(hq0 + g) * p.nb + blk] = 0.f;
+    }
+  };
+  if (n_items == 0) {
+    if (split == 0)
+      for (int blk = tid; blk < p.nb; blk += NT) put(blk);
+    return;
+  }
+  for (int t = tid; t < n; t += NT) {
+    const int k = i0 + t;
+    const int cur = t < NT ? cur0 : list[k];
+    const int prev = t < NT ? prev0 : list[k - 1];
+    const int a = max(prev, -1) + 1, e = min(cur, p.nb);
+    for (int blk = a; blk < e; ++blk) put(blk);
+  }
+  if (n > 0 && i0 + n == n_items) {
+    const int last = min(max(list[n_items - 1], -1), p.nb - 1);
+    for (int blk = last + 1 + tid; blk < p.nb; blk += NT) put(blk);
+  }
+}
+
 template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF>
 __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   constexpr int GP = gpad<G>();
@@ -28,6 +61,13 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   const int i0 = min(n_items, split * per);
   const int n = min(n_items, i0 + per) - i0;
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
+  int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this thread's gap
+  if constexpr (MASKED && STATS) {
+    if (tid < n) {
+      gap_cur = list[i0 + tid];
+      gap_prev = i0 + tid > 0 ? list[i0 + tid - 1] : -1;
+    }
+  }
 
   const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(p.T, p.k_st, D));
   const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, LOAD_V ? head_bytes(p.T, p.v_st, D) : 0);
@@ -211,38 +251,42 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
       }
     }
   }
+  if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, tid, gap_prev, gap_cur);
   finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
 }
 
 template <int D, int G, bool M, bool ST, bool LV>
-hipError_t launch_decode_t(const AttnP& p, bool mf, hipStream_t s) {
-  if (mf)
-    hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true>), attn_grid(p), dim3(NT), 0, s, p);
-  else
-    hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false>), attn_grid(p), dim3(NT), 0, s, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (p.num_splits > 1) e = launch_combine(p, D, false, s);
-  return e;
+hipError_t launch_decode_t(const AttnP& p, bool mf, int phase, hipStream_t s) {
+  if (phase & 1) {
+    if (mf)
+      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true>), attn_grid(p), dim3(NT), 0, s, p);
+    else
+      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false>), attn_grid(p), dim3(NT), 0, s, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if ((phase & 2) && p.num_splits > 1) return launch_combine(p, D, false, s);
+  return hipSuccess;
 }
 
 template <int D, int G>
-hipError_t dispatch_flags(const AttnP& p, bool masked, bool stats, bool load_v, bool mf, hipStream_t s) {
-  if (!masked && !stats && load_v) return launch_decode_t<D, G, false, false, true>(p, mf, s);
-  if (!masked && stats && load_v) return launch_decode_t<D, G, false, true, true>(p, mf, s);
-  if (!masked && stats && !load_v) return launch_decode_t<D, G, false, true, false>(p, mf, s);
-  if (masked && !stats && load_v) return launch_decode_t<D, G, true, false, true>(p, mf, s);
-  if (masked && stats && load_v) return launch_decode_t<D, G, true, true, true>(p, mf, s);
-  if (masked && stats && !load_v) return launch_decode_t<D, G, true, true, false>(p, mf, s);
+hipError_t dispatch_flags(const AttnP& p, bool masked, bool stats, bool load_v, bool mf, int phase, hipStream_t s) {
+  if (!masked && !stats && load_v) return launch_decode_t<D, G, false, false, true>(p, mf, phase, s);
+  if (!masked && stats && load_v) return launch_decode_t<D, G, false, true, true>(p, mf, phase, s);
+  if (!masked && stats && !load_v) return launch_decode_t<D, G, false, true, false>(p, mf, phase, s);
+  if (masked && !stats && load_v) return launch_decode_t<D, G, true, false, true>(p, mf, phase, s);
+  if (masked && stats && load_v) return launch_decode_t<D, G, true, true, true>(p, mf, phase, s);
+  if (masked && stats && !load_v) return launch_decode_t<D, G, true, true, false>(p, mf, phase, s);
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t launch_decode(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, hipStream_t s) {
+hipError_t launch_decode(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, int phase,
+                         hipStream_t s) {
   const bool mf = qk_use_mfma();
 #define KVS_CASE(DD, GG) \
-  if (D == DD && G == GG) return dispatch_flags<DD, GG>(p, masked, stats, load_v, mf, s);
+  if (D == DD && G == GG) return dispatch_flags<DD, GG>(p, masked, stats, load_v, mf, phase, s);
   KVS_FOR_G(KVS_CASE, 64)
   KVS_FOR_G(KVS_CASE, 128)
 #undef KVS_CASE

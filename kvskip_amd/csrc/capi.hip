@@ -116,7 +116,7 @@ int kvskip_struct_size(int which) {
   }
 }
 
-int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+static int decode_phases(const kvskip_attn_args* a, int stats, int load_v, int phase, void* stream) {
   kvs::AttnP p;
   int rc = prepare_attn(a, true, true, load_v != 0, &p);
   if (rc != KVSKIP_OK) return rc;
@@ -132,11 +132,24 @@ int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream
     if (a->block_cnt == nullptr) return fail(KVSKIP_E_INVALID, "block_cnt is required with block_idx");
     if (a->max_blocks < 0) return fail(KVSKIP_E_INVALID, "block_idx must be contiguous int32 [B, Hkv, max_blocks]");
   }
+  if (phase != 3 && a->num_splits < 2) return fail(KVSKIP_E_INVALID, "decode phases need num_splits >= 2");
   if (!load_v) p.out = nullptr;
   const int G = a->Hq / a->Hkv;
-  return launched(kvs::launch_decode(p, a->D, G, masked, stats != 0, load_v != 0,
+  return launched(kvs::launch_decode(p, a->D, G, masked, stats != 0, load_v != 0, phase,
                                      static_cast<hipStream_t>(stream)),
                   "kvskip_decode");
+}
+
+int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+  return decode_phases(a, stats, load_v, 3, stream);
+}
+
+int kvskip_decode_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+  return decode_phases(a, stats, load_v, 1, stream);
+}
+
+int kvskip_merge_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+  return decode_phases(a, stats, load_v, 2, stream);
 }
 
 int kvskip_pv(const kvskip_attn_args* a, void* stream) {

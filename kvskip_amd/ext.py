@@ -102,9 +102,9 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     out32 = torch.empty(B, Hq, D, **f32) if (load_v and want_f32) else None
     lse = torch.empty(B, Hq, **f32)
     bmax = bsum = None
-    if stats:
-        bmax = torch.full((B, Hq, nb), -math.inf, **f32)
-        bsum = torch.zeros(B, Hq, nb, **f32)
+    if stats:                           # every block is written (-inf / 0 where a list skips it)
+        bmax = torch.empty(B, Hq, nb, **f32)
+        bsum = torch.empty(B, Hq, nb, **f32)
     pbuf = torch.empty(B, Hq, nb * TILE, dtype=torch.float16, device=dev) if write_p else None
     part_acc = part_ml = None
     if num_splits > 1:
@@ -118,7 +118,7 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
-    [B, Hq, nb] over the blocks read only: no -inf / 0 fill) and part_acc / part_ml fp32
+    [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
     (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way."""
     check_q(q)
     check_kv(k, "k")
@@ -143,6 +143,47 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
                    part_acc, part_ml)
+
+
+class DecodeOp:
+    """One decode-attention op with its arguments and outputs built once (fixed q, k, v views):
+    run() = decode(); splits() then merge() = its two launches (kvskip_decode_splits /
+    kvskip_merge_splits), for timing each kernel or placing work between them. Not in the
+    reference. Outputs: .out bf16 [B, Hq, D], .lse fp32 [B, Hq]."""
+
+    def __init__(self, q, k, v, scale, num_splits, block_idx=None, block_cnt=None):
+        check_q(q)
+        check_kv(k, "k")
+        check_kv(v, "v")
+        _require(2 <= num_splits <= 256, "DecodeOp: num_splits in 2..256")
+        B, Hq, D = q.shape
+        Hkv, T = k.shape[1], k.shape[2]
+        dev = q.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+        self.lse = torch.empty(B, Hq, **f32)
+        self._keep = [q, k, v, block_idx, block_cnt,
+                      torch.empty(B, Hq, num_splits, D, **f32), torch.empty(B, Hq, num_splits, 2, **f32)]
+        a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
+        if block_idx is not None:
+            a.block_idx, a.block_cnt, a.max_blocks = block_idx.data_ptr(), block_cnt.data_ptr(), block_idx.shape[2]
+        a.num_splits = int(num_splits)
+        a.part_acc, a.part_ml = self._keep[5].data_ptr(), self._keep[6].data_ptr()
+        a.out, a.lse = self.out.data_ptr(), self.lse.data_ptr()
+        self.args, self.dev = a, dev
+        self.lib = _native.lib()
+
+    def _call(self, fn):
+        _native.check(fn(ctypes.byref(self.args), 0, 1, _stream(self.dev)))
+
+    def run(self):
+        self._call(self.lib.kvskip_decode)
+
+    def splits(self):
+        self._call(self.lib.kvskip_decode_splits)
+
+    def merge(self):
+        self._call(self.lib.kvskip_merge_splits)
 
 
 def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,

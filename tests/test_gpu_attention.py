@@ -234,3 +234,55 @@ def test_qk_engines(gpu, engine, monkeypatch):
         keep1, z = O.vskip1_keep(q, k, scale, 1e-3, 2)
         ref1, _ = O.decode(q, k, v, scale, keep=keep1)
         assert O.rel_err(r1["out_f32"].cpu(), ref1) <= F32_TOL
+
+
+def test_decode_op_phases(gpu):
+    """DecodeOp: run() and splits() + merge() (the two launches of decode, exposed separately)
+    give the same bits as ext.decode."""
+    from kvskip_amd import ext as E
+    L = W.cfg1(device="cuda")
+    ref = E.decode(L.q, L.k, L.v, L.scale, None, None, False, True, 8, 2, False, False)
+    op = E.DecodeOp(L.q, L.k, L.v, L.scale, 8)
+    op.run()
+    assert torch.equal(op.out, ref[0]) and torch.equal(op.lse, ref[1])
+    op.out.zero_()
+    op.lse.zero_()
+    op.splits()
+    op.merge()
+    assert torch.equal(op.out, ref[0]) and torch.equal(op.lse, ref[1])
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 8, 32])
+def test_masked_stats_gaps(gpu, num_splits):
+    """Masked statistics into NaN-poisoned buffers: listed blocks carry the dense pass's statistics
+    and every skipped block reads (-inf, 0) -- leading, inner and trailing gaps, a one-entry list
+    and an empty list -- with no fill by the caller."""
+    from kvskip_amd import ext as E
+    g = torch.Generator().manual_seed(7)
+    B, Hq, Hkv, T, D = 2, 8, 4, 64 * 40 - 17, 64
+    nb = math.ceil(T / 64)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).cuda()
+    lists = [[5, 6, 17, 30], [0], [], [nb - 1], [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 20, 38], list(range(nb)),
+             [3, nb - 3], [12, 13, 14, 15]]
+    bi = torch.zeros(B, Hkv, nb, dtype=torch.int32)
+    bc = torch.zeros(B, Hkv, dtype=torch.int32)
+    keep = torch.zeros(B, Hkv, nb, dtype=torch.bool)
+    for i, lst in enumerate(lists):
+        b, h = divmod(i, Hkv)
+        bi[b, h, :len(lst)] = torch.tensor(lst, dtype=torch.int32)
+        bc[b, h] = len(lst)
+        keep[b, h, lst] = True
+    f32 = dict(dtype=torch.float32, device="cuda")
+    bufs = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device="cuda"), lse=torch.empty(B, Hq, **f32),
+                blk_max=torch.full((B * Hq * nb,), math.nan, **f32), blk_sum=torch.full((B * Hq * nb,), math.nan, **f32),
+                part_acc=torch.empty(B * Hq * num_splits * D, **f32), part_ml=torch.empty(B * Hq * num_splits * 2, **f32))
+    E.decode_into(q, k, v, 0.125, bufs, bi.cuda(), bc.cuda(), stats=True, num_splits=num_splits)
+    bmax = bufs["blk_max"].view(B, Hq, nb).cpu()
+    bsum = bufs["blk_sum"].view(B, Hq, nb).cpu()
+    dense = E.decode(q, k, v, 0.125, None, None, True, True, 4, 2, False, False)
+    vis = keep.repeat_interleave(Hq // Hkv, 1)
+    assert not torch.isnan(bmax).any() and not torch.isnan(bsum).any(), "a block was left unwritten"
+    assert (bmax[~vis] == -math.inf).all() and (bsum[~vis] == 0).all()
+    assert torch.equal(bmax[vis], dense[2].cpu()[vis]) and torch.equal(bsum[vis], dense[3].cpu()[vis])
