@@ -146,7 +146,8 @@ typedef struct kvskip_plan_args {
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
 
-/* Floats of kvskip_plan_args.part for a state of capacity NBC blocks. */
+/* Floats of kvskip_plan_args.part for a state of capacity NBC blocks (-1 for invalid sizes).
+ * Not in the reference: sizes the optional multi-workgroup plan workspace. */
 int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC);
 
 /* Refresh planner, after the attention pass. Replaces kvskip::UpdateParams + launch_update

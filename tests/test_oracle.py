@@ -237,6 +237,35 @@ def test_calibration_peak_bounds_the_residual():
     assert torch.allclose(st.calib, torch.clamp(real - pr["miss"], min=0.0), atol=1e-12)
 
 
+@pytest.mark.parametrize("kind", ["add", "logit"])
+def test_calibration_ema_kinds_closed_form(kind):
+    """Kinds "add" and "logit" are exponential averages of the residual; at rate 1 the new c is the
+    residual itself (real - est, or logit(real) - logit(est) with the 1e-6 clamp), at rate 0 the old
+    c, and in between their convex mix (rate 0.3, starting from c = 0.2); clamped at 0 unless free."""
+    q, k, v = _layer(seed=42)
+    q2 = q + 0.8 * rnd(*q.shape, seed=43)
+    p = torch.softmax(O.scores(q2, k, 1.0), -1)
+
+    def run(rate, c0, free=False):
+        pol = OP.Policy(calib=rate, calib_kind=kind, dense_heads=(0, 1), calib_free=free)
+        st, _ = OP.init(q, k, v, 1.0, pol)
+        st.calib = torch.full_like(st.calib, c0)
+        _, pr = OP.step(st, q2, k, v, pol)
+        att = O.heads(O.token_mask(pr["sel"], k.shape[2]), 4)
+        real = (p * ~att).sum(-1).reshape(1, 2, 4).amax(-1)
+        clamp = lambda x: x.clamp(1e-6, 1 - 1e-6)
+        lg = lambda x: torch.log(clamp(x)) - torch.log1p(-clamp(x))
+        resid = real - pr["miss"] if kind == "add" else lg(real) - lg(pr["miss"])
+        return st.calib, resid
+
+    c1, resid = run(1.0, 0.2, free=True)
+    assert torch.allclose(c1, resid, atol=1e-12)
+    c0, _ = run(0.0, 0.2)
+    assert torch.allclose(c0, torch.full_like(c0, 0.2), atol=1e-15)
+    cm, resid = run(0.3, 0.2)
+    assert torch.allclose(cm, (0.7 * 0.2 + 0.3 * resid).clamp_min(0.0), atol=1e-12)
+
+
 def test_token_index_vs_loops():
     g = np.random.default_rng(3)
     ids = g.integers(0, 7, size=(2, 300))
