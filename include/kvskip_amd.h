@@ -77,6 +77,14 @@ typedef struct kvskip_attn_args {
   int32_t local;               /* newest blocks always kept (block 0 always kept too) */
   int32_t* vcount;             /* optional [B, Hkv] V blocks loaded (atomically added) */
   const float* lse_prev;       /* optional [B, Hq] natural-log normaliser estimate; NULL: block-0 bound */
+
+  /* Ragged batch (not in the reference; kvskip_decode only): optional [B] int32 device array,
+   * sequence b attends tokens [0, clamp(seq_lens[b], 1, T)) of its view (T = the views' capacity,
+   * nb = ceil(T / 64) sizes the statistics). The split pass then partitions each KV head's work
+   * over the whole batch: chunks of C = ceil(sum_b items_b / num_splits) blocks (or list entries),
+   * so every workgroup gets at most C whatever the lengths; needs num_splits >= 2, B <= 256, and
+   * part_acc / part_ml of [B, Hq, num_splits, ...]. */
+  const int32_t* seq_lens;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block
@@ -142,6 +150,10 @@ typedef struct kvskip_plan_args {
    * launch decides and compacts; NULL: one workgroup per head, one launch. Calls sharing a
    * workspace must not overlap. */
   float* part;
+  /* Optional [B] int32 device array (not in the reference): ragged batch, sequence b holds
+   * clamp(seq_lens[b], 1, T) tokens (T = the views' capacity); add_token adds each sequence's
+   * last row. */
+  const int32_t* seq_lens;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
@@ -173,22 +185,26 @@ typedef struct kvskip_update_args {
   int32_t list_stats;          /* 0: blk_max / blk_sum cover every block (the reference's contract);
                                   1: they hold values only for the blocks of this step's plan (the
                                   rest is uninitialised and ignored), so they need no fill */
+  const int32_t* seq_lens;     /* optional [B] int32 (ragged batch, as in kvskip_plan_args); the
+                                  statistics keep the row length ceil(T / 64) */
 } kvskip_update_args;
 
 int kvskip_update(const kvskip_update_args* p, void* stream);
 
 /* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
  * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums
- * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. */
+ * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. seq_lens: optional
+ * [B] int32 device array (ragged batch: sequence b sums its first clamp(seq_lens[b], 1, T) rows). */
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv,
-                      int32_t T, int32_t D, float* csum, int32_t NBC, void* stream);
+                      int32_t T, int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens, void* stream);
 
 /* Token index of a decode step: idx[b, blk] = 1 if block blk (of the first T tokens) holds an
  * earlier copy of ids[b, T-1] or the position right after one; blocks >= nb up to NBC are
  * zeroed. The device form of index_steps / index_blocks (src/lab.py:149-167,
- * src/run_free.py:103-113). ids [B, ids_stride] int32. */
+ * src/run_free.py:103-113). ids [B, ids_stride] int32. seq_lens: optional [B] int32 device array
+ * (ragged batch: sequence b's current token is ids[b, clamp(seq_lens[b], 1, T) - 1]). */
 int kvskip_token_index(const int32_t* ids, int64_t ids_stride, int32_t B, int32_t T, uint8_t* idx,
-                       int32_t NBC, void* stream);
+                       int32_t NBC, const int32_t* seq_lens, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* kvskip_last_error(void);

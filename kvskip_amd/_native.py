@@ -29,6 +29,7 @@ class AttnArgs(ctypes.Structure):
         ("blk_max", c_void_p), ("blk_sum", c_void_p),
         ("p_out", c_void_p), ("p_in", c_void_p), ("blk_scale", c_void_p),
         ("tau", c_float), ("local", c_int32), ("vcount", c_void_p), ("lse_prev", c_void_p),
+        ("seq_lens", c_void_p),
     ]
 
 
@@ -45,7 +46,7 @@ class PlanArgs(ctypes.Structure):
         ("NBC", c_int32), ("local", c_int32), ("max_age", c_int32), ("add_token", c_int32),
         ("calib_on", c_int32), ("calib_kind", c_int32),
         ("scale", c_float), ("delta", c_float),
-        ("part", c_void_p),
+        ("part", c_void_p), ("seq_lens", c_void_p),
     ]
 
 
@@ -58,7 +59,7 @@ class UpdateArgs(ctypes.Structure):
         ("calib_rate", c_float), ("aix_thr", c_float), ("level", c_float),
         ("calib_free", c_int32), ("calib_kind", c_int32),
         ("B", c_int32), ("Hq", c_int32), ("Hkv", c_int32), ("T", c_int32), ("NBC", c_int32), ("local", c_int32),
-        ("list_stats", c_int32),
+        ("list_stats", c_int32), ("seq_lens", c_void_p),
     ]
 
 
@@ -74,8 +75,8 @@ SIGNATURES = {
     "kvskip_plan_part_floats": ([c_int32, c_int32, c_int32, c_int32], c_int64),
     "kvskip_update": ([POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
-                           c_int32, c_void_p], c_int),
-    "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p], c_int),
+                           c_int32, c_void_p, c_void_p], c_int),
+    "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),
     "kvskip_last_error": ([], c_char_p),
     "kvskip_version": ([], c_char_p),
     "kvskip_struct_size": ([c_int], c_int),

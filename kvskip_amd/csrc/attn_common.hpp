@@ -67,15 +67,80 @@ constexpr int gpad() {
 }
 
 // Work coordinates of this workgroup: the launch index i is dispatched to XCD i % 8; work item
+// Launch index -> work index, XCD-aware (consecutive work on one XCD) when n % 8 == 0.
+__device__ __forceinline__ int xcd_remap(int i, int n) { return n % 8 == 0 ? (i % 8) * (n / 8) + i / 8 : i; }
+
 // w = (i % 8) * (n / 8) + i / 8 gives each XCD a contiguous run of work items.
 __device__ __forceinline__ void work_coords(int S, int Hkv, int B, int& split, int& h, int& b) {
-  const int n = S * Hkv * B;
-  int i = blockIdx.x;
-  if (n % 8 == 0) i = (i % 8) * (n / 8) + i / 8;
+  const int i = xcd_remap(blockIdx.x, S * Hkv * B);
   split = i % S;
   const int r = i / S;
   h = r % Hkv;
   b = r / Hkv;
+}
+
+// ---- Ragged batches (seq_lens): sequence b attends tokens [0, clamp(seq_lens[b], 1, T)).
+__device__ __forceinline__ int seq_len(const AttnP& p, int b) {
+  return p.seq_lens != nullptr ? min(max(p.seq_lens[b], 1), p.T) : p.T;
+}
+
+// Items of sequence b on KV head h: its blocks (dense) or its list entries (masked).
+__device__ __forceinline__ int ragged_items(const AttnP& p, int b, int h, bool masked) {
+  if (masked) return min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
+  return (seq_len(p, b) + BLK - 1) / BLK;
+}
+
+// Ragged partition of KV head h, uniform over the wavefront: chunks of C = ceil(sum_b items_b / S)
+// items, numbered sequence by sequence (at most S + B chunks per head). For chunk number `it`:
+// b (-1 past the head's last chunk), the chunk within b and b's item count. Returns C.
+__device__ int ragged_lookup(const AttnP& p, int h, int it, bool masked, int& b, int& chunk, int& items) {
+  constexpr int NR = MAX_RAGGED_B / WAVE;
+  const int lane = threadIdx.x % WAVE;
+  int nv[NR];
+  int tot = 0;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int bb = r * WAVE + lane;
+    nv[r] = bb < p.B ? ragged_items(p, bb, h, masked) : 0;
+    tot += nv[r];
+  }
+  tot = wave_sum_int(tot);
+  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  b = -1;
+  chunk = 0;
+  items = 0;
+  int base = 0;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (r * WAVE >= p.B) break;
+    const int ch = (nv[r] + C - 1) / C;
+    const int incl = wave_incl_scan(ch);
+    const int excl = base + incl - ch;
+    const uint64_t hit = __ballot(ch > 0 && it >= excl && it < excl + ch);
+    if (hit != 0) {
+      const int l = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      b = r * WAVE + l;
+      chunk = it - __shfl(excl, l, WAVE);
+      items = __shfl(nv[r], l, WAVE);
+    }
+    base += __shfl(incl, WAVE - 1, WAVE);
+  }
+  return C;
+}
+
+// Chunks (split partials) of (b, KV head h) under the ragged partition.
+__device__ __forceinline__ int ragged_chunks(const AttnP& p, int b, int h, bool masked) {
+  constexpr int NR = MAX_RAGGED_B / WAVE;
+  const int lane = threadIdx.x % WAVE;
+  int tot = 0;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int bb = r * WAVE + lane;
+    tot += bb < p.B ? ragged_items(p, bb, h, masked) : 0;
+  }
+  tot = wave_sum_int(tot);
+  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  return (ragged_items(p, b, h, masked) + C - 1) / C;
 }
 
 // Byte range of one (b, head) of a K or V view: rows 0..T-1 of D bf16 each, row stride st.
@@ -383,12 +448,17 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   const int tid = threadIdx.x, cls = tid / 32, dl = tid % 32;
   const int d = blockIdx.y * 32 + dl;
   const int S = p.num_splits;
+  // ragged: (b, hq) has ragged_chunks partials (0: nothing attended, out 0 and lse -inf)
+  const int Sv = p.seq_lens == nullptr
+                     ? S
+                     : ragged_chunks(p, static_cast<int>(hq / p.Hq), static_cast<int>(hq % p.Hq) / (p.Hq / p.Hkv),
+                                     p.block_idx != nullptr);
   const float* ml = p.part_ml + hq * S * 2;
   __shared__ float rA[NC][32], rL[NC], rM[NC];
   float ms[U], ls[U], as[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int s = min(cls + NC * u, S - 1);
+    const int s = max(min(cls + NC * u, Sv - 1), 0);
     const float2 t = *reinterpret_cast<const float2*>(ml + 2 * s);
     ms[u] = t.x;
     ls[u] = t.y;
@@ -397,7 +467,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   float mloc = NEG_INF;
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (cls + NC * u < S) mloc = fmaxf(mloc, ms[u]);
+    if (cls + NC * u < Sv) mloc = fmaxf(mloc, ms[u]);
   if (dl == 0) rM[cls] = mloc;
   __syncthreads();
   float M = NEG_INF;
@@ -407,7 +477,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
   float A = 0.f, L = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (cls + NC * u < S) {
+    if (cls + NC * u < Sv) {
       const float w = plain ? 1.f : fexp2(ms[u] - mu);
       L += ls[u] * w;
       if constexpr (WITH_V) A += as[u] * w;
@@ -458,7 +528,10 @@ inline hipError_t launch_combine(const AttnP& p, int D, bool plain, hipStream_t 
   return hipGetLastError();
 }
 
-inline dim3 attn_grid(const AttnP& p) { return dim3(p.num_splits * p.Hkv * p.B); }
+// Ragged: S + B chunk slots per KV head (a head has at most that many chunks).
+inline dim3 attn_grid(const AttnP& p) {
+  return dim3(p.seq_lens != nullptr ? (p.num_splits + p.B) * p.Hkv : p.num_splits * p.Hkv * p.B);
+}
 
 // Instantiated group sizes.
 #define KVS_FOR_G(X, D) \

@@ -38,28 +38,56 @@ __device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, in
   }
 }
 
-template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF>
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG>
 __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
 
-  int split, h, b;
-  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int r8 = lane >> 3, sub = lane & 7;
 
-  int n_items;
-  const int* list = nullptr;
-  if constexpr (MASKED) {
-    n_items = min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
-    list = p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks;
-  } else {
-    n_items = p.nb;
+  // This workgroup's work: (b, KV head h, split) and list positions / blocks [i0, i0 + n) of the
+  // n_items of (b, h); Tb, nbb: the sequence's tokens and blocks.
+  int split, h, b, n_items, i0, n;
+  int Tb = p.T, nbb = p.nb;
+  if constexpr (!RAG) {
+    work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+    n_items = MASKED ? min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks) : p.nb;
+    const int per = (n_items + p.num_splits - 1) / p.num_splits;
+    i0 = min(n_items, split * per);
+    n = min(n_items, i0 + per) - i0;
+  } else {  // ragged: chunks of C items over the whole batch, per KV head
+    const int W = p.num_splits + p.B;
+    const int it = xcd_remap(blockIdx.x, W * p.Hkv);
+    h = it / W;
+    int chunk;
+    const int C = ragged_lookup(p, h, it % W, MASKED, b, chunk, n_items);
+    if constexpr (MASKED && STATS) {
+      if (it % W == 0) {  // (b', h) with an empty list have no chunk: their statistics are written here
+        for (int b0 = wave * WAVE; b0 < p.B; b0 += NT) {
+          const int bb = b0 + lane;
+          uint64_t empty = __ballot(bb < p.B && ragged_items(p, bb, h, true) == 0);
+          while (empty != 0) {
+            const int be = b0 + __ffsll(static_cast<unsigned long long>(empty)) - 1;
+            empty &= empty - 1;
+            const int64_t q0 = static_cast<int64_t>(be) * p.Hq + static_cast<int64_t>(h) * G;
+            for (int t = lane; t < G * p.nb; t += WAVE) {
+              p.blk_max[(q0 + t / p.nb) * p.nb + t % p.nb] = NEG_INF;
+              p.blk_sum[(q0 + t / p.nb) * p.nb + t % p.nb] = 0.f;
+            }
+          }
+        }
+      }
+    }
+    if (b < 0) return;
+    split = chunk;
+    i0 = chunk * C;
+    n = min(n_items, i0 + C) - i0;
+    Tb = seq_len(p, b);
+    nbb = (Tb + BLK - 1) / BLK;
   }
-  const int per = (n_items + p.num_splits - 1) / p.num_splits;
-  const int i0 = min(n_items, split * per);
-  const int n = min(n_items, i0 + per) - i0;
+  const int* list = MASKED ? p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks : nullptr;
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
   int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this thread's gap
   if constexpr (MASKED && STATS) {
@@ -69,8 +97,8 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     }
   }
 
-  const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(p.T, p.k_st, D));
-  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, LOAD_V ? head_bytes(p.T, p.v_st, D) : 0);
+  const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(Tb, p.k_st, D));
+  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, LOAD_V ? head_bytes(Tb, p.v_st, D) : 0);
   const uint32_t voff = static_cast<uint32_t>((lane / Lay<D>::VLPR) * p.v_st * 2 + 16 * (lane % Lay<D>::VLPR));
   const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
 
@@ -84,7 +112,7 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   // Block of this wavefront's k-th item; out-of-range list entries read block 0 and are masked.
   auto block_of = [&](int k) -> int {
     const int blk = MASKED ? list[i0 + wave + NWAVE * k] : i0 + wave + NWAVE * k;
-    return (blk >= 0 && blk < p.nb) ? blk : -1;
+    return (blk >= 0 && blk < nbb) ? blk : -1;
   };
   auto accumulate = [&](const u32x4 (&vr)[Lay<D>::VN], const float (&alpha)[G]) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -115,7 +143,7 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     auto process = [&](int blk, const u32x4 (&kr)[4][KS], float (&alpha)[G]) {
       const int t0 = blk >= 0 ? blk * BLK : 0;
       float s[4][4];
-      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, blk >= 0 ? p.T : 0, lane);
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, blk >= 0 ? Tb : 0, lane);
       float pv[4][4], ar[4];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -201,7 +229,7 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     auto process = [&](int blk, const u32x4 (&kr)[8][Lay<D>::KC], float (&alpha)[G]) {
       const int t0 = blk >= 0 ? blk * BLK : 0;
       float s[8][G];
-      qk_block<D, G>(s, kr, qv, p.scale_log2, t0, blk >= 0 ? p.T : 0, lane);
+      qk_block<D, G>(s, kr, qv, p.scale_log2, t0, blk >= 0 ? Tb : 0, lane);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float e[8], mt, st, c;
@@ -252,16 +280,27 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     }
   }
   if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, tid, gap_prev, gap_cur);
+  if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
+    if (nbb < p.nb && i0 + n == n_items) {
+      for (int t = tid; t < G * (p.nb - nbb); t += NT) {
+        const int64_t i = (hq0 + t / (p.nb - nbb)) * p.nb + nbb + t % (p.nb - nbb);
+        p.blk_max[i] = NEG_INF;
+        p.blk_sum[i] = 0.f;
+      }
+    }
+  }
   finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
 }
 
 template <int D, int G, bool M, bool ST, bool LV>
 hipError_t launch_decode_t(const AttnP& p, bool mf, int phase, hipStream_t s) {
   if (phase & 1) {
-    if (mf)
-      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true>), attn_grid(p), dim3(NT), 0, s, p);
+    if (p.seq_lens != nullptr)  // ragged batches: MFMA engine only
+      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true, true>), attn_grid(p), dim3(NT), 0, s, p);
+    else if (mf)
+      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true, false>), attn_grid(p), dim3(NT), 0, s, p);
     else
-      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false>), attn_grid(p), dim3(NT), 0, s, p);
+      hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, false, false>), attn_grid(p), dim3(NT), 0, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -89,6 +89,7 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->local = a->local;
   p->vcount = a->vcount;
   p->lse_prev = a->lse_prev;
+  p->seq_lens = a->seq_lens;
   return KVSKIP_OK;
 }
 
@@ -133,6 +134,11 @@ static int decode_phases(const kvskip_attn_args* a, int stats, int load_v, int p
     if (a->max_blocks < 0) return fail(KVSKIP_E_INVALID, "block_idx must be contiguous int32 [B, Hkv, max_blocks]");
   }
   if (phase != 3 && a->num_splits < 2) return fail(KVSKIP_E_INVALID, "decode phases need num_splits >= 2");
+  if (a->seq_lens != nullptr) {
+    if (a->num_splits < 2) return fail(KVSKIP_E_INVALID, "seq_lens needs num_splits >= 2");
+    if (a->B > kvs::MAX_RAGGED_B) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: B <= %d", kvs::MAX_RAGGED_B);
+    if (a->p_out != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: no fp16 P output");
+  }
   if (!load_v) p.out = nullptr;
   const int G = a->Hq / a->Hkv;
   return launched(kvs::launch_decode(p, a->D, G, masked, stats != 0, load_v != 0, phase,
@@ -156,6 +162,7 @@ int kvskip_pv(const kvskip_attn_args* a, void* stream) {
   kvs::AttnP p;
   int rc = prepare_attn(a, false, false, true, &p);
   if (rc != KVSKIP_OK) return rc;
+  if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "pv: seq_lens is not supported");
   if (a->p_in == nullptr) return fail(KVSKIP_E_INVALID, "P: fp16 [B, Hq, t_pad]");
   if (!aligned16(a->p_in)) return fail(KVSKIP_E_INVALID, "P must be 16-byte aligned");
   if (a->blk_scale == nullptr) return fail(KVSKIP_E_INVALID, "blk_scale: contiguous fp32 [B, Hkv, nb, G]");
@@ -172,6 +179,7 @@ int kvskip_vskip1(const kvskip_attn_args* a, void* stream) {
   kvs::AttnP p;
   int rc = prepare_attn(a, true, true, true, &p);
   if (rc != KVSKIP_OK) return rc;
+  if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "vskip1: seq_lens is not supported");
   if (!(a->tau > 0.f) || a->local < 0) return fail(KVSKIP_E_INVALID, "tau > 0, local >= 0, num_splits >= 1");
   if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
   if (a->num_splits > 1 && a->part_acc == nullptr)
@@ -242,21 +250,24 @@ int kvskip_update(const kvskip_update_args* p, void* stream) {
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,
-                      int32_t D, float* csum, int32_t NBC, void* stream) {
+                      int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens, void* stream) {
   if (k == nullptr || csum == nullptr) return fail(KVSKIP_E_INVALID, "block_sums: null tensor");
   if (B < 1 || Hkv < 1 || T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
   if (D != 64 && D != 128) return fail(KVSKIP_E_UNSUPPORTED, "block_sums: D in {64, 128}");
   if ((T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK > NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
-  return launched(kvs::launch_block_sums(k, k_sb, k_sh, k_st, B, Hkv, T, D, csum, NBC, static_cast<hipStream_t>(stream)),
+  if (k_st % 8 != 0 || k_sh % 8 != 0 || k_sb % 8 != 0 || !aligned16(k))
+    return fail(KVSKIP_E_INVALID, "k strides must be multiples of 8 elements (16-byte rows)");
+  return launched(kvs::launch_block_sums(k, k_sb, k_sh, k_st, B, Hkv, T, D, csum, NBC, seq_lens,
+                                         static_cast<hipStream_t>(stream)),
                   "kvskip_block_sums");
 }
 
 int kvskip_token_index(const int32_t* ids, int64_t ids_stride, int32_t B, int32_t T, uint8_t* idx, int32_t NBC,
-                       void* stream) {
+                       const int32_t* seq_lens, void* stream) {
   if (ids == nullptr || idx == nullptr) return fail(KVSKIP_E_INVALID, "token_index: null tensor");
   if (B < 1 || T < 1 || ids_stride < T) return fail(KVSKIP_E_INVALID, "token_index: ids must be [B, >= T] int32");
   if ((T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK > NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
-  return launched(kvs::launch_token_index(ids, ids_stride, B, T, idx, NBC, static_cast<hipStream_t>(stream)),
+  return launched(kvs::launch_token_index(ids, ids_stride, B, T, idx, NBC, seq_lens, static_cast<hipStream_t>(stream)),
                   "kvskip_token_index");
 }
 

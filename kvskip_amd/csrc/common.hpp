@@ -98,6 +98,20 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<DPP_MIRROR>(v);
   return rows4_sum(v);
 }
+// Integer wavefront scan (inclusive, over lanes) and sum; uniform sum.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x % WAVE;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int t = __shfl_up(v, o, WAVE);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+  return __builtin_amdgcn_readlane(wave_incl_scan(v), WAVE - 1);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_XOR1>(v));
   v = fmaxf(v, dpp<DPP_XOR2>(v));

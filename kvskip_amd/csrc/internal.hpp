@@ -38,7 +38,10 @@ struct AttnP {
   int local;
   int* vcount;
   const float* lse_prev;
+  const int* seq_lens;  // [B] or null: sequence b uses tokens [0, clamp(seq_lens[b], 1, T))
 };
+
+constexpr int MAX_RAGGED_B = 256;  // batch bound of the ragged partition (one scan per 64)
 
 constexpr int MAX_SPLITS = 256;
 
@@ -59,9 +62,9 @@ hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, 
 hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s);
 hipError_t launch_update(const kvskip_update_args& p, hipStream_t s);
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
-                             int D, float* csum, int NBC, hipStream_t s);
+                             int D, float* csum, int NBC, const int32_t* seq_lens, hipStream_t s);
 hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,
-                              hipStream_t s);
+                              const int32_t* seq_lens, hipStream_t s);
 
 // Largest block count the planner kernels hold in LDS for a group of G query heads.
 int planner_max_blocks(int G);

@@ -30,6 +30,11 @@ namespace {
 
 __device__ __forceinline__ bool always_block(int blk, int nb, int local) { return blk == 0 || blk >= nb - local; }
 
+// Tokens of sequence b: clamp(seq_lens[b], 1, T) in a ragged batch, else T.
+__device__ __forceinline__ int seq_T(const int32_t* seq_lens, int b, int T) {
+  return seq_lens != nullptr ? min(max(seq_lens[b], 1), T) : T;
+}
+
 __device__ __forceinline__ float clamped_logit(float x) {
   x = fminf(fmaxf(x, 1e-6f), 1.f - 1e-6f);
   return __logf(x) - __logf(1.f - x);
@@ -95,7 +100,8 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   constexpr int PU = (D == 128 && G >= 7) ? 2 : 4;  // block-row groups (4 rows each) in flight, 128 VGPRs
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
-  const int nb = (p.T + BLK - 1) / BLK;
+  const int Tb = seq_T(p.seq_lens, b, p.T);
+  const int nb = (Tb + BLK - 1) / BLK;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;  // head g: + g*NBC
   float* csum = p.csum + bh * p.NBC * D;
@@ -148,7 +154,7 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   uint2 kx[DW];
   if (add) {
     const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
-                         static_cast<int64_t>(p.T - 1) * p.k_st;
+                         static_cast<int64_t>(Tb - 1) * p.k_st;
 #pragma unroll
     for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
   }
@@ -189,7 +195,7 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
               make_float4(cv[u][4 * w], cv[u][4 * w + 1], cv[u][4 * w + 2], cv[u][4 * w + 3]);
         }
       }
-      const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? p.T - blk * BLK : BLK);
+      const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? Tb - blk * BLK : BLK);
       float mine = 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -276,7 +282,8 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   constexpr int DL = D / 16, DW = DL / 4, SP = part_stride(G);
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, C = gridDim.x;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
-  const int nb = (p.T + BLK - 1) / BLK;
+  const int Tb = seq_T(p.seq_lens, b, p.T);
+  const int nb = (Tb + BLK - 1) / BLK;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;
   float* csum = p.csum + bh * p.NBC * D;
@@ -306,7 +313,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
           qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
     }
     const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
-                         static_cast<int64_t>(p.T - 1) * p.k_st;
+                         static_cast<int64_t>(Tb - 1) * p.k_st;
 #pragma unroll
     for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
   }
@@ -357,7 +364,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
             make_float4(cv[u][4 * w], cv[u][4 * w + 1], cv[u][4 * w + 2], cv[u][4 * w + 3]);
       }
     }
-    const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? p.T - blk * BLK : BLK);
+    const float inv_n = 1.f / static_cast<float>(blk == nb - 1 ? Tb - blk * BLK : BLK);
     float mine = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -408,7 +415,8 @@ template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
   constexpr int SP = part_stride(G);
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int nb = (p.T + BLK - 1) / BLK, C = (nb + WCB - 1) / WCB;
+  const int nb = (seq_T(p.seq_lens, b, p.T) + BLK - 1) / BLK;     // the sequence's blocks
+  const int C = ((p.T + BLK - 1) / BLK + WCB - 1) / WCB;          // chunks of the scores pass (capacity)
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int fl = p.flags[h];
   const float* pb = p.part + bh * C * SP;
@@ -489,7 +497,8 @@ __global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_ar
   constexpr int RC = R < 16 ? R : 16;  // register slots whose loads are in flight together
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
-  const int nb = (p.T + BLK - 1) / BLK;
+  const int nbl = (p.T + BLK - 1) / BLK;                       // row length of the statistics
+  const int nb = (seq_T(p.seq_lens, b, p.T) + BLK - 1) / BLK;   // the sequence's blocks
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t hrow = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + wave;
   __shared__ uint64_t sKm[G][R];  // each query head's top-p blocks (lane bits of r)
@@ -513,8 +522,8 @@ __global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_ar
 #pragma unroll
     for (int r = 0; r < RC; ++r) {  // loads of the chunk first, clamped in range
       const int ic = min(lane + WAVE * (c + r), nb - 1);
-      bm[r] = p.blk_max[hrow * nb + ic];
-      bs[r] = p.blk_sum[hrow * nb + ic];
+      bm[r] = p.blk_max[hrow * nbl + ic];
+      bs[r] = p.blk_sum[hrow * nbl + ic];
       kb[r] = keep[ic];
       ib[r] = ixp[ic];
     }
@@ -642,27 +651,55 @@ __global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_ar
   if (lane == 0) p.lse_att[hrow] = s2 > 0.f ? m2 + __logf(s2) : NEG_INF;
 }
 
-// csum[b, h, blk, d] = sum over the block's rows t < T of k[b, h, t, d]; zero for blk >= nb.
+// csum[b, h, blk, d] = sum over the block's rows t < T_b of k[b, h, t, d]; zero for blk >= nb_b.
+// 256 threads: thread (row group rg, 4-dim column c) adds its 64 / RG rows, all loads in flight,
+// then the RG partial rows are added in LDS (in row-group order).
 template <int D>
-__global__ void __launch_bounds__(D) block_sums_kernel(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                                                       int Hkv, int T, float* csum, int NBC) {
+__global__ void __launch_bounds__(256) block_sums_kernel(const uint16_t* k, int64_t k_sb, int64_t k_sh,
+                                                         int64_t k_st, int Hkv, int T, float* csum, int NBC,
+                                                         const int32_t* seq_lens) {
+  constexpr int DL = D / 4, RG = 256 / DL, RPT = BLK / RG;
   const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int d = threadIdx.x;
-  const int t0 = blk * BLK, t1 = min(T, t0 + BLK);
-  const uint16_t* kb = k + b * k_sb + h * k_sh + d;
-  float a = 0.f;
-  for (int t = t0; t < t1; ++t) a += __uint_as_float(static_cast<uint32_t>(kb[static_cast<int64_t>(t) * k_st]) << 16);
-  csum[((static_cast<int64_t>(b) * Hkv + h) * NBC + blk) * D + d] = a;
+  const int tid = threadIdx.x, rg = tid / DL, c = tid % DL;
+  const int Tb = seq_T(seq_lens, b, T);
+  const uint16_t* kb = k + b * k_sb + h * k_sh + 4 * c;
+  __shared__ float part[RG][D];
+  uint2 x[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int t = blk * BLK + rg + RG * i;
+    x[i] = t < Tb ? *reinterpret_cast<const uint2*>(kb + static_cast<int64_t>(t) * k_st) : make_uint2(0u, 0u);
+  }
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    a0 += bf_lo(x[i].x);
+    a1 += bf_hi(x[i].x);
+    a2 += bf_lo(x[i].y);
+    a3 += bf_hi(x[i].y);
+  }
+  part[rg][4 * c] = a0;
+  part[rg][4 * c + 1] = a1;
+  part[rg][4 * c + 2] = a2;
+  part[rg][4 * c + 3] = a3;
+  __syncthreads();
+  if (tid < D) {
+    float a = 0.f;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) a += part[r][tid];
+    csum[((static_cast<int64_t>(b) * Hkv + h) * NBC + blk) * D + tid] = a;
+  }
 }
 
 // idx[b, blk] = any position j < T of the block with ids[j] == cur (j < T-1) or ids[j-1] == cur
 // (j-1 < T-1), cur = ids[T-1]. One wavefront per block, lane = token.
-__global__ void __launch_bounds__(256) token_index_kernel(const int32_t* ids, int64_t stride, int T, uint8_t* idx,
-                                                          int NBC) {
+__global__ void __launch_bounds__(256) token_index_kernel(const int32_t* ids, int64_t stride, int Tcap, uint8_t* idx,
+                                                          int NBC, const int32_t* seq_lens) {
   const int b = blockIdx.y;
   const int blk = blockIdx.x * 4 + threadIdx.x / WAVE;
   const int lane = threadIdx.x % WAVE;
   if (blk >= NBC) return;
+  const int T = seq_T(seq_lens, b, Tcap);
   const int32_t* x = ids + b * stride;
   const int32_t cur = x[T - 1];
   const int j = blk * BLK + lane;
@@ -735,22 +772,24 @@ hipError_t launch_update(const kvskip_update_args& p, hipStream_t s) {
 }
 
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
-                             int D, float* csum, int NBC, hipStream_t s) {
+                             int D, float* csum, int NBC, const int32_t* seq_lens, hipStream_t s) {
   const dim3 grid(NBC, Hkv, B);
   const uint16_t* kk = reinterpret_cast<const uint16_t*>(k);
   if (D == 128)
-    hipLaunchKernelGGL((block_sums_kernel<128>), grid, dim3(128), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC);
+    hipLaunchKernelGGL((block_sums_kernel<128>), grid, dim3(256), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC,
+                       seq_lens);
   else if (D == 64)
-    hipLaunchKernelGGL((block_sums_kernel<64>), grid, dim3(64), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC);
+    hipLaunchKernelGGL((block_sums_kernel<64>), grid, dim3(256), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC,
+                       seq_lens);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
-hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,
+hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC, const int32_t* seq_lens,
                               hipStream_t s) {
   const dim3 grid((NBC + 3) / 4, B);
-  hipLaunchKernelGGL(token_index_kernel, grid, dim3(256), 0, s, ids, ids_stride, T, idx, NBC);
+  hipLaunchKernelGGL(token_index_kernel, grid, dim3(256), 0, s, ids, ids_stride, T, idx, NBC, seq_lens);
   return hipGetLastError();
 }
 

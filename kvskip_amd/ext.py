@@ -78,11 +78,15 @@ def _attn_args(q, k, v, scale, B, Hq, Hkv, T, D) -> AttnArgs:
 
 
 def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
-           want_f32=False, write_p=False):
+           want_f32=False, write_p=False, seq_lens=None):
     """Split-K decode attention (kernels/kvskip_ext.cpp:25-101).
 
     Returns [out bf16 [B,Hq,D], lse fp32 [B,Hq], blk_max, blk_sum ([B,Hq,nb] or None), out_f32 (or None),
-    P fp16 [B,Hq,nb*64] (write_p) or None]."""
+    P fp16 [B,Hq,nb*64] (write_p) or None].
+
+    seq_lens (not in the reference): int32 [B] on the device, a ragged batch; sequence b attends
+    tokens [0, clamp(seq_lens[b], 1, T)) of its view; num_splits is then the per-KV-head split
+    budget over the whole batch (>= 2)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -111,11 +115,12 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
         part_acc = torch.empty(B, Hq, num_splits, D, **f32) if load_v else None
         part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml)
+                   pbuf, part_acc, part_ml, seq_lens)
     return [out, lse, bmax, bsum, out32, pbuf]
 
 
-def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1):
+def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,
+                seq_lens=None):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
     [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
@@ -142,7 +147,7 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
         _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
-                   part_acc, part_ml)
+                   part_acc, part_ml, seq_lens)
 
 
 class DecodeOp:
@@ -187,10 +192,14 @@ class DecodeOp:
 
 
 def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml):
+                   pbuf, part_acc, part_ml, seq_lens=None):
     B, Hq, D = q.shape
     Hkv, T = k.shape[1], k.shape[2]
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
+    if seq_lens is not None:
+        _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
+                 and seq_lens.numel() == B, "seq_lens: contiguous CUDA int32 [B]")
+        a.seq_lens = seq_lens.data_ptr()
     if block_idx is not None:
         _require(block_cnt is not None, "block_cnt is required with block_idx")
         bi, bc = block_idx, block_cnt
@@ -281,11 +290,13 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None):
+         part=None, seq_lens=None):
     """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
 
     part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
-    centroid pass is spread over all compute units (two launches instead of one)."""
+    centroid pass is spread over all compute units (two launches instead of one).
+    seq_lens (not in the reference): int32 [B] on the device, a ragged batch over views of
+    capacity T (sequence b holds seq_lens[b] tokens; add_token adds each one's last row)."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
@@ -333,6 +344,7 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
         check_f32(part, "part")
         _require(part.numel() >= plan_part_floats(B, Hq, Hkv, NBC), "part: too small")
         p.part = part.data_ptr()
+    p.seq_lens = _seq_lens_ptr(seq_lens, B)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
@@ -345,7 +357,7 @@ def plan_part_floats(B, Hq, Hkv, NBC) -> int:
 
 def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
            est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0,
-           list_stats=False):
+           list_stats=False, seq_lens=None):
     """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place.
 
     list_stats (not in the reference): blk_max / blk_sum hold values only for the blocks of this
@@ -389,6 +401,7 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
         _require(flags is not None, "list_stats needs flags")
         set_flags_idx()
         p.list_stats = 1
+    p.seq_lens = _seq_lens_ptr(seq_lens, B)
     dev = keep.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_update(ctypes.byref(p), _stream(dev)))
@@ -404,8 +417,17 @@ def read_bw(x, out, blocks):
                                                 int(blocks), _stream(dev)))
 
 
-def block_sums(k, NBC, out=None):
-    """Per-block key sums [B, Hkv, NBC, D] fp32 of k [B, Hkv, T, D] (blocks >= nb are zero)."""
+def _seq_lens_ptr(seq_lens, B):
+    if seq_lens is None:
+        return None
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
+             and seq_lens.numel() == B, "seq_lens: contiguous CUDA int32 [B]")
+    return seq_lens.data_ptr()
+
+
+def block_sums(k, NBC, out=None, seq_lens=None):
+    """Per-block key sums [B, Hkv, NBC, D] fp32 of k [B, Hkv, T, D] (blocks >= nb are zero);
+    seq_lens: ragged batch (sequence b sums its first seq_lens[b] rows)."""
     check_kv(k, "k")
     B, Hkv, T, D = k.shape
     _require((T + TILE - 1) // TILE <= NBC, "block capacity exceeded")
@@ -415,12 +437,14 @@ def block_sums(k, NBC, out=None):
     _require(tuple(out.shape) == (B, Hkv, NBC, D), "csum: [B, Hkv, NBC, D]")
     with torch.cuda.device(k.device):
         _native.check(_native.lib().kvskip_block_sums(k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), B, Hkv, T, D,
-                                                      out.data_ptr(), NBC, _stream(k.device)))
+                                                      out.data_ptr(), NBC, _seq_lens_ptr(seq_lens, B),
+                                                      _stream(k.device)))
     return out
 
 
-def token_index(ids, T, NBC, out=None):
-    """Token-index blocks [B, NBC] uint8 of the step whose current token is ids[:, T-1]."""
+def token_index(ids, T, NBC, out=None, seq_lens=None):
+    """Token-index blocks [B, NBC] uint8 of the step whose current token is ids[:, T-1]
+    (ids[b, seq_lens[b] - 1] with seq_lens: ragged batch)."""
     _require(ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 2 and ids.stride(1) == 1,
              "ids: CUDA int32 [B, >= T]")
     B = ids.shape[0]
@@ -430,5 +454,5 @@ def token_index(ids, T, NBC, out=None):
     _require(out.dtype == torch.uint8 and out.is_contiguous() and tuple(out.shape) == (B, NBC), "idx: uint8 [B, NBC]")
     with torch.cuda.device(ids.device):
         _native.check(_native.lib().kvskip_token_index(ids.data_ptr(), ids.stride(0), B, int(T), out.data_ptr(), NBC,
-                                                       _stream(ids.device)))
+                                                       _seq_lens_ptr(seq_lens, B), _stream(ids.device)))
     return out

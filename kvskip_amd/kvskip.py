@@ -56,6 +56,13 @@ def num_splits_for(bh: int, n_tiles: int, sms: int | None = None, max_splits: in
     return best
 
 
+def ragged_splits(B: int, Hkv: int, nb_max: int, sms: int | None = None) -> int:
+    """Split budget per KV head for a ragged batch (seq_lens): about two workgroups per CU over all
+    KV heads, at least 8 blocks per chunk at full length, in 2..256."""
+    slots = (sms or num_sms()) * 2
+    return max(2, min(256, slots // max(Hkv, 1), max(1, B * nb_max // 8)))
+
+
 @dataclass
 class Plan:
     """Kept-block list for the masked kernel (kernels/kvskip.py:70-76)."""
@@ -74,10 +81,12 @@ def make_plan(keep: torch.Tensor, sync: bool = True) -> Plan:
 
 
 def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = False, load_v: bool = True,
-           num_splits: int | None = None, stages: int = 2, out_f32: bool = False, write_p: bool = False) -> dict:
+           num_splits: int | None = None, stages: int = 2, out_f32: bool = False, write_p: bool = False,
+           seq_lens: torch.Tensor | None = None) -> dict:
     """Decode attention for one layer (kernels/kvskip.py:88-113). Returns dict(out [B, Hq, D] bf16,
     lse [B, Hq] fp32, blk_max / blk_sum [B, Hq, nb] fp32 (stats), out_f32 (if asked), p (write_p:
-    fp16 [B, Hq, nb*64] = exp(s - blk_max)))."""
+    fp16 [B, Hq, nb*64] = exp(s - blk_max))). seq_lens (int32 [B] on the device, not in the
+    reference): a ragged batch over views of capacity T, with the split budget shared by the batch."""
     if q.dim() == 4:
         q = q.squeeze(2)
     B, Hq, D = q.shape
@@ -85,10 +94,10 @@ def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = Fal
     nb = math.ceil(T / TILE)
     n_items = nb if plan is None else plan.max_cnt
     if num_splits is None:
-        num_splits = num_splits_for(B * Hkv, n_items)
+        num_splits = num_splits_for(B * Hkv, n_items) if seq_lens is None else ragged_splits(B, Hkv, n_items)
     res = ext().decode(q, k, v, float(scale), None if plan is None else plan.block_idx,
                        None if plan is None else plan.block_cnt, stats, load_v, int(num_splits), int(stages),
-                       out_f32, write_p)
+                       out_f32, write_p, seq_lens)
     out, lse, bmax, bsum, o32, pbuf = res
     d = {"out": out if load_v else None, "lse": lse, "num_splits": num_splits}
     if stats:

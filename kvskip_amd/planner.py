@@ -118,12 +118,12 @@ class FusedPlanner:
         self.state["part"] = torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), dtype=torch.float32, device=idx.device)
         self.NBC = NBC
 
-    def _attend(self, q, k, v, scale, nb):
+    def _attend(self, q, k, v, scale, nb, seq_lens=None):
         """Masked + statistics pass over the plan's lists into the planner's buffers. Returns
         out [B, Hq, D] (valid until the next step) and the [B, Hq, nb] statistics views."""
         B, Hq, D = q.shape
         Hkv = k.shape[1]
-        S = K.num_splits_for(B * Hkv, nb)
+        S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb)
         n_st, n_part = B * Hq * self.NBC, B * Hq * S * D
         b = self.bufs
         if b is None or b["blk_max"].numel() < n_st or b["part_acc"].numel() < n_part or b["out"].shape != q.shape:
@@ -134,7 +134,7 @@ class FusedPlanner:
                                  blk_sum=torch.empty(n_st, **f32), part_acc=torch.empty(n_part, **f32),
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
-        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S)
+        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, seq_lens=seq_lens)
         n = B * Hq * nb
         return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
 
@@ -142,13 +142,13 @@ class FusedPlanner:
         if self.count:
             self.counters[key] = self.counters.get(key, 0) + value
 
-    def _set_idx(self, idx, ids, T):
+    def _set_idx(self, idx, ids, T, seq_lens=None):
         """This step's token-index blocks into state['idx'] ([B, NBC] uint8): from idx (bool / uint8
         [B, >= nb]) or from token ids [B, >= T] int32 with the device token-index kernel."""
         s = self.state
         nb = math.ceil(T / TILE)
         if ids is not None:
-            E.token_index(ids, T, self.NBC, out=s["idx"])
+            E.token_index(ids, T, self.NBC, out=s["idx"], seq_lens=seq_lens)
         elif idx is not None and idx.dtype == torch.uint8 and idx.is_contiguous() and idx.shape[1] == self.NBC:
             return idx                                               # a ready [B, NBC] device buffer
         elif idx is not None:
@@ -159,10 +159,12 @@ class FusedPlanner:
         return s["idx"]
 
     # -- steps
-    def first(self, q, k, v, scale):
+    def first(self, q, k, v, scale, seq_lens=None):
         """First decode step: dense + block statistics and the state initialisation
         (src/kvskip_attn.py:339-354), on the device: per-block key sums of the prefix, a plan that
-        refreshes every head, the attention pass, and an update without calibration."""
+        refreshes every head, the attention pass, and an update without calibration.
+        seq_lens (int32 [B] on the device): a ragged batch; k, v are then views of a common
+        capacity and sequence b holds seq_lens[b] tokens (every later step appends one to each)."""
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape
@@ -170,27 +172,31 @@ class FusedPlanner:
         nb = math.ceil(T / TILE)
         self._alloc(q, k, nb + MARGIN)
         s = self.state
-        E.block_sums(k, self.NBC, out=s["csum"])
+        E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens)
         every = torch.ones(Hkv, dtype=torch.int32, device=q.device)      # refresh all, no index heads
         pol = self.policy
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
-               int(pol.local), False, part=s["part"])
-        out, bmax, bsum = self._attend(q, k, v, scale, nb)
+               int(pol.local), False, part=s["part"], seq_lens=seq_lens)
+        out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
-                 float(pol.level), int(pol.local), every, list_stats=True)
+                 float(pol.level), int(pol.local), every, list_stats=True, seq_lens=seq_lens)
         self.t, self.T = 0, T
-        self._count("dense_heads", B * Hkv)
-        self._count("blocks_read", B * Hkv * nb)
-        self._count("blocks_total", B * Hkv * nb)
+        self.ragged = seq_lens is not None
+        if self.count:
+            total = B * Hkv * nb if seq_lens is None else ((seq_lens + TILE - 1) // TILE).sum() * Hkv
+            self._count("dense_heads", B * Hkv)
+            self._count("blocks_read", total)
+            self._count("blocks_total", total)
         return out
 
-    def step(self, q, k, v, scale, idx=None, ids=None):
+    def step(self, q, k, v, scale, idx=None, ids=None, seq_lens=None):
         """One later decode step (src/kvskip_attn.py:451-478): plan -> masked + stats attention ->
         update. idx: this step's token-index blocks (bool [B, >= nb], or a uint8 [B, NBC] device
-        buffer used as is) or ids: token ids [B, >= T] int32 (index heads / auto index only)."""
+        buffer used as is) or ids: token ids [B, >= T] int32 (index heads / auto index only).
+        seq_lens: the ragged batch's lengths after this step's token (one more per sequence)."""
         if self.state is None:
-            return self.first(q, k, v, scale)
+            return self.first(q, k, v, scale, seq_lens)
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape
@@ -200,28 +206,32 @@ class FusedPlanner:
             self._grow(nb + MARGIN)
         s = self.state
         pol = self.policy
-        add_token = T == self.T + 1
-        if not add_token and T != self.T:
-            E.block_sums(k, self.NBC, out=s["csum"])                  # several tokens appended: resum
+        if seq_lens is not None:
+            add_token = True                                          # one token per sequence per step
+        else:
+            add_token = T == self.T + 1
+            if not add_token and T != self.T:
+                E.block_sums(k, self.NBC, out=s["csum"])              # several tokens appended: resum
         self.t += 1
         self.T = T
-        ix = self._set_idx(idx, ids, T) if pol.needs_index else None
+        ix = self._set_idx(idx, ids, T, seq_lens) if pol.needs_index else None
         cal = pol.calib is not None
         kind = KINDS[pol.calib_kind]
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"], s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
                int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
                cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None,
-               part=s["part"])
-        out, bmax, bsum = self._attend(q, k, v, scale, nb)
+               part=s["part"], seq_lens=seq_lens)
+        out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
                  float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
                  float(pol.calib or 0.0), bool(pol.calib_free), kind,
                  s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0),
-                 list_stats=True)
+                 list_stats=True, seq_lens=seq_lens)
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
-            self._count("blocks_total", B * Hkv * nb)
+            self._count("blocks_total", B * Hkv * nb if seq_lens is None
+                        else ((seq_lens + TILE - 1) // TILE).sum() * Hkv)
             self._count("masked_heads", B * Hkv)
             self._count("dense_heads", s["trig"].sum())
         return out

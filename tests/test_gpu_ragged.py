@@ -1,0 +1,185 @@
+"""GPU parity of ragged batches (config 5: per-sequence lengths, split budget shared by the batch)
+against the fp64 oracle run on each sequence alone (oracle/attention.py)."""
+
+import math
+
+import pytest
+import torch
+
+from kvskip_amd import ext as E
+from kvskip_amd import kvskip as K
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+REL = 2e-3       # bf16 output, relative L2 (bench/harness.py:134)
+LSE_TOL = 2e-4   # natural-log units
+
+
+def _layer(lens, Hq, Hkv, D, cap, seed):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, cap, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, cap, D, generator=g).to(torch.bfloat16)
+    for b, T in enumerate(lens):          # rows past a sequence's end hold garbage the pass must not read
+        k[b, :, T:] = 1e4
+        v[b, :, T:] = float("nan")
+    return q, k, v
+
+
+def _bufs(B, Hq, D, nb, S):
+    f32 = dict(dtype=torch.float32, device="cuda")
+    return dict(out=torch.full((B, Hq, D), math.nan, dtype=torch.bfloat16, device="cuda"),
+                lse=torch.full((B, Hq), math.nan, **f32),
+                blk_max=torch.full((B * Hq * nb,), math.nan, **f32), blk_sum=torch.full((B * Hq * nb,), math.nan, **f32),
+                part_acc=torch.empty(B * Hq * S * D, **f32), part_ml=torch.empty(B * Hq * S * 2, **f32))
+
+
+@pytest.mark.parametrize("G,D", [(7, 128), (4, 64)])
+@pytest.mark.parametrize("S", [2, 7, 64])
+def test_ragged_dense_stats(gpu, G, D, S):
+    lens = [1, 63, 64, 65, 1000, 4097, 300]
+    Hkv = 4
+    Hq = Hkv * G
+    cap = 4160
+    nb = math.ceil(cap / 64)
+    q, k, v = _layer(lens, Hq, Hkv, D, cap, seed=5 + G + S)
+    scale = 1 / math.sqrt(D)
+    B = len(lens)
+    bufs = _bufs(B, Hq, D, nb, S)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    E.decode_into(q.cuda(), k.cuda(), v.cuda(), scale, bufs, stats=True, num_splits=S, seq_lens=sl)
+    bmax = bufs["blk_max"].view(B, Hq, nb).cpu()
+    bsum = bufs["blk_sum"].view(B, Hq, nb).cpu()
+    for b, T in enumerate(lens):
+        ref, lse = O.decode(q[b:b + 1], k[b:b + 1, :, :T], v[b:b + 1, :, :T], scale)
+        err = O.rel_err(bufs["out"][b:b + 1].float().cpu(), ref)
+        assert err <= REL, (b, T, err)
+        assert (bufs["lse"][b:b + 1].cpu().double() - lse).abs().max().item() <= LSE_TOL
+        M, Sx = O.block_stats(q[b:b + 1], k[b:b + 1, :, :T], scale)
+        nbb = M.shape[-1]
+        assert (bmax[b, :, :nbb].double() - M[0]).abs().max().item() <= LSE_TOL, (b, T)
+        assert ((bsum[b, :, :nbb].double() - Sx[0]) / Sx[0]).abs().max().item() <= 2e-4
+        assert (bmax[b, :, nbb:] == -math.inf).all() and (bsum[b, :, nbb:] == 0).all(), (b, T)
+    # the reference-surface op with the shared split budget agrees
+    r = K.decode(q.cuda(), k.cuda(), v.cuda(), scale, seq_lens=sl)
+    assert torch.isfinite(r["out"].float()).all()
+    for b, T in enumerate(lens):
+        ref, _ = O.decode(q[b:b + 1], k[b:b + 1, :, :T], v[b:b + 1, :, :T], scale)
+        assert O.rel_err(r["out"][b:b + 1].float().cpu(), ref) <= REL
+
+
+@pytest.mark.parametrize("S", [2, 16, 128])
+def test_ragged_masked_stats(gpu, S):
+    lens = [4096, 70, 2500, 640, 1, 3333]
+    Hkv, G, D = 4, 7, 128
+    Hq = Hkv * G
+    cap = 4096
+    nb = math.ceil(cap / 64)
+    q, k, v = _layer(lens, Hq, Hkv, D, cap, seed=50 + S)
+    scale = 1 / math.sqrt(D)
+    B = len(lens)
+    g = torch.Generator().manual_seed(60 + S)
+    keep = torch.zeros(B, Hkv, nb, dtype=torch.bool)
+    for b, T in enumerate(lens):
+        nbb = math.ceil(T / 64)
+        for h in range(Hkv):
+            if (b + h) % 5 == 4:
+                continue                                  # an empty list
+            keep[b, h, :nbb] = torch.rand(nbb, generator=g) < 0.3
+            keep[b, h, 0] = True
+    bi = torch.zeros(B, Hkv, nb, dtype=torch.int32)
+    bc = torch.zeros(B, Hkv, dtype=torch.int32)
+    for b in range(B):
+        for h in range(Hkv):
+            idx = torch.nonzero(keep[b, h])[:, 0].to(torch.int32)
+            bi[b, h, :len(idx)] = idx
+            bc[b, h] = len(idx)
+    bufs = _bufs(B, Hq, D, nb, S)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    E.decode_into(q.cuda(), k.cuda(), v.cuda(), scale, bufs, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
+                  seq_lens=sl)
+    bmax = bufs["blk_max"].view(B, Hq, nb).cpu()
+    bsum = bufs["blk_sum"].view(B, Hq, nb).cpu()
+    out = bufs["out"].float().cpu()
+    lse_d = bufs["lse"].cpu().double()
+    for b, T in enumerate(lens):
+        nbb = math.ceil(T / 64)
+        kb = keep[b:b + 1, :, :nbb]
+        ref, lse = O.decode(q[b:b + 1], k[b:b + 1, :, :T], v[b:b + 1, :, :T], scale, keep=kb)
+        empty = ~kb.any(-1).repeat_interleave(G, 1)[0]        # query heads whose group attends nothing
+        if (~empty).any():
+            assert O.rel_err(out[b][~empty][None], ref[0][~empty][None]) <= REL, (b, T)
+            assert (lse_d[b][~empty] - lse[0][~empty]).abs().max().item() <= LSE_TOL
+        assert (out[b][empty] == 0).all() and (lse_d[b][empty] == -math.inf).all()
+        M, Sx = O.block_stats(q[b:b + 1], k[b:b + 1, :, :T], scale, keep=kb)
+        vis = kb.repeat_interleave(G, 1)[0]
+        assert (bmax[b, :, :nbb][vis].double() - M[0][vis]).abs().max().item() <= LSE_TOL if vis.any() else True
+        assert (bmax[b, :, :nbb][~vis] == -math.inf).all() and (bsum[b, :, :nbb][~vis] == 0).all(), (b, T)
+        assert (bmax[b, :, nbb:] == -math.inf).all() and (bsum[b, :, nbb:] == 0).all(), (b, T)
+
+
+def test_ragged_rejects(gpu):
+    q, k, v = _layer([10, 20], 8, 2, 64, 64, seed=1)
+    sl = torch.tensor([10, 20], dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="num_splits >= 2"):
+        E.decode(q.cuda(), k.cuda(), v.cuda(), 0.125, num_splits=1, seq_lens=sl)
+    with pytest.raises(RuntimeError, match="seq_lens"):
+        E.decode(q.cuda(), k.cuda(), v.cuda(), 0.125, num_splits=4, seq_lens=sl[:1])
+
+
+def test_planner_loop_ragged(gpu):
+    """Config 5 in small: a ragged batch (3 sequences, 28 / 4 heads, G 7) through the fused planner
+    loop for 24 steps, each sequence against its own oracle planner (refresh_pre_step semantics):
+    identical read sets on every head-step (borderline margins excepted), outputs within 2e-3."""
+    from kvskip_amd import workloads as W
+    from kvskip_amd.planner import FusedPlanner, Policy as DPolicy
+    from oracle import planner as OP
+
+    lens0 = [2000, 700, 3100]
+    steps = 24
+    Hkv, G, D = 4, 7, 128
+    run = W.planner_run(layers=1, B=3, Hq=Hkv * G, Hkv=Hkv, D=D, steps=steps, seed=9, ragged=lens0)
+    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    qp = W.QueryProcess(run, 0, p_jump=0.05, revert=True)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    ids = run.ids.cuda()
+    fp = FusedPlanner(DPolicy(**pol.__dict__))
+    states = [None] * 3
+    same = total = border = 0
+    for t in range(steps):
+        lens = [T0 + t + 1 for T0 in lens0]
+        sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        q = qp.next()
+        if t == 0:
+            out_d = fp.first(q.cuda(), k, v, run.scale, seq_lens=sl)
+        else:
+            out_d = fp.step(q.cuda(), k, v, run.scale, ids=ids, seq_lens=sl)
+        read_d = fp.read_mask(math.ceil(k.shape[2] / 64)).cpu()
+        for b, T in enumerate(lens):
+            qb, kb, vb = q[b:b + 1], run.k[0][b:b + 1, :, :T], run.v[0][b:b + 1, :, :T]
+            nbb = math.ceil(T / 64)
+            if t == 0:
+                states[b], out_r = OP.init(qb, kb, vb, run.scale, pol)
+                read_r = torch.ones(1, Hkv, nbb, dtype=torch.bool)
+                margin = torch.full((1, Hkv), math.inf, dtype=torch.float64)
+            else:
+                idx_b = torch.from_numpy(OP.index_blocks(run.ids[b:b + 1].numpy(), T))
+                out_r, pr = OP.step(states[b], qb, kb, vb, pol, idx=idx_b)
+                read_r, margin = pr["read"], pr["margin"]
+            rd = read_d[b:b + 1, :, :nbb]
+            assert not read_d[b, :, nbb:].any(), "a block past the sequence's end was listed"
+            diff = (rd != read_r).any(-1)
+            bad = diff & (margin < 1e-5)
+            border += int(bad.sum())
+            assert not bool((diff & (margin >= 1e-5)).any()), f"read set differs at step {t}, sequence {b}"
+            same += int((~diff).sum())
+            total += diff.numel()
+            hq = (~diff).repeat_interleave(G, 1)[0]
+            if bool(hq.any()):
+                err = O.rel_err(out_d[b][hq].float().cpu()[None], out_r[0][hq][None])
+                assert err <= REL, (t, b, err)
+            assert (fp.state["calib"][b].double().cpu() - states[b].calib[0]).abs().max().item() <= 1e-4
+            assert torch.equal(fp.state["aix"][b].bool().cpu(), states[b].aix[0])
+    print(f"ragged planner loop: identical read sets on {same}/{total} head-steps, borderline {border}", flush=True)
