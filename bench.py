@@ -124,6 +124,7 @@ def main():
     ap.add_argument("--no-planner", action="store_true", help="skip the config-4 planner loop")
     ap.add_argument("--planner-layers", type=int, default=32)
     ap.add_argument("--planner-steps", type=int, default=128)
+    ap.add_argument("--cfg5-steps", type=int, default=32, help="decode steps of the config-5 ragged loop")
     ap.add_argument("--pmc-target", action="store_true",
                     help="profiling target only: 20 dense config-2 decodes + copy kernels of known size, then exit")
     args = ap.parse_args()
@@ -268,6 +269,15 @@ def main():
                                                     steps=min(args.planner_steps, 64), revert=True,
                                                     tag="cfg4-focused")
         torch.cuda.empty_cache()
+        # config 5: batch 16 of Qwen2.5-7B layers (28 / 4 heads, G 7), contexts log-uniform in
+        # [4096, 65536], 28 layers, ragged split-K over the batch
+        g5 = torch.Generator().manual_seed(5)
+        lens5 = [int(round(math.exp(x))) for x in
+                 (torch.rand(16, generator=g5, dtype=torch.float64) * math.log(16) + math.log(4096)).tolist()]
+        res["planner_cfg5"] = bench_planner(dev, layers=28, steps=min(args.planner_steps, args.cfg5_steps), B=16,
+                                            Hq=28, Hkv=4, ragged=lens5, dense_layer0=False, seed=5, chunk=8,
+                                            tag="cfg5")
+        torch.cuda.empty_cache()
 
     achieved = bytes_split / t_split / 1e3
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -353,13 +363,16 @@ def pmc_target(dense, dev):
     print(json.dumps({"pmc_target": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2}), flush=True)
 
 
-def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4"):
-    """Config 4: `layers` Llama-3.1-8B attention layers, `steps` decode steps from T0 (one token
-    appended per step), query drift + jumps, stage-4 policy (delta 0.05, max age 32, calibration
-    0.05 peak, warm-up (32, 8), token-index latch at 0.1; reproduce/04-tails.sh:16,63-69), layer 0
-    dense. One eager pass with counters gives the read fraction and refresh rate; the timed passes
-    replay HIP graphs of `chunk` steps x all layers (decisions still made on the device) for the
-    planner loop and for dense decode of every layer."""
+def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
+                  Hkv=8, ragged=None, dense_layer0=True, seed=4):
+    """The device-side planner loop over `layers` attention layers for `steps` decode steps (one
+    token appended per step and sequence), query drift + jumps, stage-4 policy (delta 0.05, max
+    age 32, calibration 0.05 peak, warm-up (32, 8), token-index latch at 0.1;
+    reproduce/04-tails.sh:16,63-69). Config 4: B 1, 32 / 8 heads, T0 32768, layer 0 dense.
+    Config 5: `ragged` per-sequence prefix lengths (views of a common capacity, seq_lens). One
+    eager pass with counters gives the read fraction and refresh rate; the timed passes replay HIP
+    graphs of `chunk` steps x all layers (decisions still made on the device) for the planner loop
+    and for dense decode of every layer."""
     import torch
 
     from kvskip_amd import ext as E
@@ -368,46 +381,58 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     from kvskip_amd.planner import FusedPlanner, Policy
 
     t_gen = time.perf_counter()
-    run = W.planner_run(layers=layers, T0=T0, steps=steps, seed=4, device=dev)
-    B, Hkv, _, D = run.k[0].shape
-    Hq = run.q0[0].shape[1]
+    run = W.planner_run(layers=layers, B=B, Hq=Hq, Hkv=Hkv, T0=T0, steps=steps, seed=seed, ragged=ragged, device=dev)
+    _, _, Tcap, D = run.k[0].shape
     qps = [W.QueryProcess(run, l, noise=noise, revert=revert) for l in range(layers)]
     qs = torch.stack([torch.stack([qps[l].next() for l in range(layers)]) for _ in range(steps)]).to(dev)
-    NBC = math.ceil((T0 + 1) / 64) + 64
-    idx_all = torch.zeros(steps, B, NBC, dtype=torch.uint8, device=dev)
     ids = run.ids.to(dev)
+    if ragged is None:
+        NBC = math.ceil((T0 + 1) / 64) + 64
+        sl_all = [None] * steps
+    else:
+        NBC = math.ceil(Tcap / 64) + 64
+        base = torch.tensor(ragged, dtype=torch.int32, device=dev)
+        sl_all = [(base + t + 1).contiguous() for t in range(steps)]
+    idx_all = torch.zeros(steps, B, NBC, dtype=torch.uint8, device=dev)
     for t in range(steps):
-        E.token_index(ids, T0 + t + 1, NBC, out=idx_all[t])
+        E.token_index(ids, T0 + t + 1 if ragged is None else Tcap, NBC, out=idx_all[t], seq_lens=sl_all[t])
     pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
-    log(f"{tag}: {layers} layers x {steps} steps from T {T0} generated in {time.perf_counter() - t_gen:.1f} s")
+    first_planned = 1 if dense_layer0 else 0
+    ctx = f"T {T0}" if ragged is None else f"ragged T in [{min(ragged)}, {max(ragged)}], sum {sum(ragged)}"
+    log(f"{tag}: {layers} layers x {steps} steps, B {B}, {Hq} / {Hkv} heads, {ctx}, generated in "
+        f"{time.perf_counter() - t_gen:.1f} s")
 
-    def kv(l, T):
+    def kv(l, t):
+        if ragged is not None:
+            return run.k[l], run.v[l]
+        T = T0 + t + 1
         return run.k[l][:, :, :T], run.v[l][:, :, :T]
 
     def dense_layer(l, t):
-        k, v = kv(l, T0 + t + 1)
-        return K.decode(qs[t, l], k, v, run.scale)["out"]
+        k, v = kv(l, t)
+        return K.decode(qs[t, l], k, v, run.scale, seq_lens=sl_all[t])["out"]
 
     def planner_pass(planners, t):
         for l in range(layers):
-            if l == 0:
-                dense_layer(0, t)
+            if l < first_planned:
+                dense_layer(l, t)
                 continue
-            k, v = kv(l, T0 + t + 1)
+            k, v = kv(l, t)
             if t == 0:
-                planners[l].first(qs[t, l], k, v, run.scale)
+                planners[l].first(qs[t, l], k, v, run.scale, seq_lens=sl_all[t])
             else:
-                planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t])
+                planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t], seq_lens=sl_all[t])
 
     # eager pass with counters
-    planners = [None] + [FusedPlanner(pol) for _ in range(1, layers)]
+    planners = [None] * first_planned + [FusedPlanner(pol) for _ in range(first_planned, layers)]
     for t in range(steps):
         planner_pass(planners, t)
     torch.cuda.synchronize()
-    read = sum(float(p.counters["blocks_read"]) for p in planners[1:])
-    total = sum(float(p.counters["blocks_total"]) for p in planners[1:])
-    refresh = sum(float(p.counters.get("dense_heads", 0)) for p in planners[1:]) - (layers - 1) * B * Hkv
-    head_steps = (layers - 1) * (steps - 1) * B * Hkv
+    pl = planners[first_planned:]
+    read = sum(float(p.counters["blocks_read"]) for p in pl)
+    total = sum(float(p.counters["blocks_total"]) for p in pl)
+    refresh = sum(float(p.counters.get("dense_heads", 0)) for p in pl) - len(pl) * B * Hkv
+    head_steps = len(pl) * (steps - 1) * B * Hkv
     log(f"{tag} eager: blocks read {read / total:.3f}, refresh rate {refresh / head_steps:.3f}")
 
     def capture(fn_step, t0, t1):
@@ -433,18 +458,21 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3          # us for steps 1 .. steps-1, all layers
 
-    planners = [None] + [FusedPlanner(pol, count=False) for _ in range(1, layers)]
+    planners = [None] * first_planned + [FusedPlanner(pol, count=False) for _ in range(first_planned, layers)]
     us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
-    out = {"layers": layers, "steps": steps, "T0": T0, "query_noise": noise, "query_revert": revert, "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, "
-           "warm (32, 8), auto index 0.1), layer 0 dense", "blocks_read_frac": read / total,
+    out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
+           "T0": T0 if ragged is None else list(ragged), "query_noise": noise, "query_revert": revert,
+           "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)"
+                     + (", layer 0 dense" if dense_layer0 else ""),
+           "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
     log(f"{tag}: policy {us_plan / n:.2f} us/layer-step vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), "
-        f"{us_plan / (steps - 1) / 1e3:.3f} ms per 32-layer step")
+        f"{us_plan / (steps - 1) / 1e3:.3f} ms per {layers}-layer step")
     del planners, run, qs
     return out
 

@@ -125,7 +125,10 @@ __device__ int ragged_lookup(const AttnP& p, int h, int it, bool masked, int& b,
     }
     base += __shfl(incl, WAVE - 1, WAVE);
   }
-  return C;
+  b = __builtin_amdgcn_readfirstlane(b);  // uniform: scalar registers for the addressing that follows
+  chunk = __builtin_amdgcn_readfirstlane(chunk);
+  items = __builtin_amdgcn_readfirstlane(items);
+  return __builtin_amdgcn_readfirstlane(C);
 }
 
 // Chunks (split partials) of (b, KV head h) under the ragged partition.

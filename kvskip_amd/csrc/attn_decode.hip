@@ -110,8 +110,8 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   float* sPw = sP[wave];
 
   // Block of this wavefront's k-th item; out-of-range list entries read block 0 and are masked.
-  auto block_of = [&](int k) -> int {
-    const int blk = MASKED ? list[i0 + wave + NWAVE * k] : i0 + wave + NWAVE * k;
+  auto block_of = [&](int k) -> int {  // uniform over the wavefront
+    const int blk = __builtin_amdgcn_readfirstlane(MASKED ? list[i0 + wave + NWAVE * k] : i0 + wave + NWAVE * k);
     return (blk >= 0 && blk < nbb) ? blk : -1;
   };
   auto accumulate = [&](const u32x4 (&vr)[Lay<D>::VN], const float (&alpha)[G]) {
@@ -132,6 +132,14 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     constexpr int NI = G < 4 ? G : 4;               // score rows i in use per lane group
     const int j4 = lane >> 4, c16 = lane & 15;
     const uint32_t koffm = static_cast<uint32_t>(c16 * p.k_st * 2 + 16 * j4);
+    // statistics and P of this (b, KV head) through buffer resources: one 32-bit offset per lane
+    // (head 4 j4 + i: + i * row bytes), the block in the scalar offset
+    const uint32_t nb4 = 4u * static_cast<uint32_t>(p.nb), tp2 = 2u * static_cast<uint32_t>(p.t_pad);
+    const rsrc_t rs_max = make_rsrc(STATS ? p.blk_max + hq0 * p.nb : nullptr, STATS ? G * nb4 : 0);
+    const rsrc_t rs_sum = make_rsrc(STATS ? p.blk_sum + hq0 * p.nb : nullptr, STATS ? G * nb4 : 0);
+    const rsrc_t rs_p = make_rsrc(STATS && p.p_out != nullptr ? p.p_out + hq0 * p.t_pad : nullptr,
+                                  STATS && p.p_out != nullptr ? G * tp2 : 0);
+    const uint32_t v_stat = 4u * j4 * nb4, v_p = 4u * j4 * tp2 + 2u * c16;
     u32x4 qa[KS];
     load_q_mf<D, G>(qa, p, b, h, lane);
     float mr[4], lr[4];                             // running (m, l) of head 4 j4 + i
@@ -164,14 +172,13 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
         for (int nt = 0; nt < 4; ++nt) pv[nt][i] = e[nt] * cf;
         if constexpr (STATS) {
           if (blk >= 0 && g < G) {
-            const int64_t hq = hq0 + g;
             if (c16 == 0) {
-              p.blk_max[hq * p.nb + blk] = mt * LN2;
-              p.blk_sum[hq * p.nb + blk] = st;
+              bstore_f32(mt * LN2, rs_max, v_stat + i * nb4, 4 * blk);
+              bstore_f32(st, rs_sum, v_stat + i * nb4, 4 * blk);
             }
             if (p.p_out != nullptr) {
 #pragma unroll
-              for (int nt = 0; nt < 4; ++nt) p.p_out[hq * p.t_pad + t0 + 16 * nt + c16] = f2h(e[nt]);
+              for (int nt = 0; nt < 4; ++nt) bstore_u16(f2h(e[nt]), rs_p, v_p + i * tp2 + 32 * nt, 2 * t0);
             }
           }
         }

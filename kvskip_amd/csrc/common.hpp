@@ -138,6 +138,15 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff)
   return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), AUX);
 }
 
+// 4- and 2-byte stores through a buffer resource: per-lane 32-bit offset + scalar offset, so a
+// loop keeps one offset register per store stream instead of a 64-bit address.
+__device__ __forceinline__ void bstore_f32(float v, rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ void bstore_u16(uint16_t v, rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
 // Online log-sum-exp accumulator in natural units (planner): (m, s) with s = sum exp(x - m).
 __device__ __forceinline__ void lse_push(float& m, float& s, float x) {
   if (x == NEG_INF) return;
