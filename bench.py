@@ -125,6 +125,8 @@ def main():
     ap.add_argument("--planner-layers", type=int, default=32)
     ap.add_argument("--planner-steps", type=int, default=128)
     ap.add_argument("--cfg5-steps", type=int, default=32, help="decode steps of the config-5 ragged loop")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant kernel's timed region (the rocprofv3 --stats target), then exit")
     ap.add_argument("--pmc-target", action="store_true",
                     help="profiling target only: 20 dense config-2 decodes + copy kernels of known size, then exit")
     args = ap.parse_args()
@@ -172,9 +174,10 @@ def main():
     bytes_dense = attn_bytes(B, Hq, Hkv, D, B * Hkv * T)
     bytes_mask = attn_bytes(B, Hq, Hkv, D, kept_rows, stats_nb=nb, list_entries=int(bc.sum()))
 
-    res = {}
+    res = {"dense": {}}
     flush = Flush(dev)
-    for name, fn, nbytes in (("dense", dense, bytes_dense), ("masked_stats", masked, bytes_mask)):
+    for name, fn, nbytes in () if args.roofline_only else (("dense", dense, bytes_dense),
+                                                            ("masked_stats", masked, bytes_mask)):
         for i in range(NCOPY):
             fn(i)
         torch.cuda.synchronize()
@@ -184,14 +187,24 @@ def main():
                      "GBs_event_median": nbytes / med / 1e3}
         log(f"{name}: event median {med:.1f} us -> {nbytes / med / 1e3:.0f} GB/s")
 
-    # ---- the dominant kernel on its own: the split pass of the dense op (HIP events around each
-    # launch on the current stream, after a cache flush), and the split merge after it
+    # ---- the dominant kernel on its own: the split pass of the dense op, `steps` launches back to
+    # back from a HIP graph cycling the 8 KV copies, HIP events around the timed replays (average
+    # per launch); per-launch event medians after a flush as well (they carry ~5 us of event and
+    # dispatch overhead per call)
     ops = [E.DecodeOp(q, ks[i], vs[i], L.scale, S_dense) for i in range(NCOPY)]
-    t_split, t_merge = split_merge_events(ops, args.events, flush)
+    t_split = events_region(lambda i: ops[i].splits(), args.steps, args.warmup)
+    t_merge = events_region(lambda i: ops[i].merge(), args.steps, args.warmup)
+    ev_split, ev_merge = (math.nan, math.nan) if args.roofline_only else split_merge_events(ops, args.events, flush)
     bytes_split = 2 * B * Hkv * T * D * 2 + B * Hq * D * 2          # K + V + q, the split pass's reads
-    res["dense"].update(split_pass_us_median=t_split, merge_us_median=t_merge, split_pass_bytes=bytes_split)
-    log(f"dense split pass: {t_split:.2f} us ({bytes_split / t_split / 1e3:.0f} GB/s), merge {t_merge:.2f} us")
+    res["dense"].update(split_pass_us=t_split, merge_us=t_merge, split_pass_us_event_median=ev_split,
+                        merge_us_event_median=ev_merge, split_pass_bytes=bytes_split)
+    log(f"dense split pass: {t_split:.2f} us per launch ({bytes_split / t_split / 1e3:.0f} GB/s), merge "
+        f"{t_merge:.2f} us; per-call event medians {ev_split:.2f} / {ev_merge:.2f} us")
     del ops
+    if args.roofline_only:
+        print(json.dumps({"roofline_only": True, "split_pass_us": t_split, "merge_us": t_merge,
+                          "GBs": bytes_split / t_split / 1e3}), flush=True)
+        return
 
     # ---- timed steps (dense, the headline) and the masked path, from graphs
     el = timed_steps(dense, args.steps, args.warmup)
@@ -283,7 +296,8 @@ def main():
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4), "traffic": read_traffic(),
             "kernel": f"decode_kernel<128,4,dense,mfma> (split pass, {S_dense} splits) at config 2: K+V+q bytes / "
-                      "median HIP-event duration of one launch after a 512 MiB cache flush",
+                      f"average launch duration, {args.steps} launches back to back from HIP graphs over 8 KV "
+                      "copies (1.07 GB), HIP events around the timed region",
             "algorithmic_bytes": bytes_split, "us_per_launch": round(t_split, 3),
             "read_ceiling_GBs": round(res["read_ceiling_GBs"], 1)}
 
@@ -304,6 +318,25 @@ def main():
         "paths": res, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def events_region(fn, steps, warmup):
+    """Average us per launch of fn(i) (i cycling NCOPY inputs): `steps` launches replayed from HIP
+    graphs of NCOPY launches each, HIP events on the current stream around the timed replays."""
+    import torch
+
+    g = graph_of(fn, NCOPY)
+    for _ in range(max(1, warmup // NCOPY)):
+        g.replay()
+    reps = max(1, steps // NCOPY)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * NCOPY)
 
 
 def split_merge_events(ops, n, flush):
