@@ -191,6 +191,11 @@ typedef struct kvskip_update_args {
 
 int kvskip_update(const kvskip_update_args* p, void* stream);
 
+/* kvskip_merge_splits of an attention pass (num_splits >= 2, load_v) and kvskip_update of the
+ * planner in one launch (disjoint workgroups: both read only what the split pass wrote). Not in
+ * the reference: the device planner loop's pass ends this way (kvskip_decode_splits, then this). */
+int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream);
+
 /* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
  * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums
  * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. seq_lens: optional

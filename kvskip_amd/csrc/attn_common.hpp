@@ -444,12 +444,15 @@ __device__ __forceinline__ void qk_block_mf(float (&s)[4][4], const u32x4 (&kr)[
 // parameter so every load is unconditional, clamped to S - 1, and in flight together), the
 // classes agree on the max through LDS, then weight (2^(m_s - M), log-sum-exp mode; 1, plain
 // mode for the two-pass pass 2) and add in LDS. WITH_V = false (stats-only): only lse.
+// Body of one merge workgroup (query head hq, dims [32 slice, 32 slice + 32)). A workgroup wider
+// than 256 threads (the fused merge + update launch) runs it with its first 256; the others only
+// pass the barriers.
 template <int D, int U, bool WITH_V>
-__global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
+__device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq, int slice) {
   constexpr int NC = 8;
-  const int64_t hq = blockIdx.x;
-  const int tid = threadIdx.x, cls = tid / 32, dl = tid % 32;
-  const int d = blockIdx.y * 32 + dl;
+  const int tid = threadIdx.x, cls = (tid / 32) % NC, dl = tid % 32;
+  const bool act = tid < 256;
+  const int d = slice * 32 + dl;
   const int S = p.num_splits;
   // ragged: (b, hq) has ragged_chunks partials (0: nothing attended, out 0 and lse -inf)
   const int Sv = p.seq_lens == nullptr
@@ -471,7 +474,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (cls + NC * u < Sv) mloc = fmaxf(mloc, ms[u]);
-  if (dl == 0) rM[cls] = mloc;
+  if (act && dl == 0) rM[cls] = mloc;
   __syncthreads();
   float M = NEG_INF;
 #pragma unroll
@@ -486,8 +489,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
       if constexpr (WITH_V) A += as[u] * w;
     }
   }
-  rA[cls][dl] = A;
-  if (dl == 0) rL[cls] = L;
+  if (act) rA[cls][dl] = A;
+  if (act && dl == 0) rL[cls] = L;
   __syncthreads();
   if (tid < 32) {
     float a = 0.f, l = 0.f;
@@ -502,8 +505,25 @@ __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) 
       p.out[hq * D + d] = f2bf(o);
       if (p.out_f32) p.out_f32[hq * D + d] = o;
     }
-    if (!plain && tid == 0 && blockIdx.y == 0 && p.lse) p.lse[hq] = l > 0.f ? (M + flog2(l)) * LN2 : NEG_INF;
+    if (!plain && tid == 0 && slice == 0 && p.lse) p.lse[hq] = l > 0.f ? (M + flog2(l)) * LN2 : NEG_INF;
   }
+}
+
+template <int D, int U, bool WITH_V>
+__global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
+  merge_body<D, U, WITH_V>(p, plain, blockIdx.x, blockIdx.y);
+}
+
+// merge_body with U chosen at run time (U = ceil(S / 8) rounded up to the instantiated sizes).
+template <int D>
+__device__ void merge_body_rt(const AttnP& p, int64_t hq, int slice) {
+  const int u = (p.num_splits + 7) / 8;
+  if (u <= 1) merge_body<D, 1, true>(p, 0, hq, slice);
+  else if (u <= 2) merge_body<D, 2, true>(p, 0, hq, slice);
+  else if (u <= 4) merge_body<D, 4, true>(p, 0, hq, slice);
+  else if (u <= 8) merge_body<D, 8, true>(p, 0, hq, slice);
+  else if (u <= 16) merge_body<D, 16, true>(p, 0, hq, slice);
+  else merge_body<D, MAX_SPLITS / 8, true>(p, 0, hq, slice);
 }
 
 template <int D, bool WITH_V>

@@ -225,7 +225,7 @@ int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC)
   return kvs::plan_part_floats(B, Hq, Hkv, NBC);
 }
 
-int kvskip_update(const kvskip_update_args* p, void* stream) {
+static int check_update(const kvskip_update_args* p) {
   if (p == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
   if (p->blk_max == nullptr || p->blk_sum == nullptr) return fail(KVSKIP_E_INVALID, "blk_max must be contiguous CUDA fp32");
   if (p->trig == nullptr || p->cs_now == nullptr || p->keep == nullptr || p->lse_ref == nullptr ||
@@ -246,7 +246,25 @@ int kvskip_update(const kvskip_update_args* p, void* stream) {
   }
   if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
   if (p->list_stats && p->flags == nullptr) return fail(KVSKIP_E_INVALID, "list_stats needs flags");
+  return KVSKIP_OK;
+}
+
+int kvskip_update(const kvskip_update_args* p, void* stream) {
+  const int rc = check_update(p);
+  if (rc != KVSKIP_OK) return rc;
   return launched(kvs::launch_update(*p, static_cast<hipStream_t>(stream)), "kvskip_update");
+}
+
+int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream) {
+  kvs::AttnP p;
+  int rc = prepare_attn(a, false, false, false, &p);
+  if (rc != KVSKIP_OK) return rc;
+  if ((rc = check_update(u)) != KVSKIP_OK) return rc;
+  if (a->num_splits < 2 || a->part_acc == nullptr) return fail(KVSKIP_E_INVALID, "merge_update needs num_splits >= 2");
+  if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required with load_v");
+  if (a->B != u->B || a->Hq != u->Hq || a->Hkv != u->Hkv || a->T != u->T)
+    return fail(KVSKIP_E_INVALID, "merge_update: attention and update shapes differ");
+  return launched(kvs::launch_merge_update(p, *u, a->D, static_cast<hipStream_t>(stream)), "kvskip_merge_update");
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,

@@ -22,8 +22,7 @@
 //         score key whose upper set holds >= level of the mass (the fewest blocks reaching
 //         level; ties at the threshold are all kept), on weights computed once; wavefront sums
 //         stay in DPP rows + readlane; the group's union goes through LDS as ballot masks.
-#include "common.hpp"
-#include "internal.hpp"
+#include "attn_common.hpp"
 
 namespace kvs {
 namespace {
@@ -492,10 +491,15 @@ __device__ __forceinline__ uint32_t fkey(float y) {
 }
 
 // One wavefront per query head g of the group; lane holds blocks i = lane + 64 r, r < R (nb <= 64 R).
+// Body of the update workgroup of (b, KV head h): wavefronts 0..G-1; in a wider workgroup (the fused
+// merge + update launch) the others only pass the barrier.
 template <int G, int R>
-__global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_args p) {
+__device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, int b) {
   constexpr int RC = R < 16 ? R : 16;  // register slots whose loads are in flight together
-  const int h = blockIdx.x, b = blockIdx.y;
+  if (threadIdx.x >= G * WAVE) {
+    __syncthreads();
+    return;
+  }
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int nbl = (p.T + BLK - 1) / BLK;                       // row length of the statistics
   const int nb = (seq_T(p.seq_lens, b, p.T) + BLK - 1) / BLK;   // the sequence's blocks
@@ -651,6 +655,28 @@ __global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_ar
   if (lane == 0) p.lse_att[hrow] = s2 > 0.f ? m2 + __logf(s2) : NEG_INF;
 }
 
+template <int G, int R>
+__global__ void __launch_bounds__(G * WAVE) update_kernel(const kvskip_update_args p) {
+  update_body<G, R>(p, blockIdx.x, blockIdx.y);
+}
+
+// One launch for the split merge of the attention pass and the update of the planner: workgroups
+// [0, B Hkv) update (first, so their longer latency chain starts at once), the next B Hq D/32
+// merge (both read only what the split pass wrote).
+constexpr int fused_threads(int G) { return G * WAVE > 256 ? G * WAVE : 256; }
+
+template <int D, int G, int R>
+__global__ void __launch_bounds__(fused_threads(G)) merge_update_kernel(const AttnP a, const kvskip_update_args u) {
+  const int n_update = u.B * u.Hkv;
+  const int i = blockIdx.x;
+  if (i < n_update) {
+    update_body<G, R>(u, i % u.Hkv, i / u.Hkv);
+  } else {
+    const int j = i - n_update;
+    merge_body_rt<D>(a, j / (D / 32), j % (D / 32));
+  }
+}
+
 // csum[b, h, blk, d] = sum over the block's rows t < T_b of k[b, h, t, d]; zero for blk >= nb_b.
 // 256 threads: thread (row group rg, 4-dim column c) adds its 64 / RG rows, all loads in flight,
 // then the RG partial rows are added in LDS (in row-group order).
@@ -739,7 +765,34 @@ hipError_t launch_update_t(const kvskip_update_args& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int D, int G>
+hipError_t launch_merge_update_t(const AttnP& a, const kvskip_update_args& p, hipStream_t s) {
+  const int nb = (p.T + BLK - 1) / BLK;
+  const dim3 grid(a.B * a.Hq * (D / 32) + p.B * p.Hkv), blk(fused_threads(G));
+  if (nb <= 2 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 2>), grid, blk, 0, s, a, p);
+  else if (nb <= 4 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 4>), grid, blk, 0, s, a, p);
+  else if (nb <= 8 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 8>), grid, blk, 0, s, a, p);
+  else if (nb <= 16 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 16>), grid, blk, 0, s, a, p);
+  else if (nb <= 32 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 32>), grid, blk, 0, s, a, p);
+  else {  // > 2048 blocks: the fused kernel would spill; two launches
+    const hipError_t e = launch_combine(a, D, false, s);
+    if (e != hipSuccess) return e;
+    return launch_update_t<G>(p, s);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_merge_update(const AttnP& a, const kvskip_update_args& p, int D, hipStream_t s) {
+  const int G = p.Hq / p.Hkv;
+#define KVS_CASE(DD, GG) \
+  if (D == DD && G == GG) return launch_merge_update_t<DD, GG>(a, p, s);
+  KVS_CASE(64, 1) KVS_CASE(64, 2) KVS_CASE(64, 4) KVS_CASE(64, 7) KVS_CASE(64, 8)
+  KVS_CASE(128, 1) KVS_CASE(128, 2) KVS_CASE(128, 4) KVS_CASE(128, 7) KVS_CASE(128, 8)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
 
 // Blocks per head the planner kernels hold (plan: LDS flags; update: registers), any G.
 int planner_max_blocks(int) { return MAX_NB; }

@@ -120,11 +120,12 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
 
 
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,
-                seq_lens=None):
+                seq_lens=None, phase=3):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
     [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
-    (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way."""
+    (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way.
+    phase: 3 = the whole op, 1 = the split pass only (its merge left to merge_splits / merge_update)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -147,7 +148,7 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
         _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
-                   part_acc, part_ml, seq_lens)
+                   part_acc, part_ml, seq_lens, phase)
 
 
 class DecodeOp:
@@ -191,8 +192,8 @@ class DecodeOp:
         self._call(self.lib.kvskip_merge_splits)
 
 
-def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens=None):
+def _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
+                 part_ml, seq_lens=None) -> AttnArgs:
     B, Hq, D = q.shape
     Hkv, T = k.shape[1], k.shape[2]
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
@@ -213,9 +214,20 @@ def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_spli
     a.out, a.out_f32, a.lse = _ptr(out), _ptr(out32), lse.data_ptr()
     a.blk_max, a.blk_sum = _ptr(bmax), _ptr(bsum)
     a.p_out = _ptr(pbuf)
+    return a
+
+
+_PHASES = {3: "kvskip_decode", 1: "kvskip_decode_splits", 2: "kvskip_merge_splits"}
+
+
+def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
+                   pbuf, part_acc, part_ml, seq_lens=None, phase=3):
+    a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
+                     part_ml, seq_lens)
     dev = q.device
     with torch.cuda.device(dev):
-        _native.check(_native.lib().kvskip_decode(ctypes.byref(a), int(bool(stats)), int(bool(load_v)), _stream(dev)))
+        _native.check(getattr(_native.lib(), _PHASES[phase])(ctypes.byref(a), int(bool(stats)), int(bool(load_v)),
+                                                              _stream(dev)))
 
 
 def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
@@ -355,14 +367,10 @@ def plan_part_floats(B, Hq, Hkv, NBC) -> int:
     return int(_native.lib().kvskip_plan_part_floats(int(B), int(Hq), int(Hkv), int(NBC)))
 
 
-def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
-           est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0,
-           list_stats=False, seq_lens=None):
-    """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place.
-
-    list_stats (not in the reference): blk_max / blk_sum hold values only for the blocks of this
-    step's plan (the masked pass ran on unfilled buffers); the kernel derives the read set from
-    trig, keep, flags and idx and ignores the rest. Needs flags (and idx if the plan had one)."""
+def _update_args(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None,
+                 idx=None, est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None,
+                 aix_thr=0.0, list_stats=False, seq_lens=None) -> UpdateArgs:
+    """kvskip_update_args of update() (kernels/kvskip_ext.cpp:270-319), validated."""
     check_f32(blk_max, "blk_max")
     check_f32(blk_sum, "blk_sum")
     B, Hkv, NBC = keep.shape
@@ -402,9 +410,37 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
         set_flags_idx()
         p.list_stats = 1
     p.seq_lens = _seq_lens_ptr(seq_lens, B)
+    return p
+
+
+def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
+           est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0,
+           list_stats=False, seq_lens=None):
+    """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place.
+
+    list_stats (not in the reference): blk_max / blk_sum hold values only for the blocks of this
+    step's plan (the masked pass ran on unfilled buffers); the kernel derives the read set from
+    trig, keep, flags and idx and ignores the rest. Needs flags (and idx if the plan had one)."""
+    p = _update_args(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags, idx,
+                     est, calib, calib_rate, calib_free, calib_kind, aix, aix_thr, list_stats, seq_lens)
     dev = keep.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_update(ctypes.byref(p), _stream(dev)))
+
+
+def merge_update(q, k, v, scale, bufs: dict, num_splits, update_args: tuple, update_kwargs: dict,
+                 block_idx=None, block_cnt=None, seq_lens=None):
+    """The split merge of a decode_into(..., phase=1) pass (same q, k, v, bufs, list, num_splits >= 2)
+    and update(*update_args, **update_kwargs), in one launch (kvskip_merge_update; not in the
+    reference)."""
+    B, Hq, D = q.shape
+    _require(num_splits >= 2, "merge_update needs num_splits >= 2")
+    a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], None, None, None,
+                     None, bufs["part_acc"], bufs["part_ml"], seq_lens)
+    u = _update_args(*update_args, **update_kwargs)
+    dev = q.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_merge_update(ctypes.byref(a), ctypes.byref(u), _stream(dev)))
 
 
 def read_bw(x, out, blocks):

@@ -4,10 +4,9 @@ device too (the reference runs its Python planner for it, src/kvskip_attn.py:445
 
 Per decode step: plan (estimate, refresh decision, block list) -> masked + block-statistics
 attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
-Three kernel launches per layer-step (four with the split merge), all on the current stream, no
-host synchronisation, no allocation after the first step of a capacity: the pass writes into
-buffers the planner owns, and its statistics need no -inf / 0 fill because update reads only
-the blocks the plan listed (list_stats).
+Four launches per layer-step (plan: scores + decide; the split pass; the split merge and update
+together), all on the current stream, no host synchronisation, no allocation after the first step
+of a capacity: the pass writes into buffers the planner owns.
 
 The policy fields follow KvskipConfig (src/kvskip_attn.py:116-147) for one layer.
 """
@@ -119,8 +118,9 @@ class FusedPlanner:
         self.NBC = NBC
 
     def _attend(self, q, k, v, scale, nb, seq_lens=None):
-        """Masked + statistics pass over the plan's lists into the planner's buffers. Returns
-        out [B, Hq, D] (valid until the next step) and the [B, Hq, nb] statistics views."""
+        """Split pass (masked + statistics) over the plan's lists into the planner's buffers.
+        Returns out [B, Hq, D] (valid until the next step; written by _finish when the pass is
+        split) and the [B, Hq, nb] statistics views."""
         B, Hq, D = q.shape
         Hkv = k.shape[1]
         S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb)
@@ -134,9 +134,21 @@ class FusedPlanner:
                                  blk_sum=torch.empty(n_st, **f32), part_acc=torch.empty(n_part, **f32),
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
-        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, seq_lens=seq_lens)
+        self._S = S
+        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, seq_lens=seq_lens,
+                      phase=1 if S > 1 else 3)
         n = B * Hq * nb
         return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
+
+    def _finish(self, q, k, v, scale, seq_lens, update_args, update_kwargs):
+        """The pass's split merge and the planner update: one launch (kvskip_merge_update) when
+        the pass was split, else the update alone."""
+        s = self.state
+        if self._S > 1:
+            E.merge_update(q, k, v, scale, self.bufs, self._S, update_args, update_kwargs, s["block_idx"],
+                           s["block_cnt"], seq_lens)
+        else:
+            E.update(*update_args, **update_kwargs)
 
     def _count(self, key, value):
         if self.count:
@@ -179,8 +191,9 @@ class FusedPlanner:
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
                int(pol.local), False, part=s["part"], seq_lens=seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
-        E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
-                 float(pol.level), int(pol.local), every, list_stats=True, seq_lens=seq_lens)
+        self._finish(q, k, v, scale, seq_lens,
+                     (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
+                      float(pol.level), int(pol.local), every), dict(list_stats=True, seq_lens=seq_lens))
         self.t, self.T = 0, T
         self.ragged = seq_lens is not None
         if self.count:
@@ -223,11 +236,12 @@ class FusedPlanner:
                cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None,
                part=s["part"], seq_lens=seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
-        E.update(bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
-                 float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
-                 float(pol.calib or 0.0), bool(pol.calib_free), kind,
-                 s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0),
-                 list_stats=True, seq_lens=seq_lens)
+        self._finish(q, k, v, scale, seq_lens,
+                     (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
+                      float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
+                      float(pol.calib or 0.0), bool(pol.calib_free), kind,
+                      s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0)),
+                     dict(list_stats=True, seq_lens=seq_lens))
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
             self._count("blocks_total", B * Hkv * nb if seq_lens is None

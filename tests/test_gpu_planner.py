@@ -224,3 +224,45 @@ def test_planner_loop(gpu, name):
 def test_planner_loop_gqa7_batch(gpu):
     """Config 5 shape (28 / 4 heads, G 7) at batch 3 with the stage-4 policy."""
     _run_loop(POLICIES["stage4"], G=7, Hkv=4, B=3, T0=2500, steps=30, seed=5, p_jump=0.05)
+
+
+def test_merge_update_matches_separate_launches(gpu):
+    """kvskip_merge_update (split merge + planner update in one launch) against the split merge and
+    the update launched separately, on the same split pass: bit-identical output and state."""
+    run = W.planner_run(layers=1, B=2, Hq=28, Hkv=4, D=128, T0=3000, steps=4, seed=31)
+    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8))
+    qp = W.QueryProcess(run, 0, p_jump=0.3)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    fp = FusedPlanner(dpolicy(pol))
+    T = run.T0[0] + 1
+    fp.first(qp.next().cuda(), k[:, :, :T], v[:, :, :T], run.scale)
+    T += 1
+    q = qp.next().cuda()
+    s = fp.state
+    nb = O.nblocks(T)
+    E.plan(q, k[:, :, :T], s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"],
+           s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], run.scale, pol.delta, 32, pol.local, True, None,
+           s["calib"], s["est"], True, OP.KINDS["peak"], None, part=s["part"])
+    s["trig"][0, 1] = 1                                           # at least one refreshing head
+    out, bmax, bsum = fp._attend(q, k[:, :, :T], v[:, :, :T], run.scale, nb)
+    assert fp._S > 1
+    mut = ("keep", "lse_ref", "cs_ref", "lse_att", "calib")
+    alt = {key: s[key].clone() for key in mut}
+
+    def uargs(st):
+        return ((bmax, bsum, s["trig"], s["cs_now"], st["keep"], st["lse_ref"], st["cs_ref"], st["lse_att"], T,
+                 pol.level, pol.local, s["flags"], None, s["est"], st["calib"], pol.calib, pol.calib_free,
+                 OP.KINDS["peak"]), dict(list_stats=True))
+
+    a, kw = uargs(s)
+    E.merge_update(q, k[:, :, :T], v[:, :, :T], run.scale, fp.bufs, fp._S, a, kw, s["block_idx"], s["block_cnt"])
+    out_f, lse_f = fp.bufs["out"].clone(), fp.bufs["lse"].clone()
+    fp.bufs["out"].zero_()
+    fp.bufs["lse"].zero_()
+    E.decode_into(q, k[:, :, :T], v[:, :, :T], run.scale, fp.bufs, s["block_idx"], s["block_cnt"], stats=False,
+                  num_splits=fp._S, phase=2)
+    assert torch.equal(fp.bufs["out"], out_f) and torch.equal(fp.bufs["lse"], lse_f)
+    a, kw = uargs(alt)
+    E.update(*a, **kw)
+    for key in mut:
+        assert torch.equal(alt[key], s[key]), key
