@@ -6,35 +6,41 @@ namespace kvs {
 namespace {
 
 // Masked statistics of the blocks the list skips: (-inf, 0), so the outputs need no fill. The
-// split holding list positions [i0, i0 + n) writes the gaps before each of its entries (from the
+// split holding list positions [i0, i0 + n) writes the gap before each of its entries (from the
 // previous entry, or from block 0) and, if it holds the list's last entry, the tail up to nb;
 // an empty list is written by split 0. Every unlisted block falls to exactly one split.
-// Thread t < NT has the entries of position i0 + t and the one before it loaded (prev, cur).
+// Wavefront w takes positions i0 + w + NWAVE j; its lane j < 64 holds that entry and the one
+// before it (cur0, prev0: loaded at the start of the pass, written after it, so these stores
+// overlap the partial results' instead of delaying them).
 template <int G>
 __device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, int i0, int n, int split,
-                                int64_t hq0, int tid, int prev0, int cur0) {
-  auto put = [&](int blk) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
-      p.blk_sum[(hq0 + g) * p.nb + blk] = 0.f;
-    }
+                                int64_t hq0, int wave, int lane, int prev0, int cur0) {
+  auto put = [&](int g, int blk) {
+    p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
+    p.blk_sum[(hq0 + g) * p.nb + blk] = 0.f;
   };
+  const int tid = wave * WAVE + lane;
   if (n_items == 0) {
     if (split == 0)
-      for (int blk = tid; blk < p.nb; blk += NT) put(blk);
+      for (int x = tid; x < G * p.nb; x += NT) put(x / p.nb, x % p.nb);
     return;
   }
-  for (int t = tid; t < n; t += NT) {
-    const int k = i0 + t;
-    const int cur = t < NT ? cur0 : list[k];
-    const int prev = t < NT ? prev0 : list[k - 1];
-    const int a = max(prev, -1) + 1, e = min(cur, p.nb);
-    for (int blk = a; blk < e; ++blk) put(blk);
+  for (int j = 0; wave + NWAVE * j < n; ++j) {  // uniform over the wavefront
+    int prev, cur;
+    if (j < WAVE) {
+      prev = __builtin_amdgcn_readlane(prev0, j);
+      cur = __builtin_amdgcn_readlane(cur0, j);
+    } else {
+      const int k = i0 + wave + NWAVE * j;
+      cur = __builtin_amdgcn_readfirstlane(list[k]);
+      prev = __builtin_amdgcn_readfirstlane(list[k - 1]);
+    }
+    const int a = max(prev, -1) + 1, len = min(cur, p.nb) - a;
+    for (int x = lane; x < G * len; x += WAVE) put(x / len, a + x % len);
   }
   if (n > 0 && i0 + n == n_items) {
-    const int last = min(max(list[n_items - 1], -1), p.nb - 1);
-    for (int blk = last + 1 + tid; blk < p.nb; blk += NT) put(blk);
+    const int a = min(max(list[n_items - 1], -1), p.nb - 1) + 1, len = p.nb - a;
+    for (int x = tid; x < G * len; x += NT) put(x / len, a + x % len);
   }
 }
 
@@ -89,11 +95,12 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
   }
   const int* list = MASKED ? p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks : nullptr;
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
-  int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this thread's gap
+  int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this lane's gap
   if constexpr (MASKED && STATS) {
-    if (tid < n) {
-      gap_cur = list[i0 + tid];
-      gap_prev = i0 + tid > 0 ? list[i0 + tid - 1] : -1;
+    const int t = wave + NWAVE * lane;
+    if (t < n) {
+      gap_cur = list[i0 + t];
+      gap_prev = i0 + t > 0 ? list[i0 + t - 1] : -1;
     }
   }
 
@@ -109,9 +116,12 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   float* sPw = sP[wave];
 
-  // Block of this wavefront's k-th item; out-of-range list entries read block 0 and are masked.
-  auto block_of = [&](int k) -> int {  // uniform over the wavefront
-    const int blk = __builtin_amdgcn_readfirstlane(MASKED ? list[i0 + wave + NWAVE * k] : i0 + wave + NWAVE * k);
+  // List entry of this wavefront's k-th item (k clamped to its items): a vector load whose value is
+  // used two items later, so that waiting for it never waits for the block loads issued after it.
+  auto entry_of = [&](int k) -> int { return MASKED ? list[i0 + wave + NWAVE * min(k, nw - 1)] : 0; };
+  // Block of the k-th item from its entry; out-of-range entries read block 0 and are masked.
+  auto block_of = [&](int e, int k) -> int {  // uniform over the wavefront
+    const int blk = __builtin_amdgcn_readfirstlane(MASKED ? e : i0 + wave + NWAVE * k);
     return (blk >= 0 && blk < nbb) ? blk : -1;
   };
   auto accumulate = [&](const u32x4 (&vr)[Lay<D>::VN], const float (&alpha)[G]) {
@@ -197,11 +207,14 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     if (nw > 0) {
       u32x4 kr[4][KS];
       u32x4 vr[Lay<D>::VN];
-      int blk = block_of(0);
+      int e_n = entry_of(1);
+      int blk = block_of(entry_of(0), 0);
       load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk, 0) * BLK);
       if constexpr (LOAD_V) load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
       for (int k = 0; k + 1 < nw; ++k) {
-        const int blk_n = block_of(k + 1);
+        const int e_nn = entry_of(k + 2);
+        const int blk_n = block_of(e_n, k + 1);
+        e_n = e_nn;
         float alpha[G];
         process(blk, kr, alpha);
         __builtin_amdgcn_sched_barrier(0);
@@ -265,10 +278,13 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
     if (nw > 0) {
       u32x4 kr[8][Lay<D>::KC];
       u32x4 vr[Lay<D>::VN];
-      int blk = block_of(0);
+      int e_n = entry_of(1);
+      int blk = block_of(entry_of(0), 0);
       load_k_block<D>(kr, rk, koff, p.k_st, max(blk, 0) * BLK);
       for (int k = 0; k + 1 < nw; ++k) {
-        const int blk_n = block_of(k + 1);
+        const int e_nn = entry_of(k + 2);
+        const int blk_n = block_of(e_n, k + 1);
+        e_n = e_nn;
         float alpha[G];
         process(blk, kr, alpha);
         __builtin_amdgcn_sched_barrier(0);
@@ -286,7 +302,8 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
       }
     }
   }
-  if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, tid, gap_prev, gap_cur);
+  finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
+  if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
   if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
     if (nbb < p.nb && i0 + n == n_items) {
       for (int t = tid; t < G * (p.nb - nbb); t += NT) {
@@ -296,7 +313,6 @@ __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
       }
     }
   }
-  finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
 }
 
 template <int D, int G, bool M, bool ST, bool LV>
