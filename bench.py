@@ -411,7 +411,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     from kvskip_amd import ext as E
     from kvskip_amd import kvskip as K
     from kvskip_amd import workloads as W
-    from kvskip_amd.planner import FusedPlanner, Policy
+    from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
 
     t_gen = time.perf_counter()
     run = W.planner_run(layers=layers, B=B, Hq=Hq, Hkv=Hkv, T0=T0, steps=steps, seed=seed, ragged=ragged, device=dev)
@@ -457,9 +457,11 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
                 planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t], seq_lens=sl_all[t])
 
     # eager pass with counters
-    planners = [None] * first_planned + [FusedPlanner(pol) for _ in range(first_planned, layers)]
+    carrier = UpdateCarrier()
+    planners = [None] * first_planned + [FusedPlanner(pol, carrier=carrier) for _ in range(first_planned, layers)]
     for t in range(steps):
         planner_pass(planners, t)
+    carrier.flush()
     torch.cuda.synchronize()
     pl = planners[first_planned:]
     read = sum(float(p.counters["blocks_read"]) for p in pl)
@@ -468,20 +470,24 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     head_steps = len(pl) * (steps - 1) * B * Hkv
     log(f"{tag} eager: blocks read {read / total:.3f}, refresh rate {refresh / head_steps:.3f}")
 
-    def capture(fn_step, t0, t1):
+    def capture(fn_step, t0, t1, tail=None):
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
             for t in range(t0, t1):
                 fn_step(t)
+            if tail is not None:
+                tail()
         return g
 
-    def timed(fn_step, init=None):
+    def timed(fn_step, init=None, tail=None):
+        """tail: launches that close the last step (a carried update still pending), in the last graph."""
         if init is not None:
             init()
         torch.cuda.synchronize()
-        graphs = [capture(fn_step, t0, min(steps, t0 + chunk)) for t0 in range(1, steps, chunk)]
+        graphs = [capture(fn_step, t0, min(steps, t0 + chunk), tail if t0 + chunk >= steps else None)
+                  for t0 in range(1, steps, chunk)]
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -491,8 +497,15 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3          # us for steps 1 .. steps-1, all layers
 
+    # timed: updates carried by the next layer's pass (the loop's default form here), then beside
+    # the merge of their own layer
+    carrier = UpdateCarrier()
+    planners = [None] * first_planned + [FusedPlanner(pol, count=False, carrier=carrier)
+                                         for _ in range(first_planned, layers)]
+    us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0), tail=carrier.flush)
+    del planners
     planners = [None] * first_planned + [FusedPlanner(pol, count=False) for _ in range(first_planned, layers)]
-    us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
+    us_plan_own = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
     out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
@@ -501,11 +514,13 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
                      + (", layer 0 dense" if dense_layer0 else ""),
            "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
+           "us_per_layer_step_policy_update_own_launch": us_plan_own / n,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
-    log(f"{tag}: policy {us_plan / n:.2f} us/layer-step vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), "
-        f"{us_plan / (steps - 1) / 1e3:.3f} ms per {layers}-layer step")
+    log(f"{tag}: policy {us_plan / n:.2f} us/layer-step (updates carried; {us_plan_own / n:.2f} with their own "
+        f"launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
+        f"{layers}-layer step")
     del planners, run, qs
     return out
 

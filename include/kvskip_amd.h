@@ -196,6 +196,15 @@ int kvskip_update(const kvskip_update_args* p, void* stream);
  * the reference: the device planner loop's pass ends this way (kvskip_decode_splits, then this). */
 int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream);
 
+/* kvskip_decode_splits of a masked + statistics pass (block list, stats, load_v; with
+ * num_splits == 1 the whole op) and kvskip_update u of ANOTHER layer, in one launch. Not in the
+ * reference: a layer's update only reads that layer's statistics and is only read by that
+ * layer's next plan, so the device planner loop runs it inside the next layer's pass (under its
+ * streaming) instead of in a launch of its own. u and a must not share outputs; u's group size
+ * equals a's. Updates over more than 1024 blocks, or with the VALU engine selected, run as two
+ * launches (same results). */
+int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream);
+
 /* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
  * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums
  * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. seq_lens: optional

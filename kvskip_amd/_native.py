@@ -75,6 +75,7 @@ SIGNATURES = {
     "kvskip_plan_part_floats": ([c_int32, c_int32, c_int32, c_int32], c_int64),
     "kvskip_update": ([POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_merge_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
+    "kvskip_decode_splits_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_int32, c_void_p, c_void_p], c_int),
     "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),

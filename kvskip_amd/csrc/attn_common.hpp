@@ -66,17 +66,21 @@ constexpr int gpad() {
   return G <= 4 ? 4 : 8;
 }
 
-// Work coordinates of this workgroup: the launch index i is dispatched to XCD i % 8; work item
-// Launch index -> work index, XCD-aware (consecutive work on one XCD) when n % 8 == 0.
+// Launch index -> work index, XCD-aware when n % 8 == 0: launch index i is dispatched to XCD
+// i % 8, and w = (i % 8) * (n / 8) + i / 8 gives each XCD a contiguous run of work items (a
+// launch whose first workgroups do other work only rotates which XCD holds which run).
 __device__ __forceinline__ int xcd_remap(int i, int n) { return n % 8 == 0 ? (i % 8) * (n / 8) + i / 8 : i; }
 
-// w = (i % 8) * (n / 8) + i / 8 gives each XCD a contiguous run of work items.
-__device__ __forceinline__ void work_coords(int S, int Hkv, int B, int& split, int& h, int& b) {
-  const int i = xcd_remap(blockIdx.x, S * Hkv * B);
+// Work coordinates (split, KV head, sequence) of decode workgroup `bid`.
+__device__ __forceinline__ void work_coords(int bid, int S, int Hkv, int B, int& split, int& h, int& b) {
+  const int i = xcd_remap(bid, S * Hkv * B);
   split = i % S;
   const int r = i / S;
   h = r % Hkv;
   b = r / Hkv;
+}
+__device__ __forceinline__ void work_coords(int S, int Hkv, int B, int& split, int& h, int& b) {
+  work_coords(blockIdx.x, S, Hkv, B, split, h, b);
 }
 
 // ---- Ragged batches (seq_lens): sequence b attends tokens [0, clamp(seq_lens[b], 1, T)).

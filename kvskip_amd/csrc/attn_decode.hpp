@@ -1,0 +1,322 @@
+// Split-K decode attention, the body of one workgroup: dense or over block lists, with optional
+// per-block statistics, stats-only (K only) and fp16 P; both QK engines (MFMA, VALU dot2). Used
+// by the decode kernels and by the planner's split pass that carries an update.
+#pragma once
+#include "attn_common.hpp"
+
+namespace kvs {
+namespace {
+
+// Masked statistics of the blocks the list skips: (-inf, 0), so the outputs need no fill. The
+// split holding list positions [i0, i0 + n) writes the gap before each of its entries (from the
+// previous entry, or from block 0) and, if it holds the list's last entry, the tail up to nb;
+// an empty list is written by split 0. Every unlisted block falls to exactly one split.
+// Wavefront w takes positions i0 + w + NWAVE j; its lane j < 64 holds that entry and the one
+// before it (cur0, prev0: loaded at the start of the pass, written after it, so these stores
+// overlap the partial results' instead of delaying them).
+template <int G>
+__device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, int i0, int n, int split,
+                                int64_t hq0, int wave, int lane, int prev0, int cur0) {
+  auto put = [&](int g, int blk) {
+    p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
+    p.blk_sum[(hq0 + g) * p.nb + blk] = 0.f;
+  };
+  const int tid = wave * WAVE + lane;
+  if (n_items == 0) {
+    if (split == 0)
+      for (int x = tid; x < G * p.nb; x += NT) put(x / p.nb, x % p.nb);
+    return;
+  }
+  for (int j = 0; wave + NWAVE * j < n; ++j) {  // uniform over the wavefront
+    int prev, cur;
+    if (j < WAVE) {
+      prev = __builtin_amdgcn_readlane(prev0, j);
+      cur = __builtin_amdgcn_readlane(cur0, j);
+    } else {
+      const int k = i0 + wave + NWAVE * j;
+      cur = __builtin_amdgcn_readfirstlane(list[k]);
+      prev = __builtin_amdgcn_readfirstlane(list[k - 1]);
+    }
+    const int a = max(prev, -1) + 1, len = min(cur, p.nb) - a;
+    for (int x = lane; x < G * len; x += WAVE) put(x / len, a + x % len);
+  }
+  if (n > 0 && i0 + n == n_items) {
+    const int a = min(max(list[n_items - 1], -1), p.nb - 1) + 1, len = p.nb - a;
+    for (int x = tid; x < G * len; x += NT) put(x / len, a + x % len);
+  }
+}
+
+// The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads.
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG>
+__device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
+  constexpr int GP = gpad<G>();
+  __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
+  __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
+
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+  const int r8 = lane >> 3, sub = lane & 7;
+
+  // This workgroup's work: (b, KV head h, split) and list positions / blocks [i0, i0 + n) of the
+  // n_items of (b, h); Tb, nbb: the sequence's tokens and blocks.
+  int split, h, b, n_items, i0, n;
+  int Tb = p.T, nbb = p.nb;
+  if constexpr (!RAG) {
+    work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
+    n_items = MASKED ? min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks) : p.nb;
+    const int per = (n_items + p.num_splits - 1) / p.num_splits;
+    i0 = min(n_items, split * per);
+    n = min(n_items, i0 + per) - i0;
+  } else {  // ragged: chunks of C items over the whole batch, per KV head
+    const int W = p.num_splits + p.B;
+    const int it = xcd_remap(bid, W * p.Hkv);
+    h = it / W;
+    int chunk;
+    const int C = ragged_lookup(p, h, it % W, MASKED, b, chunk, n_items);
+    if constexpr (MASKED && STATS) {
+      if (it % W == 0) {  // (b', h) with an empty list have no chunk: their statistics are written here
+        for (int b0 = wave * WAVE; b0 < p.B; b0 += NT) {
+          const int bb = b0 + lane;
+          uint64_t empty = __ballot(bb < p.B && ragged_items(p, bb, h, true) == 0);
+          while (empty != 0) {
+            const int be = b0 + __ffsll(static_cast<unsigned long long>(empty)) - 1;
+            empty &= empty - 1;
+            const int64_t q0 = static_cast<int64_t>(be) * p.Hq + static_cast<int64_t>(h) * G;
+            for (int t = lane; t < G * p.nb; t += WAVE) {
+              p.blk_max[(q0 + t / p.nb) * p.nb + t % p.nb] = NEG_INF;
+              p.blk_sum[(q0 + t / p.nb) * p.nb + t % p.nb] = 0.f;
+            }
+          }
+        }
+      }
+    }
+    if (b < 0) return;
+    split = chunk;
+    i0 = chunk * C;
+    n = min(n_items, i0 + C) - i0;
+    Tb = seq_len(p, b);
+    nbb = (Tb + BLK - 1) / BLK;
+  }
+  const int* list = MASKED ? p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks : nullptr;
+  const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
+  int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this lane's gap
+  if constexpr (MASKED && STATS) {
+    const int t = wave + NWAVE * lane;
+    if (t < n) {
+      gap_cur = list[i0 + t];
+      gap_prev = i0 + t > 0 ? list[i0 + t - 1] : -1;
+    }
+  }
+
+  const rsrc_t rk = make_rsrc(p.k + b * p.k_sb + h * p.k_sh, head_bytes(Tb, p.k_st, D));
+  const rsrc_t rv = make_rsrc(p.v + b * p.v_sb + h * p.v_sh, LOAD_V ? head_bytes(Tb, p.v_st, D) : 0);
+  const uint32_t voff = static_cast<uint32_t>((lane / Lay<D>::VLPR) * p.v_st * 2 + 16 * (lane % Lay<D>::VLPR));
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  float* sPw = sP[wave];
+
+  // List entry of this wavefront's k-th item (k clamped to its items): a vector load whose value is
+  // used two items later, so that waiting for it never waits for the block loads issued after it.
+  auto entry_of = [&](int k) -> int { return MASKED ? list[i0 + wave + NWAVE * min(k, nw - 1)] : 0; };
+  // Block of the k-th item from its entry; out-of-range entries read block 0 and are masked.
+  auto block_of = [&](int e, int k) -> int {  // uniform over the wavefront
+    const int blk = __builtin_amdgcn_readfirstlane(MASKED ? e : i0 + wave + NWAVE * k);
+    return (blk >= 0 && blk < nbb) ? blk : -1;
+  };
+  auto accumulate = [&](const u32x4 (&vr)[Lay<D>::VN], const float (&alpha)[G]) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= alpha[g];
+    pv_block<D, G>(acc, vr, sPw, lane);
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  float m[G], l[G];
+  if constexpr (MF) {
+    // ---- MFMA engine: K(j) and V(j) both prefetched one block ahead.
+    constexpr int KS = MLay<D>::KS;
+    constexpr int NI = G < 4 ? G : 4;               // score rows i in use per lane group
+    const int j4 = lane >> 4, c16 = lane & 15;
+    const uint32_t koffm = static_cast<uint32_t>(c16 * p.k_st * 2 + 16 * j4);
+    // statistics and P of this (b, KV head) through buffer resources: one 32-bit offset per lane
+    // (head 4 j4 + i: + i * row bytes), the block in the scalar offset
+    const uint32_t nb4 = 4u * static_cast<uint32_t>(p.nb), tp2 = 2u * static_cast<uint32_t>(p.t_pad);
+    const rsrc_t rs_max = make_rsrc(STATS ? p.blk_max + hq0 * p.nb : nullptr, STATS ? G * nb4 : 0);
+    const rsrc_t rs_sum = make_rsrc(STATS ? p.blk_sum + hq0 * p.nb : nullptr, STATS ? G * nb4 : 0);
+    const rsrc_t rs_p = make_rsrc(STATS && p.p_out != nullptr ? p.p_out + hq0 * p.t_pad : nullptr,
+                                  STATS && p.p_out != nullptr ? G * tp2 : 0);
+    const uint32_t v_stat = 4u * j4 * nb4, v_p = 4u * j4 * tp2 + 2u * c16;
+    u32x4 qa[KS];
+    load_q_mf<D, G>(qa, p, b, h, lane);
+    float mr[4], lr[4];                             // running (m, l) of head 4 j4 + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mr[i] = NEG_INF;
+      lr[i] = 0.f;
+    }
+    auto process = [&](int blk, const u32x4 (&kr)[4][KS], float (&alpha)[G]) {
+      const int t0 = blk >= 0 ? blk * BLK : 0;
+      float s[4][4];
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, blk >= 0 ? Tb : 0, lane);
+      float pv[4][4], ar[4];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int g = 4 * j4 + i;
+        const float mt = row16_max(fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i])));
+        const float mtu = mt == NEG_INF ? 0.f : mt;
+        float e[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) e[nt] = fexp2(s[nt][i] - mtu);
+        const float st = row16_sum((e[0] + e[1]) + (e[2] + e[3]));
+        const float m_new = fmaxf(mr[i], mt);
+        const float mu = m_new == NEG_INF ? 0.f : m_new;
+        ar[i] = fexp2(mr[i] - mu);
+        const float cf = mt == NEG_INF ? 0.f : fexp2(mt - mu);
+        lr[i] = lr[i] * ar[i] + st * cf;
+        mr[i] = m_new;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) pv[nt][i] = e[nt] * cf;
+        if constexpr (STATS) {
+          if (blk >= 0 && g < G) {
+            if (c16 == 0) {
+              bstore_f32(mt * LN2, rs_max, v_stat + i * nb4, 4 * blk);
+              bstore_f32(st, rs_sum, v_stat + i * nb4, 4 * blk);
+            }
+            if (p.p_out != nullptr) {
+#pragma unroll
+              for (int nt = 0; nt < 4; ++nt) bstore_u16(f2h(e[nt]), rs_p, v_p + i * tp2 + 32 * nt, 2 * t0);
+            }
+          }
+        }
+      }
+      if constexpr (LOAD_V) {
+        if (4 * j4 < GP) {
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt)
+            *reinterpret_cast<float4*>(sPw + (16 * nt + c16) * GP + 4 * j4) =
+                make_float4(pv[nt][0], NI > 1 ? pv[nt][1] : 0.f, NI > 2 ? pv[nt][2] : 0.f, NI > 3 ? pv[nt][3] : 0.f);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) alpha[g] = lane_value(ar[g % 4], 16 * (g / 4));
+    };
+    if (nw > 0) {
+      u32x4 kr[4][KS];
+      u32x4 vr[Lay<D>::VN];
+      int e_n = entry_of(1);
+      int blk = block_of(entry_of(0), 0);
+      load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk, 0) * BLK);
+      if constexpr (LOAD_V) load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+      for (int k = 0; k + 1 < nw; ++k) {
+        const int e_nn = entry_of(k + 2);
+        const int blk_n = block_of(e_n, k + 1);
+        e_n = e_nn;
+        float alpha[G];
+        process(blk, kr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk_n, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) {
+          accumulate(vr, alpha);
+          __builtin_amdgcn_sched_barrier(0);
+          load_v_block<D>(vr, rv, voff, p.v_st, max(blk_n, 0) * BLK);
+        }
+        blk = blk_n;
+      }
+      float alpha[G];
+      process(blk, kr, alpha);
+      if constexpr (LOAD_V) accumulate(vr, alpha);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = lane_value(mr[g % 4], 16 * (g / 4));
+      l[g] = lane_value(lr[g % 4], 16 * (g / 4));
+    }
+  } else {
+    // ---- VALU engine: V(j) issued after QK(j), together with K(j+1) (register budget).
+    const uint32_t koff = static_cast<uint32_t>(r8 * p.k_st * 2 + 16 * sub);
+    u32x4 qv[G][Lay<D>::KC];
+    load_q<D, G>(qv, p, b, h, lane);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = NEG_INF;
+      l[g] = 0.f;
+    }
+    auto process = [&](int blk, const u32x4 (&kr)[8][Lay<D>::KC], float (&alpha)[G]) {
+      const int t0 = blk >= 0 ? blk * BLK : 0;
+      float s[8][G];
+      qk_block<D, G>(s, kr, qv, p.scale_log2, t0, blk >= 0 ? Tb : 0, lane);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float e[8], mt, st, c;
+        block_softmax<G>(s, g, m[g], l[g], e, mt, st, alpha[g], c);
+        if constexpr (STATS) {
+          if (blk >= 0) {
+            const int64_t hq = hq0 + g;
+            if (lane == 0) {
+              p.blk_max[hq * p.nb + blk] = mt * LN2;
+              p.blk_sum[hq * p.nb + blk] = st;
+            }
+            if (p.p_out != nullptr && sub == g) {
+#pragma unroll
+              for (int rg = 0; rg < 8; ++rg) p.p_out[hq * p.t_pad + t0 + 8 * rg + r8] = f2h(e[rg]);
+            }
+          }
+        }
+        if constexpr (LOAD_V) {
+          if (sub == 0) {
+#pragma unroll
+            for (int rg = 0; rg < 8; ++rg) sPw[(8 * rg + r8) * GP + g] = e[rg] * c;
+          }
+        }
+      }
+    };
+    if (nw > 0) {
+      u32x4 kr[8][Lay<D>::KC];
+      u32x4 vr[Lay<D>::VN];
+      int e_n = entry_of(1);
+      int blk = block_of(entry_of(0), 0);
+      load_k_block<D>(kr, rk, koff, p.k_st, max(blk, 0) * BLK);
+      for (int k = 0; k + 1 < nw; ++k) {
+        const int e_nn = entry_of(k + 2);
+        const int blk_n = block_of(e_n, k + 1);
+        e_n = e_nn;
+        float alpha[G];
+        process(blk, kr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+        load_k_block<D>(kr, rk, koff, p.k_st, max(blk_n, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LOAD_V) accumulate(vr, alpha);
+        blk = blk_n;
+      }
+      float alpha[G];
+      process(blk, kr, alpha);
+      if constexpr (LOAD_V) {
+        load_v_block<D>(vr, rv, voff, p.v_st, max(blk, 0) * BLK);
+        accumulate(vr, alpha);
+      }
+    }
+  }
+  finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
+  if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
+  if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
+    if (nbb < p.nb && i0 + n == n_items) {
+      for (int t = tid; t < G * (p.nb - nbb); t += NT) {
+        const int64_t i = (hq0 + t / (p.nb - nbb)) * p.nb + nbb + t % (p.nb - nbb);
+        p.blk_max[i] = NEG_INF;
+        p.blk_sum[i] = 0.f;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace kvs

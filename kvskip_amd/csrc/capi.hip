@@ -117,9 +117,9 @@ int kvskip_struct_size(int which) {
   }
 }
 
-static int decode_phases(const kvskip_attn_args* a, int stats, int load_v, int phase, void* stream) {
-  kvs::AttnP p;
-  int rc = prepare_attn(a, true, true, load_v != 0, &p);
+// Checks of a decode launch (phase: 3 the op, 1 its split pass, 2 its merge) into *p.
+static int check_decode(const kvskip_attn_args* a, int stats, int load_v, int phase, kvs::AttnP* p) {
+  int rc = prepare_attn(a, true, true, load_v != 0, p);
   if (rc != KVSKIP_OK) return rc;
   if (!load_v && !stats) return fail(KVSKIP_E_INVALID, "load_v=false only makes sense with stats=true");
   if (a->p_out != nullptr && !stats) return fail(KVSKIP_E_INVALID, "write_p needs stats=true");
@@ -139,9 +139,16 @@ static int decode_phases(const kvskip_attn_args* a, int stats, int load_v, int p
     if (a->B > kvs::MAX_RAGGED_B) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: B <= %d", kvs::MAX_RAGGED_B);
     if (a->p_out != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: no fp16 P output");
   }
-  if (!load_v) p.out = nullptr;
+  if (!load_v) p->out = nullptr;
+  return KVSKIP_OK;
+}
+
+static int decode_phases(const kvskip_attn_args* a, int stats, int load_v, int phase, void* stream) {
+  kvs::AttnP p;
+  const int rc = check_decode(a, stats, load_v, phase, &p);
+  if (rc != KVSKIP_OK) return rc;
   const int G = a->Hq / a->Hkv;
-  return launched(kvs::launch_decode(p, a->D, G, masked, stats != 0, load_v != 0, phase,
+  return launched(kvs::launch_decode(p, a->D, G, a->block_idx != nullptr, stats != 0, load_v != 0, phase,
                                      static_cast<hipStream_t>(stream)),
                   "kvskip_decode");
 }
@@ -265,6 +272,17 @@ int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, 
   if (a->B != u->B || a->Hq != u->Hq || a->Hkv != u->Hkv || a->T != u->T)
     return fail(KVSKIP_E_INVALID, "merge_update: attention and update shapes differ");
   return launched(kvs::launch_merge_update(p, *u, a->D, static_cast<hipStream_t>(stream)), "kvskip_merge_update");
+}
+
+int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream) {
+  kvs::AttnP p;
+  int rc = check_decode(a, 1, 1, a != nullptr && a->num_splits > 1 ? 1 : 3, &p);
+  if (rc != KVSKIP_OK) return rc;
+  if ((rc = check_update(u)) != KVSKIP_OK) return rc;
+  if (a->block_idx == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_update: the pass needs a block list");
+  if (a->Hq / a->Hkv != u->Hq / u->Hkv)
+    return fail(KVSKIP_E_INVALID, "decode_splits_update: the pass and the update have different group sizes");
+  return launched(kvs::launch_split_update(p, *u, a->D, static_cast<hipStream_t>(stream)), "kvskip_decode_splits_update");
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,

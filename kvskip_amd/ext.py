@@ -443,6 +443,46 @@ def merge_update(q, k, v, scale, bufs: dict, num_splits, update_args: tuple, upd
         _native.check(_native.lib().kvskip_merge_update(ctypes.byref(a), ctypes.byref(u), _stream(dev)))
 
 
+def update_struct(*update_args, **update_kwargs) -> UpdateArgs:
+    """The argument block of update(*update_args, **update_kwargs), checked, for a later launch
+    (decode_splits_update, launch_update); it holds raw pointers, so the tensors must outlive its use."""
+    return _update_args(*update_args, **update_kwargs)
+
+
+def launch_update(update: UpdateArgs, device):
+    """update() from an update_struct, on the current stream of `device`."""
+    dev = torch.device(device)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_update(ctypes.byref(update), _stream(dev)))
+
+
+def decode_splits_update(q, k, v, scale, bufs: dict, block_idx, block_cnt, num_splits, update: UpdateArgs,
+                         seq_lens=None):
+    """decode_into(..., stats=True, phase=1) over a block list (the whole op when num_splits == 1)
+    and the update of ANOTHER layer (an update_struct), in one launch (kvskip_decode_splits_update;
+    not in the reference). The update reads only its own layer's buffers."""
+    check_q(q)
+    check_kv(k, "k")
+    check_kv(v, "v")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    _require(1 <= num_splits <= 256, "num_splits in 1..256")
+    nb = (T + TILE - 1) // TILE
+    bmax, bsum = bufs["blk_max"], bufs["blk_sum"]
+    for t in (bmax, bsum):
+        _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= B * Hq * nb, "bufs: stats")
+    part_acc = part_ml = None
+    if num_splits > 1:
+        part_acc, part_ml = bufs["part_acc"], bufs["part_ml"]
+        _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
+                 "bufs: split partials")
+    a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None,
+                     None, part_acc, part_ml, seq_lens)
+    dev = q.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_decode_splits_update(ctypes.byref(a), ctypes.byref(update), _stream(dev)))
+
+
 def read_bw(x, out, blocks):
     """Streaming read of x (bandwidth ceiling), kernels/kvskip_ext.cpp:321-325."""
     _require(x.is_cuda and x.is_contiguous() and (x.numel() * x.element_size()) % 16 == 0,

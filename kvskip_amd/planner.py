@@ -6,7 +6,9 @@ Per decode step: plan (estimate, refresh decision, block list) -> masked + block
 attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
 Four launches per layer-step (plan: scores + decide; the split pass; the split merge and update
 together), all on the current stream, no host synchronisation, no allocation after the first step
-of a capacity: the pass writes into buffers the planner owns.
+of a capacity: the pass writes into buffers the planner owns. With an UpdateCarrier shared by the
+planners of a model's layers, a layer's update instead runs inside the next layer's split pass
+(one launch, kvskip_decode_splits_update) and the merge runs alone.
 
 The policy fields follow KvskipConfig (src/kvskip_attn.py:116-147) for one layer.
 """
@@ -62,13 +64,50 @@ class Policy:
         return bool(self.index_heads) or self.calib_auto_ix is not None
 
 
+class UpdateCarrier:
+    """Holds the update of the layer that stepped last until the next layer's split pass carries it
+    (kvskip_decode_splits_update): a layer's update reads only its own statistics and is read only
+    by its own next plan, so it can run under another layer's streaming. Share one carrier between
+    the FusedPlanners of a model's layers. A planner flushes its own pending update before it plans
+    again; call flush() before reading planner state on the host or from another stream. Tensors
+    handed to step() (idx, seq_lens) must stay unchanged until the update has been launched."""
+
+    def __init__(self):
+        self.pending = None          # (planner, G, UpdateArgs, tensors the struct points into)
+
+    def take(self, planner, G):
+        """The pending update if `planner`'s pass can carry it (another planner, same group size);
+        a pending update it cannot carry is launched on its own first."""
+        p = self.pending
+        if p is None:
+            return None
+        if p[0] is planner or p[1] != G:
+            self.flush()
+            return None
+        self.pending = None
+        return p[2]
+
+    def put(self, planner, G, update, refs):
+        self.flush()
+        self.pending = (planner, G, update, refs)
+
+    def flush(self, planner=None):
+        """Launch the pending update on its own (only `planner`'s, if given)."""
+        p = self.pending
+        if p is None or (planner is not None and p[0] is not planner):
+            return
+        self.pending = None
+        E.launch_update(p[2], p[3][0]["keep"].device)
+
+
 class FusedPlanner:
     """Planner state of one layer in device memory (the fields of src/kvskip_attn.py:420-432) and
     its step. Usage: out = p.first(q, k, v, scale) on the first decode step, then
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
-    def __init__(self, policy: Policy, count: bool = True):
+    def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None):
         self.policy = policy
+        self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
         self.state = None
         self.t = 0
         self.T = 0
@@ -135,15 +174,28 @@ class FusedPlanner:
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
         self._S = S
-        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, seq_lens=seq_lens,
-                      phase=1 if S > 1 else 3)
+        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
+        if carried is not None:
+            E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens)
+        else:
+            E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S,
+                          seq_lens=seq_lens, phase=1 if S > 1 else 3)
         n = B * Hq * nb
         return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
 
     def _finish(self, q, k, v, scale, seq_lens, update_args, update_kwargs):
         """The pass's split merge and the planner update: one launch (kvskip_merge_update) when
-        the pass was split, else the update alone."""
+        the pass was split, else the update alone; with a carrier, the merge alone and the update
+        left to the next layer's pass."""
         s = self.state
+        if self.carrier is not None:
+            if self._S > 1:
+                E.decode_into(q, k, v, scale, self.bufs, s["block_idx"], s["block_cnt"], stats=True,
+                              num_splits=self._S, seq_lens=seq_lens, phase=2)
+            G = q.shape[1] // k.shape[1]
+            self.carrier.put(self, G, E.update_struct(*update_args, **update_kwargs),
+                             (dict(s), self.bufs, update_args, update_kwargs))
+            return
         if self._S > 1:
             E.merge_update(q, k, v, scale, self.bufs, self._S, update_args, update_kwargs, s["block_idx"],
                            s["block_cnt"], seq_lens)
@@ -182,6 +234,7 @@ class FusedPlanner:
         B, Hq, D = q.shape
         Hkv, T = k.shape[1], k.shape[2]
         nb = math.ceil(T / TILE)
+        self.flush()
         self._alloc(q, k, nb + MARGIN)
         s = self.state
         E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens)
@@ -215,6 +268,7 @@ class FusedPlanner:
         B, Hq, D = q.shape
         Hkv, T = k.shape[1], k.shape[2]
         nb = math.ceil(T / TILE)
+        self.flush()                                                  # this layer's last update
         if nb > self.NBC:
             self._grow(nb + MARGIN)
         s = self.state
@@ -249,6 +303,11 @@ class FusedPlanner:
             self._count("masked_heads", B * Hkv)
             self._count("dense_heads", s["trig"].sum())
         return out
+
+    def flush(self):
+        """Launch this planner's update if a carrier still holds it (before reading its state)."""
+        if self.carrier is not None:
+            self.carrier.flush(self)
 
     def read_mask(self, nb):
         """Blocks read this step per (b, KV head): bool [B, Hkv, nb] (host-side view for checks)."""

@@ -1,0 +1,102 @@
+"""GPU: the planner loop with an UpdateCarrier (each layer's update launched inside the next layer's
+split pass, kvskip_decode_splits_update) against the same loop without one (update beside the
+merge, kvskip_merge_update). Same kernels' arithmetic, so the planner state must be bit-identical
+on every step and the outputs equal up to the merge kernel's summation order."""
+
+import pytest
+import torch
+
+from kvskip_amd import ext as E
+from kvskip_amd import workloads as W
+from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+
+pytestmark = pytest.mark.gpu
+
+STATE = ("keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt", "calib", "est", "aix")
+
+
+def _policy():
+    return Policy(calib=0.05, calib_kind="peak", calib_warm=(8, 4), calib_auto_ix=0.1)
+
+
+def _loop(layers, B, Hq, Hkv, D, T0, steps, seed, ragged=None):
+    run = W.planner_run(layers=layers, B=B, Hq=Hq, Hkv=Hkv, D=D, T0=T0, steps=steps, seed=seed, ragged=ragged,
+                        hot_shift=6.0)
+    ks = [k.cuda() for k in run.k]
+    vs = [v.cuda() for v in run.v]
+    ids = run.ids.to(torch.int32).cuda()
+    qps = [W.QueryProcess(run, l, p_jump=0.05, revert=True) for l in range(layers)]
+    qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
+    carrier = UpdateCarrier()
+    plain = [FusedPlanner(_policy(), count=False) for _ in range(layers)]
+    carried = [FusedPlanner(_policy(), count=False, carrier=carrier) for _ in range(layers)]
+    for t in range(steps):
+        if ragged is None:
+            T = T0 + t + 1
+            kv = [(ks[l][:, :, :T], vs[l][:, :, :T]) for l in range(layers)]
+            sl = None
+        else:
+            kv = [(ks[l], vs[l]) for l in range(layers)]
+            sl = torch.tensor([T + t + 1 for T in ragged], dtype=torch.int32, device="cuda")
+        for l in range(layers):
+            for fp in (plain[l], carried[l]):
+                if t == 0:
+                    out = fp.first(qs[t][l], *kv[l], run.scale, seq_lens=sl)
+                else:
+                    out = fp.step(qs[t][l], *kv[l], run.scale, ids=ids, seq_lens=sl)
+                fp._last_out = out.clone()
+            a, b = plain[l]._last_out.float(), carried[l]._last_out.float()
+            assert torch.isfinite(a).all()
+            err = ((a - b).norm() / a.norm()).item()
+            assert err <= 1e-6, (t, l, err)
+        # every layer's update but the last one's has run (carried by the next layer's pass)
+        _same_state(plain[:-1], carried[:-1], t)
+    carried[-1].flush()                 # the last layer's update rides on the next step's first pass
+    _same_state(plain, carried, steps)
+
+
+def _same_state(plain, carried, t):
+    for l, (a, b) in enumerate(zip(plain, carried)):
+        for key in STATE:
+            assert torch.equal(a.state[key], b.state[key]), (t, l, key)
+
+
+def test_carrier_cfg4_shape(gpu):
+    """3 layers of the config-4 shape (32 / 8 heads, d 128) at T 4000: every update carried by the
+    next layer's pass, the last one by the next step's first pass."""
+    _loop(layers=3, B=1, Hq=32, Hkv=8, D=128, T0=4000, steps=12, seed=21)
+
+
+def test_carrier_group7_ragged(gpu):
+    """G 7 (two query heads per wavefront in the carried update), ragged batch of 3, d 128."""
+    _loop(layers=3, B=3, Hq=28, Hkv=4, D=128, T0=2600, steps=10, seed=22, ragged=[1500, 300, 2600])
+
+
+def test_carrier_group8_d64_single_layer(gpu):
+    """One layer (the update cannot ride on its own pass: flushed before the next plan), G 8, d 64."""
+    _loop(layers=1, B=2, Hq=16, Hkv=2, D=64, T0=2000, steps=8, seed=23)
+
+
+def test_carrier_long_context_two_launch_path(gpu):
+    """An update over more than 1024 blocks runs as two launches inside decode_splits_update."""
+    _loop(layers=2, B=1, Hq=4, Hkv=1, D=64, T0=66000, steps=4, seed=24)
+
+
+def test_decode_splits_update_rejects_group_mismatch(gpu):
+    q = torch.randn(1, 8, 64, device="cuda").to(torch.bfloat16)
+    k = torch.randn(1, 2, 256, 64, device="cuda").to(torch.bfloat16)
+    fp = FusedPlanner(_policy(), count=False)
+    fp.first(q, k, k, 0.125)
+    s = fp.state
+    u = E.update_struct(fp.bufs["blk_max"][:8 * 4].view(1, 8, 4), fp.bufs["blk_sum"][:8 * 4].view(1, 8, 4), s["trig"],
+                        s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], 256, 0.99, 2, s["flags"],
+                        list_stats=True)
+    q2 = torch.randn(1, 4, 64, device="cuda").to(torch.bfloat16)        # G 2 against the update's G 4
+    bufs = dict(out=torch.empty(1, 4, 64, dtype=torch.bfloat16, device="cuda"),
+                lse=torch.empty(1, 4, device="cuda"), blk_max=torch.empty(16, device="cuda"),
+                blk_sum=torch.empty(16, device="cuda"), part_acc=torch.empty(4 * 2 * 64, device="cuda"),
+                part_ml=torch.empty(4 * 2 * 2, device="cuda"))
+    bi = torch.zeros(1, 2, 4, dtype=torch.int32, device="cuda")
+    bc = torch.ones(1, 2, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="group sizes"):
+        E.decode_splits_update(q2, k, k, 0.125, bufs, bi, bc, 2, u)
