@@ -220,6 +220,37 @@ def main():
     log(f"dense: {us_step:.2f} us/step, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak); "
         f"masked: {us_m:.2f} us/step (x{us_m / us_step:.3f} of dense)")
 
+    # ---- two-pass V-skip on config 2's layer (kernels/kvskip.py:157-179): pass 1 = stats-only + fp16
+    # P (all of K), top-p 0.99 GQA-union selection (torch, once), pass 2 = pv over the kept blocks
+    r1 = E.decode(q, ks[0], vs[0], L.scale, None, None, True, False, S_dense, 2, False, True)
+    logw = r1[2] + torch.log(r1[3])
+    keep2 = K.select_blocks(logw, Hq // Hkv, "topp", 0.99, 2)
+    keep2_h = keep2.repeat_interleave(Hq // Hkv, dim=1)
+    lse_kept = logw.masked_fill(~keep2_h, float("-inf")).logsumexp(-1, keepdim=True)
+    scale_b = torch.exp(r1[2] - lse_kept).masked_fill(~keep2_h, 0.0)
+    scale_b = scale_b.view(B, Hkv, Hq // Hkv, -1).transpose(2, 3).contiguous()
+    plan2 = K.make_plan(keep2)
+    S_pv = K.num_splits_for(B * Hkv, plan2.max_cnt)
+    P1 = r1[5]
+    kept2 = int(plan2.block_cnt.sum())
+    t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], L.scale, None, None, True, False, S_dense, 2, False,
+                                            True), args.steps // 2, args.warmup)
+    t_p2 = events_region(lambda i: E.pv(P1, vs[i], scale_b, plan2.block_idx, plan2.block_cnt, S_pv, False),
+                         args.steps // 2, args.warmup)
+    ev_two = statistics.median(time_events(lambda i: K.vskip_two_pass(q, ks[i], vs[i], L.scale), args.events // 2,
+                                           NCOPY, flush))
+    bytes_p1 = B * Hkv * T * D * 2 + B * Hq * D * 2 + B * Hq * nb * 64 * 2 + 2 * B * Hq * nb * 4
+    bytes_p2 = kept2 * 64 * D * 2 + kept2 * (Hq // Hkv) * 64 * 2 + kept2 * (Hq // Hkv) * 4 + kept2 * 4
+    res["vskip2_cfg2"] = {"kept_block_frac": kept2 / (B * Hkv * nb), "pass1_us": t_p1, "pass2_us": t_p2,
+                          "pass1_bytes": bytes_p1, "pass2_bytes": bytes_p2,
+                          "pass1_GBs": bytes_p1 / t_p1 / 1e3, "pass2_GBs": bytes_p2 / t_p2 / 1e3,
+                          "kernels_vs_dense": (t_p1 + t_p2) / us_step, "num_splits_pass2": S_pv,
+                          "op_us_event_median_incl_host_selection": ev_two}
+    log(f"vskip2 cfg2: kept {kept2 / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), "
+        f"pass 2 {t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s), kernels x{(t_p1 + t_p2) / us_step:.3f} of dense; "
+        f"whole op with torch selection + host sync {ev_two:.1f} us")
+    del r1, P1, logw
+
     # ---- config 3: single-pass V-skip at T 65536 with a +-5% lse_prev
     del ks, vs
     torch.cuda.empty_cache()

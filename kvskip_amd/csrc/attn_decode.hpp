@@ -207,7 +207,32 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
 #pragma unroll
       for (int g = 0; g < G; ++g) alpha[g] = lane_value(ar[g % 4], 16 * (g / 4));
     };
-    if (nw > 0) {
+    if (nw > 0 && !LOAD_V) {
+      // K only: two blocks in flight while one is scored (the V registers are free). Step k loads
+      // item k + 1 and scores item k; past the last item the load reads beyond the head's buffer
+      // range (zeros, no memory access), so every step issues the same loads.
+      u32x4 ka[4][KS], kb[4][KS];
+      int ea = entry_of(1), eb = entry_of(2);
+      int b0 = block_of(entry_of(0), 0), b1 = -1;
+      load_k_block_mf<D>(ka, rk, koffm, p.k_st, max(b0, 0) * BLK);
+      auto step = [&](u32x4 (&ld)[4][KS], int& bld, const u32x4 (&ac)[4][KS], int bac, int k) {
+        const int ec = entry_of(k + 3);
+        bld = block_of(ea, min(k + 1, nw - 1));
+        ea = eb;
+        eb = ec;
+        load_k_block_mf<D>(ld, rk, koffm, p.k_st, (k + 1 < nw ? max(bld, 0) : nbb) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k < nw) {
+          float alpha[G];
+          process(bac, ac, alpha);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      for (int k = 0; k < nw; k += 2) {
+        step(kb, b1, ka, b0, k);
+        step(ka, b0, kb, b1, k + 1);
+      }
+    } else if (nw > 0) {
       u32x4 kr[4][KS];
       u32x4 vr[Lay<D>::VN];
       int e_n = entry_of(1);

@@ -12,6 +12,7 @@ import math
 import pytest
 import torch
 
+from kvskip_amd import ext as E
 from kvskip_amd import kvskip as K
 from kvskip_amd import workloads as W
 from oracle import attention as O
@@ -157,6 +158,42 @@ def test_write_p_and_two_pass(gpu):
               f"bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
         assert mism <= 0.01
         assert e16 <= BF16_TOL and e32 <= 5e-4          # fp16 P bounds the fp32 output error
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 7, 64])
+def test_pv_split_counts_and_list_edges(gpu, S):
+    """Pass 2 directly against the oracle's pv (kernels/kvskip_kernel.cu:316-421) on random P,
+    scales and lists: split counts giving each wavefront 0..many items (odd and even, the
+    double-buffered loop's tail), out-of-range entries (skipped), an empty list, D 64 and 128."""
+    g = torch.Generator().manual_seed(40 + S)
+    for D, G in ((128, 4), (64, 8)):
+        B, Hkv, T = 2, 3, 2900
+        Hq, nb = Hkv * G, math.ceil(2900 / 64)
+        v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+        P = torch.rand(B, Hq, nb * 64, generator=g).to(torch.float16)
+        P[..., T:] = 0
+        scale_b = torch.rand(B, Hkv, nb, G, generator=g)
+        keep = torch.rand(B, Hkv, nb, generator=g) < 0.4
+        keep[1, 2] = False                                       # an empty list
+        bi = torch.zeros(B, Hkv, nb, dtype=torch.int32)
+        bc = torch.zeros(B, Hkv, dtype=torch.int32)
+        for b in range(B):
+            for h in range(Hkv):
+                idx = torch.nonzero(keep[b, h])[:, 0].to(torch.int32)
+                if b == 0 and h == 1:                            # invalid entries are skipped
+                    idx = torch.cat([idx, torch.tensor([nb, nb + 5, -1], dtype=torch.int32)])
+                bi[b, h, :len(idx)] = idx[:nb]
+                bc[b, h] = min(len(idx), nb)
+        out, o32 = E.pv(P.cuda(), v.cuda(), scale_b.cuda().contiguous(), bi.cuda(), bc.cuda(), S, True)
+        keep_eff = torch.zeros_like(keep)
+        for b in range(B):
+            for h in range(Hkv):
+                ent = bi[b, h, :bc[b, h]].long()
+                ent = ent[(ent >= 0) & (ent < nb)]
+                keep_eff[b, h, ent] = True
+        ref = O.pv(P, v, scale_b, keep_eff)
+        assert O.rel_err(o32.cpu(), ref) <= 2e-5, (D, G, S)
+        assert O.rel_err(out.cpu(), ref) <= BF16_TOL, (D, G, S)
 
 
 @pytest.mark.parametrize("tau", [1e-4, 1e-3])
