@@ -5,9 +5,10 @@ B 1, 32 query / 8 KV heads, D 128, T 32768, bf16): dense split-K decode over the
 `value` is its achieved HBM bandwidth (algorithmic bytes: K + V + q + out + lse) over the K timed
 steps, launched from a HIP graph that cycles through 8 distinct KV copies (1.07 GB, far more than
 L2 + the 256 MB Infinity Cache, so every step streams from HBM). The same line carries the masked
-block-list + block-statistics path (config 2's 35% list), the single-pass V-skip (config 3,
-T 65536), config 1, the measured read ceiling, per-kernel HIP-event durations (roofline) and the
-reference-semantics PyTorch CPU path timed on this host (cpu_baseline).
+block-list + block-statistics path (config 2's 35% list), the two-pass V-skip (config 2's layer
+and a layer with peaked attention), the single-pass V-skip (config 3, T 65536), config 1, the
+measured read ceiling, the device planner loops (configs 4 and 5), per-kernel HIP-event durations
+(roofline) and the reference-semantics PyTorch CPU path timed on this host (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--splits S]
 """
@@ -220,36 +221,18 @@ def main():
     log(f"dense: {us_step:.2f} us/step, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak); "
         f"masked: {us_m:.2f} us/step (x{us_m / us_step:.3f} of dense)")
 
-    # ---- two-pass V-skip on config 2's layer (kernels/kvskip.py:157-179): pass 1 = stats-only + fp16
-    # P (all of K), top-p 0.99 GQA-union selection (torch, once), pass 2 = pv over the kept blocks
-    r1 = E.decode(q, ks[0], vs[0], L.scale, None, None, True, False, S_dense, 2, False, True)
-    logw = r1[2] + torch.log(r1[3])
-    keep2 = K.select_blocks(logw, Hq // Hkv, "topp", 0.99, 2)
-    keep2_h = keep2.repeat_interleave(Hq // Hkv, dim=1)
-    lse_kept = logw.masked_fill(~keep2_h, float("-inf")).logsumexp(-1, keepdim=True)
-    scale_b = torch.exp(r1[2] - lse_kept).masked_fill(~keep2_h, 0.0)
-    scale_b = scale_b.view(B, Hkv, Hq // Hkv, -1).transpose(2, 3).contiguous()
-    plan2 = K.make_plan(keep2)
-    S_pv = K.num_splits_for(B * Hkv, plan2.max_cnt)
-    P1 = r1[5]
-    kept2 = int(plan2.block_cnt.sum())
-    t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], L.scale, None, None, True, False, S_dense, 2, False,
-                                            True), args.steps // 2, args.warmup)
-    t_p2 = events_region(lambda i: E.pv(P1, vs[i], scale_b, plan2.block_idx, plan2.block_cnt, S_pv, False),
-                         args.steps // 2, args.warmup)
-    ev_two = statistics.median(time_events(lambda i: K.vskip_two_pass(q, ks[i], vs[i], L.scale), args.events // 2,
-                                           NCOPY, flush))
-    bytes_p1 = B * Hkv * T * D * 2 + B * Hq * D * 2 + B * Hq * nb * 64 * 2 + 2 * B * Hq * nb * 4
-    bytes_p2 = kept2 * 64 * D * 2 + kept2 * (Hq // Hkv) * 64 * 2 + kept2 * (Hq // Hkv) * 4 + kept2 * 4
-    res["vskip2_cfg2"] = {"kept_block_frac": kept2 / (B * Hkv * nb), "pass1_us": t_p1, "pass2_us": t_p2,
-                          "pass1_bytes": bytes_p1, "pass2_bytes": bytes_p2,
-                          "pass1_GBs": bytes_p1 / t_p1 / 1e3, "pass2_GBs": bytes_p2 / t_p2 / 1e3,
-                          "kernels_vs_dense": (t_p1 + t_p2) / us_step, "num_splits_pass2": S_pv,
-                          "op_us_event_median_incl_host_selection": ev_two}
-    log(f"vskip2 cfg2: kept {kept2 / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), "
-        f"pass 2 {t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s), kernels x{(t_p1 + t_p2) / us_step:.3f} of dense; "
-        f"whole op with torch selection + host sync {ev_two:.1f} us")
-    del r1, P1, logw
+    # ---- two-pass V-skip (kernels/kvskip.py:157-179) on config 2's layer (flat N(0, 1) keys: top-p
+    # 0.99 keeps every block, so the path can only show its cost) and on a layer of the config-4
+    # generator with an aimed query (attention on a few planted blocks + the sink)
+    res["vskip2_cfg2"] = bench_two_pass(E, K, q, ks, vs, L.scale, S_dense, us_step, args, flush, "vskip2 cfg2")
+    run_p = W.planner_run(layers=1, T0=T, steps=1, seed=44, device=dev)
+    q_p = run_p.q0[0].to(torch.bfloat16).contiguous()
+    ks_p = [run_p.k[0][:, :, :T].clone() for _ in range(NCOPY)]
+    vs_p = [run_p.v[0][:, :, :T].clone() for _ in range(NCOPY)]
+    del run_p
+    res["vskip2_peaked"] = bench_two_pass(E, K, q_p, ks_p, vs_p, L.scale, S_dense, us_step, args, flush,
+                                          "vskip2 peaked")
+    del ks_p, vs_p
 
     # ---- config 3: single-pass V-skip at T 65536 with a +-5% lse_prev
     del ks, vs
@@ -349,6 +332,44 @@ def main():
         "paths": res, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
+    """Two-pass V-skip on one layer (NCOPY KV copies): pass 1 (stats-only + fp16 P) and pass 2 (pv
+    over the kept blocks, top-p 0.99 GQA union) each timed as a graph-replayed region; the whole op
+    (torch selection and its host sync included) by per-call events."""
+    import torch
+
+    B, Hq, D = q.shape
+    Hkv, T = ks[0].shape[1], ks[0].shape[2]
+    G, nb = Hq // Hkv, math.ceil(T / 64)
+    r1 = E.decode(q, ks[0], vs[0], scale, None, None, True, False, S1, 2, False, True)
+    logw = r1[2] + torch.log(r1[3])
+    keep = K.select_blocks(logw, G, "topp", 0.99, 2)
+    keep_h = keep.repeat_interleave(G, dim=1)
+    lse_kept = logw.masked_fill(~keep_h, float("-inf")).logsumexp(-1, keepdim=True)
+    scale_b = torch.exp(r1[2] - lse_kept).masked_fill(~keep_h, 0.0)
+    scale_b = scale_b.view(B, Hkv, G, -1).transpose(2, 3).contiguous()
+    plan = K.make_plan(keep)
+    S2 = K.num_splits_for(B * Hkv, plan.max_cnt)
+    P1 = r1[5]
+    kept = int(plan.block_cnt.sum())
+    t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], scale, None, None, True, False, S1, 2, False, True),
+                         args.steps // 2, args.warmup)
+    t_p2 = events_region(lambda i: E.pv(P1, vs[i], scale_b, plan.block_idx, plan.block_cnt, S2, False),
+                         args.steps // 2, args.warmup)
+    ev = statistics.median(time_events(lambda i: K.vskip_two_pass(q, ks[i], vs[i], scale), args.events // 2,
+                                       NCOPY, flush))
+    bytes_p1 = B * Hkv * T * D * 2 + B * Hq * D * 2 + B * Hq * nb * 64 * 2 + 2 * B * Hq * nb * 4
+    bytes_p2 = kept * 64 * D * 2 + kept * G * 64 * 2 + kept * G * 4 + kept * 4
+    out = {"kept_block_frac": kept / (B * Hkv * nb), "pass1_us": t_p1, "pass2_us": t_p2, "pass1_bytes": bytes_p1,
+           "pass2_bytes": bytes_p2, "pass1_GBs": bytes_p1 / t_p1 / 1e3, "pass2_GBs": bytes_p2 / t_p2 / 1e3,
+           "kernels_vs_dense": (t_p1 + t_p2) / us_dense, "num_splits_pass2": S2,
+           "op_us_event_median_incl_host_selection": ev}
+    log(f"{tag}: kept {kept / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), pass 2 "
+        f"{t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s), kernels x{(t_p1 + t_p2) / us_dense:.3f} of dense; whole op "
+        f"with torch selection + host sync {ev:.1f} us")
+    return out
 
 
 def events_region(fn, steps, warmup):

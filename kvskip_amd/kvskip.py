@@ -37,12 +37,12 @@ def num_sms() -> int:
 
 
 def num_splits_for(bh: int, n_tiles: int, sms: int | None = None, max_splits: int = 256,
-                   min_tiles: int = 8) -> int:
+                   min_tiles: int = 4) -> int:
     """Split count for B*Hkv work items of n_tiles blocks each (kernels/kvskip.py:51-67).
 
     Same rule as the reference -- best wave efficiency over the resident workgroup slots, lightly
-    preferring fewer splits, at least `min_tiles` blocks per split -- with the slots counted as
-    CUs x WG_PER_CU (several 4-wavefront workgroups share a CU here)."""
+    preferring fewer splits, at least `min_tiles` blocks per split (one per wavefront of a
+    workgroup) -- with the slots counted as CUs x WG_PER_CU."""
     slots = (sms or num_sms()) * WG_PER_CU
     best, best_score = 1, -1.0
     for s in range(1, max_splits + 1):
