@@ -154,6 +154,11 @@ typedef struct kvskip_plan_args {
    * clamp(seq_lens[b], 1, T) tokens (T = the views' capacity); add_token adds each sequence's
    * last row. */
   const int32_t* seq_lens;
+  /* Optional [B] int32 device array (not in the reference): the plan writes each sequence's
+   * length (clamp(seq_lens[b], 1, T), or T) here, so that the update of the same step can read
+   * the lengths from memory that only the next plan rewrites (the device planner loop hands a
+   * layer's update to a later launch). */
+  int32_t* seq_lens_out;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);

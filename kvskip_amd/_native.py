@@ -46,7 +46,7 @@ class PlanArgs(ctypes.Structure):
         ("NBC", c_int32), ("local", c_int32), ("max_age", c_int32), ("add_token", c_int32),
         ("calib_on", c_int32), ("calib_kind", c_int32),
         ("scale", c_float), ("delta", c_float),
-        ("part", c_void_p), ("seq_lens", c_void_p),
+        ("part", c_void_p), ("seq_lens", c_void_p), ("seq_lens_out", c_void_p),
     ]
 
 

@@ -64,6 +64,7 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int Tb = seq_T(p.seq_lens, b, p.T);
   const int nb = (Tb + BLK - 1) / BLK;
+  if (p.seq_lens_out != nullptr && h == 0 && tid == 0) p.seq_lens_out[b] = Tb;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;  // head g: + g*NBC
   float* csum = p.csum + bh * p.NBC * D;
@@ -377,7 +378,9 @@ template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
   constexpr int SP = part_stride(G);
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int nb = (seq_T(p.seq_lens, b, p.T) + BLK - 1) / BLK;     // the sequence's blocks
+  const int Tb = seq_T(p.seq_lens, b, p.T);
+  const int nb = (Tb + BLK - 1) / BLK;                            // the sequence's blocks
+  if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
   const int C = ((p.T + BLK - 1) / BLK + WCB - 1) / WCB;          // chunks of the scores pass (capacity)
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int fl = p.flags[h];

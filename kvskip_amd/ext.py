@@ -302,13 +302,15 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None):
+         part=None, seq_lens=None, seq_lens_out=None):
     """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
 
     part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
     centroid pass is spread over all compute units (two launches instead of one).
     seq_lens (not in the reference): int32 [B] on the device, a ragged batch over views of
-    capacity T (sequence b holds seq_lens[b] tokens; add_token adds each one's last row)."""
+    capacity T (sequence b holds seq_lens[b] tokens; add_token adds each one's last row).
+    seq_lens_out (not in the reference): int32 [B] on the device; receives each sequence's length
+    this step (for the step's update, which may run later)."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
@@ -357,6 +359,10 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
         _require(part.numel() >= plan_part_floats(B, Hq, Hkv, NBC), "part: too small")
         p.part = part.data_ptr()
     p.seq_lens = _seq_lens_ptr(seq_lens, B)
+    if seq_lens_out is not None:
+        _require(seq_lens_out.is_cuda and seq_lens_out.dtype == torch.int32 and seq_lens_out.is_contiguous()
+                 and seq_lens_out.numel() == B, "seq_lens_out: contiguous int32 [B] on the device")
+        p.seq_lens_out = seq_lens_out.data_ptr()
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))

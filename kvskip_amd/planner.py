@@ -69,8 +69,9 @@ class UpdateCarrier:
     (kvskip_decode_splits_update): a layer's update reads only its own statistics and is read only
     by its own next plan, so it can run under another layer's streaming. Share one carrier between
     the FusedPlanners of a model's layers. A planner flushes its own pending update before it plans
-    again; call flush() before reading planner state on the host or from another stream. Tensors
-    handed to step() (idx, seq_lens) must stay unchanged until the update has been launched."""
+    again; call flush() before reading planner state on the host or from another stream. A ready
+    idx buffer handed to step() must stay unchanged until the update has been launched (seq_lens
+    may change: the update reads the plan's copy of the step's lengths)."""
 
     def __init__(self):
         self.pending = None          # (planner, G, UpdateArgs, tensors the struct points into)
@@ -138,6 +139,7 @@ class FusedPlanner:
             est=torch.zeros(B, Hkv, **f32),
             aix=torch.zeros(B, Hkv, dtype=torch.uint8, device=dev),
             idx=torch.zeros(B, NBC, dtype=torch.uint8, device=dev),
+            tlen=torch.zeros(B, dtype=torch.int32, device=dev),       # this step's lengths (ragged)
             part=torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), **f32),     # multi-workgroup plan
         )
 
@@ -202,6 +204,12 @@ class FusedPlanner:
         else:
             E.update(*update_args, **update_kwargs)
 
+    def _tlen(self, seq_lens):
+        """The update's lengths: the plan's copy of seq_lens in the planner's state (rewritten only
+        by this layer's next plan), so a carried update reads this step's lengths even after the
+        caller has advanced seq_lens."""
+        return None if seq_lens is None else self.state["tlen"]
+
     def _count(self, key, value):
         if self.count:
             self.counters[key] = self.counters.get(key, 0) + value
@@ -242,11 +250,11 @@ class FusedPlanner:
         pol = self.policy
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
-               int(pol.local), False, part=s["part"], seq_lens=seq_lens)
+               int(pol.local), False, part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens))
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
-                      float(pol.level), int(pol.local), every), dict(list_stats=True, seq_lens=seq_lens))
+                      float(pol.level), int(pol.local), every), dict(list_stats=True, seq_lens=self._tlen(seq_lens)))
         self.t, self.T = 0, T
         self.ragged = seq_lens is not None
         if self.count:
@@ -288,14 +296,14 @@ class FusedPlanner:
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
                int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
                cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None,
-               part=s["part"], seq_lens=seq_lens)
+               part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens))
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
                       float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
                       float(pol.calib or 0.0), bool(pol.calib_free), kind,
                       s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0)),
-                     dict(list_stats=True, seq_lens=seq_lens))
+                     dict(list_stats=True, seq_lens=self._tlen(seq_lens)))
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
             self._count("blocks_total", B * Hkv * nb if seq_lens is None
