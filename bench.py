@@ -558,8 +558,11 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     del planners
     planners = [None] * first_planned + [FusedPlanner(pol, count=False) for _ in range(first_planned, layers)]
     us_plan_own = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
+    del planners
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
+    us_replay, n_replay = replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0) \
+        if ragged is None else (math.nan, 0)
     out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
            "T0": T0 if ragged is None else list(ragged), "query_noise": noise, "query_revert": revert,
            "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)"
@@ -567,14 +570,67 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
            "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
            "us_per_layer_step_policy_update_own_launch": us_plan_own / n,
+           "us_per_layer_step_policy_one_graph_replayed": us_replay / n_replay if n_replay else None,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
     log(f"{tag}: policy {us_plan / n:.2f} us/layer-step (updates carried; {us_plan_own / n:.2f} with their own "
         f"launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
-        f"{layers}-layer step")
-    del planners, run, qs
+        f"{layers}-layer step" + (f"; one graph replayed per step: {us_replay / n_replay:.2f}" if n_replay else ""))
+    del run, qs
     return out
+
+
+def replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0):
+    """The config-4 loop as a server would run it: the step's length in device memory (seq_lens,
+    B 1), one HIP graph of a whole step (length advance, every layer's plan / pass / merge with the
+    updates carried) captured after the policy's warm-up and replayed for each later step; the
+    query of each step is copied into the graph's input buffer between replays. Returns (us of the
+    replayed steps, their layer-steps)."""
+    import torch
+
+    from kvskip_amd import kvskip as K
+    from kvskip_amd.planner import FusedPlanner, UpdateCarrier
+
+    dev = qs.device
+    carrier = UpdateCarrier()
+    planners = [None] * first_planned + [FusedPlanner(pol, count=False, carrier=carrier)
+                                         for _ in range(first_planned, layers)]
+    sl = torch.tensor([T0], dtype=torch.int32, device=dev)
+    qbuf = torch.empty_like(qs[0])
+
+    def step(t):
+        sl.add_(1)
+        for l in range(layers):
+            if l < first_planned:
+                K.decode(qbuf[l], run.k[l], run.v[l], run.scale, seq_lens=sl)
+            elif t == 0:
+                planners[l].first(qbuf[l], run.k[l], run.v[l], run.scale, seq_lens=sl)
+            else:
+                planners[l].step(qbuf[l], run.k[l], run.v[l], run.scale, ids=ids, seq_lens=sl)
+
+    w = (pol.calib_warm[0] if pol.calib_warm else 0) + 1
+    if steps <= w + 1:
+        return math.nan, 0
+    for t in range(w):
+        qbuf.copy_(qs[t])
+        step(t)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step(w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(w, steps):
+        qbuf.copy_(qs[t])
+        g.replay()
+    e1.record()
+    carrier.flush()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3, (steps - w) * layers
 
 
 def cpu_baseline(q, k, v, scale, nbytes, budget_s=12.0):
