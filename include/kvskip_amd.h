@@ -159,6 +159,13 @@ typedef struct kvskip_plan_args {
    * the lengths from memory that only the next plan rewrites (the device planner loop hands a
    * layer's update to a later launch). */
   int32_t* seq_lens_out;
+  /* Optional, with part (not in the reference): token ids [B, >= T] int32, row stride ids_sb
+   * elements. The plan then finds this step's token-index blocks itself (kvskip_token_index's
+   * rule), uses them as idx (which must be NULL) and writes them to idx_out [B, NBC] for the
+   * update (blocks >= ceil(T / 64): untouched). One launch fewer per layer-step. */
+  const int32_t* ids;
+  int64_t ids_sb;
+  uint8_t* idx_out;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);

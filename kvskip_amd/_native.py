@@ -47,6 +47,7 @@ class PlanArgs(ctypes.Structure):
         ("calib_on", c_int32), ("calib_kind", c_int32),
         ("scale", c_float), ("delta", c_float),
         ("part", c_void_p), ("seq_lens", c_void_p), ("seq_lens_out", c_void_p),
+        ("ids", c_void_p), ("ids_sb", c_int64), ("idx_out", c_void_p),
     ]
 
 

@@ -222,7 +222,12 @@ int kvskip_plan(const kvskip_plan_args* p, void* stream) {
   if (nb > p->NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
   if (nb > kvs::planner_max_blocks(G))
     return fail(KVSKIP_E_UNSUPPORTED, "plan: %d blocks exceed the planner capacity (%d)", nb, kvs::planner_max_blocks(G));
-  if (p->aix != nullptr && p->idx == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
+  if (p->ids != nullptr) {
+    if (p->part == nullptr || p->idx_out == nullptr || p->idx != nullptr)
+      return fail(KVSKIP_E_INVALID, "plan: ids needs part and idx_out, and no idx");
+    if (p->ids_sb < p->T) return fail(KVSKIP_E_INVALID, "plan: ids rows must hold >= T tokens");
+  }
+  if (p->aix != nullptr && p->idx == nullptr && p->ids == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
   if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
   return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
 }

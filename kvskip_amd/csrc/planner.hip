@@ -254,11 +254,37 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   const int fl = p.flags[h];
   const bool ixh = (fl & 2) != 0;  // token-index head: index + sink + local, no estimate
   const bool ax = p.aix != nullptr && p.aix[bh] != 0;
-  const bool uni = p.idx != nullptr && ((fl & 4) || ax);
+  const bool have_ix = p.idx != nullptr || p.ids != nullptr;  // ids: the index is found here
+  const bool uni = have_ix && ((fl & 4) || ax);
   const uint8_t* idx = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
-  const bool use_idx = p.idx != nullptr && (ixh || uni);
+  const bool use_idx = have_ix && (ixh || uni);
   __shared__ float sM[WW][G], sS[WW][G];
   __shared__ uint32_t sMask[WW];
+  const int base = c * WCB + wave * (4 * WU);  // this wavefront's blocks: base + 4 u + rs
+
+  // Token index (ids given; kvskip_token_index's rule): lane l checks the 8 tokens 8 (l % 8) + [0, 8)
+  // of block base + l / 8, so the wavefront finds its own 8 blocks (bit i: block base + i); the
+  // workgroups of KV head 0 also write them to idx_out for the update.
+  uint32_t ixw = 0;
+  if (p.ids != nullptr) {
+    const int32_t* ids = p.ids + b * p.ids_sb;
+    const int32_t cur = ids[Tb - 1];
+    const int blk = base + (lane >> 3);
+    const int j0 = blk * BLK + 8 * (lane & 7);
+    int32_t x[9];  // tokens j0 - 1 .. j0 + 7 (clamped loads, masked below)
+#pragma unroll
+    for (int e = 0; e < 9; ++e) x[e] = ids[min(max(j0 - 1 + e, 0), Tb - 1)];
+    bool hit = false;
+#pragma unroll
+    for (int e = 1; e < 9; ++e) {
+      const int j = j0 + e - 1;
+      hit |= (j < Tb - 1 && x[e] == cur) || (j < Tb && j >= 1 && x[e - 1] == cur);
+    }
+    const uint64_t bal = __ballot(hit);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ixw |= ((bal >> (8 * i)) & 0xffu) != 0 ? 1u << i : 0u;
+    if (h == 0 && (lane & 7) == 0 && blk < nb) p.idx_out[static_cast<int64_t>(b) * p.NBC + blk] = (ixw >> (lane >> 3)) & 1;
+  }
 
   // Every load is issued without waiting for the flags (an index head's extra loads are unused).
   const int rs = lane >> 4, c16 = lane & 15, gl = min(c16, G - 1);
@@ -282,7 +308,6 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   }
   const bool add = p.add_token != 0 && !ixh;
 
-  const int base = c * WCB + wave * (4 * WU);
   float cv[WU][DL], lr[WU], cr[WU];
   uint32_t kb[WU], ib[WU];
 #pragma unroll
@@ -303,7 +328,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
       cr[u] = p.cs_ref[r];
     }
     kb[u] = keep[rc];
-    ib[u] = idx[rc];
+    ib[u] = p.ids != nullptr ? (ixw >> (4 * u + rs)) & 1 : idx[rc];
   }
   float em = NEG_INF, es = 0.f;
   uint32_t wmask = 0;  // attended blocks of this wavefront: bit 4 u + rs

@@ -302,7 +302,7 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None, seq_lens_out=None):
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None):
     """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
 
     part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
@@ -310,7 +310,9 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     seq_lens (not in the reference): int32 [B] on the device, a ragged batch over views of
     capacity T (sequence b holds seq_lens[b] tokens; add_token adds each one's last row).
     seq_lens_out (not in the reference): int32 [B] on the device; receives each sequence's length
-    this step (for the step's update, which may run later)."""
+    this step (for the step's update, which may run later).
+    ids, idx_out (not in the reference; need part, and idx None): token ids int32 [B, >= T]; the
+    plan finds this step's token-index blocks itself and writes them to idx_out (uint8 [B, NBC])."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
@@ -347,7 +349,7 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     if aix is not None:
         _require(aix.is_cuda and aix.dtype == torch.uint8 and aix.is_contiguous() and aix.numel() == B * Hkv,
                  "aix: contiguous uint8 [B, Hkv]")
-        _require(idx is not None, "aix needs idx")
+        _require(idx is not None or ids is not None, "aix needs idx")
         p.aix = aix.data_ptr()
     p.cs_now, p.trig = cs_now.data_ptr(), trig.data_ptr()
     p.block_idx, p.block_cnt = block_idx.data_ptr(), block_cnt.data_ptr()
@@ -363,6 +365,13 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
         _require(seq_lens_out.is_cuda and seq_lens_out.dtype == torch.int32 and seq_lens_out.is_contiguous()
                  and seq_lens_out.numel() == B, "seq_lens_out: contiguous int32 [B] on the device")
         p.seq_lens_out = seq_lens_out.data_ptr()
+    if ids is not None:
+        _require(part is not None and idx is None and idx_out is not None, "plan: ids needs part and idx_out, and no idx")
+        _require(ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 2 and ids.stride(1) == 1
+                 and ids.shape[0] == B and ids.shape[1] >= T, "ids: CUDA int32 [B, >= T]")
+        _require(idx_out.dtype == torch.uint8 and idx_out.is_contiguous() and tuple(idx_out.shape) == (B, NBC),
+                 "idx_out: uint8 [B, NBC]")
+        p.ids, p.ids_sb, p.idx_out = ids.data_ptr(), ids.stride(0), idx_out.data_ptr()
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))

@@ -64,6 +64,11 @@ class Policy:
         return bool(self.index_heads) or self.calib_auto_ix is not None
 
 
+def _require_ids(ids, T):
+    if not (ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 2 and ids.stride(1) == 1 and ids.shape[1] >= T):
+        raise RuntimeError("ids: CUDA int32 [B, >= T]")
+
+
 class UpdateCarrier:
     """Holds the update of the layer that stepped last until the next layer's split pass carries it
     (kvskip_decode_splits_update): a layer's update reads only its own statistics and is read only
@@ -289,14 +294,20 @@ class FusedPlanner:
                 E.block_sums(k, self.NBC, out=s["csum"])              # several tokens appended: resum
         self.t += 1
         self.T = T
-        ix = self._set_idx(idx, ids, T, seq_lens) if pol.needs_index else None
+        fuse_ix = pol.needs_index and ids is not None and idx is None     # the plan finds the index itself
+        if fuse_ix:
+            _require_ids(ids, T)
+            ix = s["idx"]
+        else:
+            ix = self._set_idx(idx, ids, T, seq_lens) if pol.needs_index else None
         cal = pol.calib is not None
         kind = KINDS[pol.calib_kind]
         E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"], s["cs_now"],
                s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
-               int(pol.max_age_at(self.t)), int(pol.local), add_token, ix, s["calib"] if cal else None, s["est"],
-               cal and self.t >= pol.calib_hold, kind, s["aix"] if pol.calib_auto_ix is not None else None,
-               part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens))
+               int(pol.max_age_at(self.t)), int(pol.local), add_token, None if fuse_ix else ix,
+               s["calib"] if cal else None, s["est"], cal and self.t >= pol.calib_hold, kind,
+               s["aix"] if pol.calib_auto_ix is not None else None, part=s["part"], seq_lens=seq_lens,
+               seq_lens_out=self._tlen(seq_lens), ids=ids if fuse_ix else None, idx_out=ix if fuse_ix else None)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,

@@ -266,3 +266,40 @@ def test_merge_update_matches_separate_launches(gpu):
     E.update(*a, **kw)
     for key in mut:
         assert torch.equal(alt[key], s[key]), key
+
+
+@pytest.mark.parametrize("ragged", [None, [2500, 700]])
+def test_plan_fused_token_index(gpu, ragged):
+    """plan(ids=..., idx_out=...) finds the token index inside the scores pass: the same decisions,
+    lists, state and outputs as the separate token_index launch feeding plan(idx=...), and idx_out
+    equal to token_index's blocks of every sequence."""
+    B, Hkv, G, D, steps = (1 if ragged is None else 2), 4, 4, 128, 10
+    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=3000, steps=steps, seed=41, ragged=ragged)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    ids = run.ids.to(torch.int32).cuda()
+    qp = W.QueryProcess(run, 0, p_jump=0.1, revert=True)
+    pol = DPolicy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.0)   # every head on the index
+    fused, sep = FusedPlanner(pol, count=False), FusedPlanner(pol, count=False)
+    for t in range(steps):
+        q = qp.next().cuda()
+        if ragged is None:
+            T = 3000 + t + 1
+            kv, sl, Tv = (k[:, :, :T], v[:, :, :T]), None, T
+        else:
+            kv, Tv = (k, v), k.shape[2]
+            sl = torch.tensor([L + t + 1 for L in ragged], dtype=torch.int32, device="cuda")
+        if t == 0:
+            o1 = fused.first(q, *kv, run.scale, seq_lens=sl)
+            o2 = sep.first(q, *kv, run.scale, seq_lens=sl)
+        else:
+            o1 = fused.step(q, *kv, run.scale, ids=ids, seq_lens=sl)
+            ix = E.token_index(ids, Tv, sep.NBC, seq_lens=sl)
+            o2 = sep.step(q, *kv, run.scale, idx=ix, seq_lens=sl)
+            lens = [Tv] if sl is None else sl.tolist()
+            for b, Tb in enumerate(lens):
+                nbb = math.ceil(Tb / 64)
+                assert torch.equal(fused.state["idx"][b, :nbb], ix[b, :nbb]), (t, b)
+        assert torch.equal(o1, o2), t
+        for key in ("keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt", "calib", "aix",
+                    "cs_now", "est", "csum"):
+            assert torch.equal(fused.state[key], sep.state[key]), (t, key)
