@@ -170,6 +170,10 @@ typedef struct kvskip_plan_args {
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
 
+/* The first launch of kvskip_plan with a workspace alone: the scores pass (needs part). Not in the
+ * reference: with kvskip_decode_splits_planned after it, the decision runs inside the masked pass. */
+int kvskip_plan_scores(const kvskip_plan_args* p, void* stream);
+
 /* Floats of kvskip_plan_args.part for a state of capacity NBC blocks (-1 for invalid sizes).
  * Not in the reference: sizes the optional multi-workgroup plan workspace. */
 int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC);
@@ -199,6 +203,9 @@ typedef struct kvskip_update_args {
                                   rest is uninitialised and ignored), so they need no fill */
   const int32_t* seq_lens;     /* optional [B] int32 (ragged batch, as in kvskip_plan_args); the
                                   statistics keep the row length ceil(T / 64) */
+  int32_t* age;                /* optional [B, Hkv] (not in the reference): the plan's age, advanced
+                                  here (0 if trig, else + 1; token-index heads untouched) when the
+                                  decision ran in the pass (kvskip_decode_splits_planned) */
 } kvskip_update_args;
 
 int kvskip_update(const kvskip_update_args* p, void* stream);
@@ -216,6 +223,16 @@ int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, 
  * equals a's. Updates over more than 1024 blocks, or with the VALU engine selected, run as two
  * launches (same results). */
 int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream);
+
+/* The second half of kvskip_plan and the masked + statistics split pass in one launch (not in the
+ * reference): after kvskip_plan_scores(p), every workgroup of the pass merges the partials of its
+ * (b, KV head), makes plan's decision (the same result in every workgroup) and takes its slice of
+ * the block list from the attended-block masks; p's trig, est, block_idx and block_cnt are written
+ * as by kvskip_plan, but NOT the age: the layer's update must advance it (u->age). a: as for
+ * kvskip_decode_splits with stats and load_v (its block list fields are ignored); no ragged
+ * batches. u: NULL, or the update of another layer to carry (as kvskip_decode_splits_update). */
+int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_args* p, const kvskip_update_args* u,
+                                 void* stream);
 
 /* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
  * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums

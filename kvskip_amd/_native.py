@@ -60,7 +60,7 @@ class UpdateArgs(ctypes.Structure):
         ("calib_rate", c_float), ("aix_thr", c_float), ("level", c_float),
         ("calib_free", c_int32), ("calib_kind", c_int32),
         ("B", c_int32), ("Hq", c_int32), ("Hkv", c_int32), ("T", c_int32), ("NBC", c_int32), ("local", c_int32),
-        ("list_stats", c_int32), ("seq_lens", c_void_p),
+        ("list_stats", c_int32), ("seq_lens", c_void_p), ("age", c_void_p),
     ]
 
 
@@ -77,6 +77,8 @@ SIGNATURES = {
     "kvskip_update": ([POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_merge_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_decode_splits_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
+    "kvskip_plan_scores": ([POINTER(PlanArgs), c_void_p], c_int),
+    "kvskip_decode_splits_planned": ([POINTER(AttnArgs), POINTER(PlanArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_int32, c_void_p, c_void_p], c_int),
     "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),

@@ -2,7 +2,7 @@
 // per-block statistics, stats-only (K only) and fp16 P; both QK engines (MFMA, VALU dot2). Used
 // by the decode kernels and by the planner's split pass that carries an update.
 #pragma once
-#include "attn_common.hpp"
+#include "planner_common.hpp"
 
 namespace kvs {
 namespace {
@@ -14,8 +14,8 @@ namespace {
 // Wavefront w takes positions i0 + w + NWAVE j; its lane j < 64 holds that entry and the one
 // before it (cur0, prev0: loaded at the start of the pass, written after it, so these stores
 // overlap the partial results' instead of delaying them).
-template <int G>
-__device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, int i0, int n, int split,
+template <int G, class List>
+__device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, int i0, int n, int split,
                                 int64_t hq0, int wave, int lane, int prev0, int cur0) {
   auto put = [&](int g, int blk) {
     p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
@@ -34,21 +34,27 @@ __device__ void write_gap_stats(const AttnP& p, const int* list, int n_items, in
       cur = __builtin_amdgcn_readlane(cur0, j);
     } else {
       const int k = i0 + wave + NWAVE * j;
-      cur = __builtin_amdgcn_readfirstlane(list[k]);
-      prev = __builtin_amdgcn_readfirstlane(list[k - 1]);
+      cur = __builtin_amdgcn_readfirstlane(list(k));
+      prev = __builtin_amdgcn_readfirstlane(list(k - 1));
     }
     const int a = max(prev, -1) + 1, len = min(cur, p.nb) - a;
     for (int x = lane; x < G * len; x += WAVE) put(x / len, a + x % len);
   }
   if (n > 0 && i0 + n == n_items) {
-    const int a = min(max(list[n_items - 1], -1), p.nb - 1) + 1, len = p.nb - a;
+    const int a = min(max(list(n_items - 1), -1), p.nb - 1) + 1, len = p.nb - a;
     for (int x = tid; x < G * len; x += NT) put(x / len, a + x % len);
   }
 }
 
-// The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads.
-template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG>
-__device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
+// The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads. PLANNED (masked,
+// not ragged): the list is the plan's decision for (b, h), made in this workgroup's prologue from
+// the scores pass's partials (pa): wavefront 0 decides (as plan_decide; every workgroup of the
+// head reaches the same result from the same partials) and puts the list positions of this split
+// into LDS; split 0 also stores trig, est and, at its end, the head's block list and count (the
+// age is advanced by the update).
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false>
+__device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
+  static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
@@ -60,7 +66,40 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
   // n_items of (b, h); Tb, nbb: the sequence's tokens and blocks.
   int split, h, b, n_items, i0, n;
   int Tb = p.T, nbb = p.nb;
-  if constexpr (!RAG) {
+  __shared__ int sPl[PLANNED ? MAX_NB + 1 : 1];  // planned: list positions i0 - 1 .. i0 + n - 1
+  __shared__ int sPi[2];                          // planned: refresh, list length
+  uint32_t pmk[DCL];                              // planned, wavefront 0: the chunk masks
+  bool dense = false;                             // planned: a refresh (every block, in order)
+  if constexpr (PLANNED) {
+    work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
+    if (wave == 0) {
+      int pre[DCL];
+      const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0, false);
+      const int cnt = t ? p.nb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
+      if (!t) {
+        const int per = (cnt + p.num_splits - 1) / p.num_splits;
+        const int a0 = min(cnt, split * per), a1 = min(cnt, a0 + per);
+#pragma unroll
+        for (int j = 0; j < DCL; ++j) {
+          int pos = pre[j];
+          if (pos + __popc(pmk[j]) <= a0 - 1 || pos >= a1) continue;
+          for (uint32_t m = pmk[j]; m != 0; m &= m - 1, ++pos)
+            if (pos >= a0 - 1 && pos < a1) sPl[pos - a0 + 1] = (lane + WAVE * j) * WCB + __ffs(m) - 1;
+        }
+        if (lane == 0 && a0 == 0) sPl[0] = -1;
+      }
+      if (lane == 0) {
+        sPi[0] = t ? 1 : 0;
+        sPi[1] = cnt;
+      }
+    }
+    __syncthreads();
+    dense = sPi[0] != 0;
+    n_items = sPi[1];
+    const int per = (n_items + p.num_splits - 1) / p.num_splits;
+    i0 = min(n_items, split * per);
+    n = min(n_items, i0 + per) - i0;
+  } else if constexpr (!RAG) {
     work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
     n_items = MASKED ? min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks) : p.nb;
     const int per = (n_items + p.num_splits - 1) / p.num_splits;
@@ -96,14 +135,21 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
     Tb = seq_len(p, b);
     nbb = (Tb + BLK - 1) / BLK;
   }
-  const int* list = MASKED ? p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks : nullptr;
+  const int* glist = MASKED && !PLANNED ? p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks : nullptr;
+  // entry at list position pos (planned: pos in [i0 - 1, i0 + n), from LDS; a refresh lists every block)
+  const auto list = [&](int pos) -> int {
+    if constexpr (PLANNED)
+      return dense ? pos : sPl[pos - i0 + 1];
+    else
+      return glist[pos];
+  };
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
   int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this lane's gap
   if constexpr (MASKED && STATS) {
     const int t = wave + NWAVE * lane;
     if (t < n) {
-      gap_cur = list[i0 + t];
-      gap_prev = i0 + t > 0 ? list[i0 + t - 1] : -1;
+      gap_cur = list(i0 + t);
+      gap_prev = i0 + t > 0 ? list(i0 + t - 1) : -1;
     }
   }
 
@@ -121,7 +167,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
 
   // List entry of this wavefront's k-th item (k clamped to its items): a vector load whose value is
   // used two items later, so that waiting for it never waits for the block loads issued after it.
-  auto entry_of = [&](int k) -> int { return MASKED ? list[i0 + wave + NWAVE * min(k, nw - 1)] : 0; };
+  auto entry_of = [&](int k) -> int { return MASKED ? list(i0 + wave + NWAVE * min(k, nw - 1)) : 0; };
   // Block of the k-th item from its entry; out-of-range entries read block 0 and are masked.
   auto block_of = [&](int e, int k) -> int {  // uniform over the wavefront
     const int blk = __builtin_amdgcn_readfirstlane(MASKED ? e : i0 + wave + NWAVE * k);
@@ -332,6 +378,9 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid) {
   }
   finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
   if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
+  if constexpr (PLANNED) {
+    if (split == 0 && wave == 0) write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, p.nb, dense, pmk, lane);
+  }
   if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
     if (nbb < p.nb && i0 + n == n_items) {
       for (int t = tid; t < G * (p.nb - nbb); t += NT) {

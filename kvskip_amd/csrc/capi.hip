@@ -203,7 +203,7 @@ int kvskip_read(const void* x, int64_t bytes, uint32_t* out, int32_t blocks, voi
   return launched(kvs::launch_read(x, bytes, out, blocks, static_cast<hipStream_t>(stream)), "kvskip_read");
 }
 
-int kvskip_plan(const kvskip_plan_args* p, void* stream) {
+static int check_plan(const kvskip_plan_args* p) {
   if (p == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
   if (p->q == nullptr || p->k == nullptr) return fail(KVSKIP_E_INVALID, "q: CUDA bf16 [B, Hq, D]");
   if (p->B < 1 || p->Hkv < 1 || p->Hq < 1 || p->T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
@@ -229,7 +229,20 @@ int kvskip_plan(const kvskip_plan_args* p, void* stream) {
   }
   if (p->aix != nullptr && p->idx == nullptr && p->ids == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
   if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
+  return KVSKIP_OK;
+}
+
+int kvskip_plan(const kvskip_plan_args* p, void* stream) {
+  const int rc = check_plan(p);
+  if (rc != KVSKIP_OK) return rc;
   return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
+}
+
+int kvskip_plan_scores(const kvskip_plan_args* p, void* stream) {
+  const int rc = check_plan(p);
+  if (rc != KVSKIP_OK) return rc;
+  if (p->part == nullptr) return fail(KVSKIP_E_INVALID, "plan_scores needs the part workspace");
+  return launched(kvs::launch_plan_scores(*p, static_cast<hipStream_t>(stream)), "kvskip_plan_scores");
 }
 
 int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC) {
@@ -288,6 +301,27 @@ int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_a
   if (a->Hq / a->Hkv != u->Hq / u->Hkv)
     return fail(KVSKIP_E_INVALID, "decode_splits_update: the pass and the update have different group sizes");
   return launched(kvs::launch_split_update(p, *u, a->D, static_cast<hipStream_t>(stream)), "kvskip_decode_splits_update");
+}
+
+int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_args* pl, const kvskip_update_args* u,
+                                 void* stream) {
+  int rc = check_plan(pl);
+  if (rc != KVSKIP_OK) return rc;
+  if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (pl->part == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_planned needs the plan's part workspace");
+  if (pl->seq_lens != nullptr || a->seq_lens != nullptr)
+    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: no ragged batches (plan and decide separately)");
+  if (a->B != pl->B || a->Hq != pl->Hq || a->Hkv != pl->Hkv || a->T != pl->T || a->D != pl->D)
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
+  kvskip_attn_args am = *a;  // the pass's list is the plan's
+  am.block_idx = pl->block_idx;
+  am.block_cnt = pl->block_cnt;
+  am.max_blocks = pl->NBC;
+  kvs::AttnP p;
+  if ((rc = check_decode(&am, 1, 1, a->num_splits > 1 ? 1 : 3, &p)) != KVSKIP_OK) return rc;
+  if (u != nullptr && (rc = check_update(u)) != KVSKIP_OK) return rc;
+  return launched(kvs::launch_planned_split(p, *pl, u, a->D, static_cast<hipStream_t>(stream)),
+                  "kvskip_decode_splits_planned");
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,

@@ -65,6 +65,12 @@ hipError_t launch_update(const kvskip_update_args& p, hipStream_t s);
 hipError_t launch_merge_update(const AttnP& a, const kvskip_update_args& p, int D, hipStream_t s);
 // The masked + statistics split pass of a (phase 1) and the update u of another layer, one launch.
 hipError_t launch_split_update(const AttnP& a, const kvskip_update_args& u, int D, hipStream_t s);
+// The plan's decision + the masked statistics split pass of a (phase 1) in one launch, with an
+// optional carried update u of another layer.
+hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
+                                hipStream_t s);
+// The plan's first launch alone (the scores pass; needs part).
+hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s);
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
                              int D, float* csum, int NBC, const int32_t* seq_lens, hipStream_t s);
 hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,

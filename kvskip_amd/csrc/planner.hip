@@ -227,19 +227,6 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   }
 }
 
-// ---- Two-kernel plan (with a workspace): plan_scores spreads the centroid pass of a head over
-// ceil(nb / 32) workgroups (4 wavefronts, 8 block rows each), each publishing per query head the
-// (m, s) log-sum-exp of its unattended blocks' estimates and the 32-bit mask of its attended
-// blocks; plan_decide (one wavefront per head) merges them, decides and compacts from the masks.
-// The kernel boundary publishes the partials (a last-arriving-workgroup ticket would need an
-// agent-scope release per workgroup, an L2 write-back each, which costs more than the launch).
-constexpr int WW = 4;                // wavefronts per workgroup
-constexpr int WU = 2;                // row groups (4 rows) per wavefront
-constexpr int WCB = WW * WU * 4;     // 32 blocks per workgroup
-constexpr int WNT = WW * WAVE;
-
-__host__ __device__ constexpr int part_stride(int G) { return 2 * G + 1; }  // m[G], s[G], mask
-
 template <int D, int G>
 __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args p) {
   constexpr int DL = D / 16, DW = DL / 4, SP = part_stride(G);
@@ -626,6 +613,20 @@ hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s) {
   const int G = p.Hq / p.Hkv;
 #define KVS_CASE(DD, GG) \
   if (p.D == DD && G == GG) return launch_plan_t<DD, GG>(p, s);
+  KVS_CASE(64, 1) KVS_CASE(64, 2) KVS_CASE(64, 4) KVS_CASE(64, 7) KVS_CASE(64, 8)
+  KVS_CASE(128, 1) KVS_CASE(128, 2) KVS_CASE(128, 4) KVS_CASE(128, 7) KVS_CASE(128, 8)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s) {
+  const int G = p.Hq / p.Hkv;
+  const int nb = (p.T + BLK - 1) / BLK;
+#define KVS_CASE(DD, GG)                                                                                     \
+  if (p.D == DD && G == GG) {                                                                                \
+    hipLaunchKernelGGL((plan_scores_kernel<DD, GG>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p); \
+    return hipGetLastError();                                                                                \
+  }
   KVS_CASE(64, 1) KVS_CASE(64, 2) KVS_CASE(64, 4) KVS_CASE(64, 7) KVS_CASE(64, 8)
   KVS_CASE(128, 1) KVS_CASE(128, 2) KVS_CASE(128, 4) KVS_CASE(128, 7) KVS_CASE(128, 8)
 #undef KVS_CASE

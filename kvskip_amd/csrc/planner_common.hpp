@@ -44,6 +44,127 @@ __device__ __forceinline__ void lse_wave(float& m, float& s) {
 
 constexpr int MAX_NB = 4096;   // planner block capacity: update holds a head's blocks in registers
 
+// ---- Two-kernel plan (with a workspace): plan_scores spreads the centroid pass of a head over
+// ceil(nb / 32) workgroups (4 wavefronts, 8 block rows each), each publishing per query head the
+// (m, s) log-sum-exp of its unattended blocks' estimates and the 32-bit mask of its attended
+// blocks; the decision (plan_decide, or the prologue of the masked pass) merges them, decides and
+// compacts from the masks. The kernel boundary publishes the partials (a last-arriving-workgroup
+// ticket would need an agent-scope release per workgroup, an L2 write-back each, which costs more
+// than the launch).
+constexpr int WW = 4;                // wavefronts per workgroup
+constexpr int WU = 2;                // row groups (4 rows) per wavefront
+constexpr int WCB = WW * WU * 4;     // 32 blocks per workgroup
+constexpr int WNT = WW * WAVE;
+constexpr int DCL = MAX_NB / WCB / WAVE;  // chunks per lane of the decision at capacity
+
+__host__ __device__ constexpr int part_stride(int G) { return 2 * G + 1; }  // m[G], s[G], mask
+
+// Chunks of the scores pass over the capacity T (tokens).
+__device__ __forceinline__ int plan_chunks(int T) { return ((T + BLK - 1) / BLK + WCB - 1) / WCB; }
+
+// The plan's decision for (b, KV head h) from the scores pass's partials: one wavefront, uniform
+// result (src/kvskip_attn.py:366-383, kernels/kvskip_planner.cu:179-201): per query head the
+// log-sum-exp of the estimates over chunks, the missed mass, its calibration, age and flags.
+// mk[j] receives the attended-block mask of chunk lane + 64 j (0 past the chunks). With `write`
+// lane 0 stores est and trig, and the advanced age if `write_age` (a decision repeated by every
+// workgroup of a pass leaves the age to the update: the others still read the old one).
+template <int G>
+__device__ __forceinline__ bool decide_head(const kvskip_plan_args& p, int b, int h, int lane, uint32_t (&mk)[DCL],
+                                            bool write, bool write_age = true) {
+  constexpr int SP = part_stride(G);
+  const int C = plan_chunks(p.T);
+  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  const int fl = p.flags[h];
+  const float* pb = p.part + bh * C * SP;
+  const int age0 = p.age[bh];
+  const float cal0 = (p.calib != nullptr && p.calib_on) ? p.calib[bh] : 0.f;
+  const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + min(lane, G - 1)];
+  float pm[DCL][G], ps[DCL][G];
+#pragma unroll
+  for (int j = 0; j < DCL; ++j) {  // every partial first
+    const int cc = min(lane + WAVE * j, C - 1);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      pm[j][g] = pb[cc * SP + g];
+      ps[j][g] = pb[cc * SP + G + g];
+    }
+    mk[j] = __float_as_uint(pb[cc * SP + 2 * G]);
+  }
+#pragma unroll
+  for (int j = 0; j < DCL; ++j)
+    if (lane + WAVE * j >= C) mk[j] = 0u;
+  bool tr = false;
+  if (!(fl & 2)) {
+    float miss = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float m = NEG_INF, sv = 0.f;
+#pragma unroll
+      for (int j = 0; j < DCL; ++j)
+        if (lane + WAVE * j < C) lse_merge(m, sv, pm[j][g], ps[j][g]);
+      lse_wave(m, sv);
+      if (sv > 0.f) miss = fmaxf(miss, 1.f / (1.f + __expf(lane_value(la, g) - (m + __logf(sv)))));
+    }
+    float dec = miss;
+    if (p.calib != nullptr && p.calib_on)
+      dec = p.calib_kind ? miss + cal0 : 1.f / (1.f + __expf(-(clamped_logit(miss) + cal0)));
+    const int a = age0 + 1;
+    tr = dec > p.delta || a >= p.max_age || (fl & 1);
+    if (write && lane == 0) {
+      if (p.est != nullptr) p.est[bh] = miss;
+      if (write_age) p.age[bh] = tr ? 0 : a;
+    }
+  }
+  if (write && lane == 0) p.trig[bh] = tr ? 1 : 0;
+  return tr;
+}
+
+// Exclusive prefix over the wavefront of the attended blocks in the chunks a lane holds (pre[j]
+// for chunk lane + 64 j, ascending block order); returns the total (uniform).
+__device__ __forceinline__ int mask_prefix(const uint32_t (&mk)[DCL], int lane, int C, int (&pre)[DCL]) {
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < DCL; ++j) {
+    pre[j] = base;
+    if (WAVE * j >= C) continue;
+    const int n = __popc(mk[j]);
+    int incl = n;  // inclusive prefix over lanes
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int t = __shfl_up(incl, o, WAVE);
+      if (lane >= o) incl += t;
+    }
+    pre[j] = base + incl - n;
+    base += __shfl(incl, WAVE - 1, WAVE);
+  }
+  return base;
+}
+
+// The head's block list and count from its decision: every block (refresh) or the ascending
+// attended blocks of the chunk masks. One wavefront.
+__device__ __forceinline__ void write_block_list(const kvskip_plan_args& p, int64_t bh, int nb, bool tr,
+                                                 const uint32_t (&mk)[DCL], int lane) {
+  int* bi = p.block_idx + bh * p.NBC;
+  if (tr) {  // refresh: every block
+    for (int i = lane; i < nb; i += WAVE) bi[i] = i;
+    if (lane == 0) p.block_cnt[bh] = nb;
+    return;
+  }
+  int pre[DCL];
+  const int cnt = mask_prefix(mk, lane, plan_chunks(p.T), pre);
+#pragma unroll
+  for (int j = 0; j < DCL; ++j) {
+    int off = pre[j];
+    for (uint32_t m = mk[j]; m != 0; m &= m - 1) bi[off++] = (lane + WAVE * j) * WCB + __ffs(m) - 1;
+  }
+  if (lane == 0) p.block_cnt[bh] = cnt;
+}
+
+// An update carried by a pass runs in the pass's NWAVE-wavefront workgroups, over up to
+// CARRY_MAX_R * 64 blocks (longer: its own launch first).
+constexpr int carry_waves(int G) { return G < NWAVE ? G : NWAVE; }
+constexpr int CARRY_MAX_R = 16;
+
 // Order-preserving key of a float (larger float -> larger key).
 __device__ __forceinline__ uint32_t fkey(float y) {
   const uint32_t u = __float_as_uint(y);
@@ -199,6 +320,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
   }
   __syncthreads();  // every read of the old stored set is done; sKm / sReal complete
 
+  if (p.age != nullptr && tid == 0 && !(fl & 2)) p.age[bh] = tr ? 0 : p.age[bh] + 1;  // a pass's decision
   if (tr && p.calib != nullptr && tid == 0) {
     float real = 0.f;
     for (int g = 0; g < G; ++g) real = fmaxf(real, sReal[g]);

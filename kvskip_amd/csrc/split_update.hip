@@ -6,13 +6,9 @@
 // pass's streaming instead of in a launch of its own. A group of G > 4 query heads runs two heads
 // per wavefront (the pass's workgroups have 4).
 #include "attn_decode.hpp"
-#include "planner_common.hpp"
 
 namespace kvs {
 namespace {
-
-constexpr int carry_waves(int G) { return G < NWAVE ? G : NWAVE; }
-constexpr int CARRY_MAX_R = 16;  // updates of up to 16 * 64 blocks ride along; longer: two launches
 
 template <int D, int G, bool RAG, int R>
 __global__ void __launch_bounds__(NT, 2) split_update_kernel(const AttnP a, const kvskip_update_args u) {

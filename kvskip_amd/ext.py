@@ -313,6 +313,59 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     this step (for the step's update, which may run later).
     ids, idx_out (not in the reference; need part, and idx None): token ids int32 [B, >= T]; the
     plan finds this step's token-index blocks itself and writes them to idx_out (uint8 [B, NBC])."""
+    p = _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale,
+                   delta, max_age, local, add_token, idx, calib, est, calib_on, calib_kind, aix, part, seq_lens,
+                   seq_lens_out, ids, idx_out)
+    dev = q.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
+
+
+def plan_struct(*plan_args, **plan_kwargs) -> PlanArgs:
+    """The argument block of plan(*plan_args, **plan_kwargs), checked (it holds raw pointers)."""
+    return _plan_args(*plan_args, **plan_kwargs)
+
+
+def plan_scores(pargs: PlanArgs, device):
+    """plan's first launch alone (kvskip_plan_scores; needs part); its decision then runs in
+    decode_splits_planned. Not in the reference."""
+    dev = torch.device(device)
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_plan_scores(ctypes.byref(pargs), _stream(dev)))
+
+
+def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None):
+    """plan's decision and the masked + statistics split pass in one launch (kvskip_decode_splits_planned;
+    after plan_scores(pargs)); the whole op when num_splits == 1. The layer's update must advance the
+    age (update_struct(..., age=...)). update: another layer's update to carry, or None."""
+    check_q(q)
+    check_kv(k, "k")
+    check_kv(v, "v")
+    B, Hq, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    _require(1 <= num_splits <= 256, "num_splits in 1..256")
+    nb = (T + TILE - 1) // TILE
+    bmax, bsum = bufs["blk_max"], bufs["blk_sum"]
+    for t in (bmax, bsum):
+        _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= B * Hq * nb, "bufs: stats")
+    part_acc = part_ml = None
+    if num_splits > 1:
+        part_acc, part_ml = bufs["part_acc"], bufs["part_ml"]
+        _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
+                 "bufs: split partials")
+    a = _decode_args(q, k, v, scale, None, None, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None, None,
+                     part_acc, part_ml, None)
+    dev = q.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(pargs),
+                                                                 None if update is None else ctypes.byref(update),
+                                                                 _stream(dev)))
+
+
+def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
+         max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None):
+    """kvskip_plan_args of plan(), validated."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
@@ -372,9 +425,7 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
         _require(idx_out.dtype == torch.uint8 and idx_out.is_contiguous() and tuple(idx_out.shape) == (B, NBC),
                  "idx_out: uint8 [B, NBC]")
         p.ids, p.ids_sb, p.idx_out = ids.data_ptr(), ids.stride(0), idx_out.data_ptr()
-    dev = q.device
-    with torch.cuda.device(dev):
-        _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
+    return p
 
 
 def plan_part_floats(B, Hq, Hkv, NBC) -> int:
@@ -384,7 +435,7 @@ def plan_part_floats(B, Hq, Hkv, NBC) -> int:
 
 def _update_args(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None,
                  idx=None, est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None,
-                 aix_thr=0.0, list_stats=False, seq_lens=None) -> UpdateArgs:
+                 aix_thr=0.0, list_stats=False, seq_lens=None, age=None) -> UpdateArgs:
     """kvskip_update_args of update() (kernels/kvskip_ext.cpp:270-319), validated."""
     check_f32(blk_max, "blk_max")
     check_f32(blk_sum, "blk_sum")
@@ -425,19 +476,24 @@ def _update_args(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att,
         set_flags_idx()
         p.list_stats = 1
     p.seq_lens = _seq_lens_ptr(seq_lens, B)
+    if age is not None:
+        _require(age.is_cuda and age.dtype == torch.int32 and age.is_contiguous() and age.numel() == B * Hkv,
+                 "age: contiguous int32 [B, Hkv]")
+        p.age = age.data_ptr()
     return p
 
 
 def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags=None, idx=None,
            est=None, calib=None, calib_rate=0.0, calib_free=False, calib_kind=0, aix=None, aix_thr=0.0,
-           list_stats=False, seq_lens=None):
+           list_stats=False, seq_lens=None, age=None):
     """Device-side refresh planner after the pass (kernels/kvskip_ext.cpp:270-319); in place.
 
     list_stats (not in the reference): blk_max / blk_sum hold values only for the blocks of this
     step's plan (the masked pass ran on unfilled buffers); the kernel derives the read set from
-    trig, keep, flags and idx and ignores the rest. Needs flags (and idx if the plan had one)."""
+    trig, keep, flags and idx and ignores the rest. Needs flags (and idx if the plan had one).
+    age (not in the reference): advance the plan's age here (after decode_splits_planned)."""
     p = _update_args(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, level, local, flags, idx,
-                     est, calib, calib_rate, calib_free, calib_kind, aix, aix_thr, list_stats, seq_lens)
+                     est, calib, calib_rate, calib_free, calib_kind, aix, aix_thr, list_stats, seq_lens, age)
     dev = keep.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_update(ctypes.byref(p), _stream(dev)))

@@ -111,9 +111,14 @@ class FusedPlanner:
     its step. Usage: out = p.first(q, k, v, scale) on the first decode step, then
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
-    def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None):
+    def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
+                 decide_in_pass: bool = False):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
+        # plan's decision inside the masked pass (not ragged): off, its first GPU run faulted and
+        # the cause is not found yet
+        self.decide_in_pass = decide_in_pass
+        self._pargs = None
         self.state = None
         self.t = 0
         self.T = 0
@@ -182,7 +187,9 @@ class FusedPlanner:
         s = self.state
         self._S = S
         carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
-        if carried is not None:
+        if self._pargs is not None:
+            E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried)
+        elif carried is not None:
             E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens)
         else:
             E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S,
@@ -208,6 +215,20 @@ class FusedPlanner:
                            s["block_cnt"], seq_lens)
         else:
             E.update(*update_args, **update_kwargs)
+
+    def _plan(self, q, plan_args, plan_kwargs, seq_lens):
+        """plan (scores + decision), or, with decide_in_pass and no ragged batch, its scores pass
+        alone: the decision then runs in the masked pass (kvskip_decode_splits_planned) and the
+        update advances the age."""
+        if self.decide_in_pass and seq_lens is None:
+            self._pargs = E.plan_struct(*plan_args, **plan_kwargs)
+            E.plan_scores(self._pargs, q.device)
+        else:
+            self._pargs = None
+            E.plan(*plan_args, **plan_kwargs)
+
+    def _age(self):
+        return dict(age=self.state["age"]) if self._pargs is not None else {}
 
     def _tlen(self, seq_lens):
         """The update's lengths: the plan's copy of seq_lens in the planner's state (rewritten only
@@ -253,13 +274,15 @@ class FusedPlanner:
         E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens)
         every = torch.ones(Hkv, dtype=torch.int32, device=q.device)      # refresh all, no index heads
         pol = self.policy
-        E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every, s["cs_now"],
-               s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta), int(pol.max_age),
-               int(pol.local), False, part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens))
+        self._plan(q, (q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every,
+                       s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
+                       int(pol.max_age), int(pol.local), False),
+                   dict(part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens)), seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
-                      float(pol.level), int(pol.local), every), dict(list_stats=True, seq_lens=self._tlen(seq_lens)))
+                      float(pol.level), int(pol.local), every),
+                     dict(list_stats=True, seq_lens=self._tlen(seq_lens), **self._age()))
         self.t, self.T = 0, T
         self.ragged = seq_lens is not None
         if self.count:
@@ -302,19 +325,20 @@ class FusedPlanner:
             ix = self._set_idx(idx, ids, T, seq_lens) if pol.needs_index else None
         cal = pol.calib is not None
         kind = KINDS[pol.calib_kind]
-        E.plan(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"], s["cs_now"],
-               s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
-               int(pol.max_age_at(self.t)), int(pol.local), add_token, None if fuse_ix else ix,
-               s["calib"] if cal else None, s["est"], cal and self.t >= pol.calib_hold, kind,
-               s["aix"] if pol.calib_auto_ix is not None else None, part=s["part"], seq_lens=seq_lens,
-               seq_lens_out=self._tlen(seq_lens), ids=ids if fuse_ix else None, idx_out=ix if fuse_ix else None)
+        self._plan(q, (q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"],
+                       s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
+                       int(pol.max_age_at(self.t)), int(pol.local), add_token, None if fuse_ix else ix,
+                       s["calib"] if cal else None, s["est"], cal and self.t >= pol.calib_hold, kind,
+                       s["aix"] if pol.calib_auto_ix is not None else None),
+                   dict(part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens),
+                        ids=ids if fuse_ix else None, idx_out=ix if fuse_ix else None), seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
                       float(pol.level), int(pol.local), s["flags"], ix, s["est"], s["calib"] if cal else None,
                       float(pol.calib or 0.0), bool(pol.calib_free), kind,
                       s["aix"] if pol.calib_auto_ix is not None else None, float(pol.calib_auto_ix or 0.0)),
-                     dict(list_stats=True, seq_lens=self._tlen(seq_lens)))
+                     dict(list_stats=True, seq_lens=self._tlen(seq_lens), **self._age()))
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
             self._count("blocks_total", B * Hkv * nb if seq_lens is None
