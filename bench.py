@@ -202,9 +202,19 @@ def main():
     log(f"dense split pass: {t_split:.2f} us per launch ({bytes_split / t_split / 1e3:.0f} GB/s), merge "
         f"{t_merge:.2f} us; per-call event medians {ev_split:.2f} / {ev_merge:.2f} us")
     del ops
+    # the read-ceiling kernel over the same bytes, timed the same way (8 buffers of the split pass's
+    # read size, launches back to back): a pure stream of these bytes at this size, launch ramp and
+    # tail included (best of 512 and 768 workgroups)
+    o_r = torch.zeros(1, dtype=torch.int32, device=dev)
+    xr = [torch.ones(bytes_split // 2, dtype=torch.bfloat16, device=dev) for _ in range(NCOPY)]
+    t_read = min(events_region(lambda i: E.read_bw(xr[i], o_r, nblk), args.steps, args.warmup) for nblk in (512, 768))
+    del xr
+    res["dense"].update(read_same_bytes_us=t_read, split_pass_vs_read=t_read / t_split)
+    log(f"read kernel over the same {bytes_split / 1e6:.1f} MB: {t_read:.2f} us per launch "
+        f"({bytes_split / t_read / 1e3:.0f} GB/s); split pass at {100 * t_read / t_split:.1f}% of it")
     if args.roofline_only:
         print(json.dumps({"roofline_only": True, "split_pass_us": t_split, "merge_us": t_merge,
-                          "GBs": bytes_split / t_split / 1e3}), flush=True)
+                          "GBs": bytes_split / t_split / 1e3, "read_same_bytes_us": t_read}), flush=True)
         return
 
     # ---- timed steps (dense, the headline) and the masked path, from graphs
@@ -313,7 +323,9 @@ def main():
                       f"average launch duration, {args.steps} launches back to back from HIP graphs over 8 KV "
                       "copies (1.07 GB), HIP events around the timed region",
             "algorithmic_bytes": bytes_split, "us_per_launch": round(t_split, 3),
-            "read_ceiling_GBs": round(res["read_ceiling_GBs"], 1)}
+            "read_ceiling_GBs": round(res["read_ceiling_GBs"], 1),
+            "read_same_bytes_GBs": round(bytes_split / t_read / 1e3, 1),
+            "frac_of_read_same_bytes": round(t_read / t_split, 4)}
 
     cpu = None
     if not args.no_cpu:

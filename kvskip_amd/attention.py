@@ -1,0 +1,267 @@
+"""Attention plugin of a transformers model on the kvskip_amd kernels: the per-layer forward that the
+model calls through AttentionInterface under the name "kvskip" (src/kvskip_attn.py:481-520), its
+configuration (src/kvskip_attn.py:116-147) and a growing KV cache whose layers hand the forward
+strided views of one preallocated buffer (src/kvskip_attn.py:68-113).
+
+Prefill (more than one query position) goes to SDPA, as in the reference. A decode step dispatches
+on KVSKIP.mode (layers in dense_layers always run dense):
+  "dense"          split-K decode over every block (kvskip_decode)
+  "vskip2"         two-pass V-skip, top-p(level) GQA union (kvskip.vskip_two_pass)
+  "vskip1"         single-pass V-skip against the layer's previous-step LSE (kept per layer)
+  "vskip1sink"     the same against the sink block's bound (no previous LSE)
+  "refresh_fused"  the device-side refresh planner loop (planner.FusedPlanner: plan -> masked +
+                   statistics pass -> update, no host synchronisation); "refresh_pre" is accepted
+                   as the same loop: the fused loop reproduces that mode's decisions
+                   (src/kvskip_attn.py:399-478), here on the device from the first step on
+  "replay"         masked + statistics decode over KVSKIP.plans[layer][t] (one kvskip.Plan per step)
+The reference's "refresh" mode (a host-side torch planner, src/kvskip_attn.py:215-270) is not on
+this path and raises.
+
+Not in the reference: KVSKIP.ids (token ids [B, >= T] int32 on the device) lets the planner find the
+token index itself instead of reading idx_blocks, and KVSKIP.carry lets each layer's planner update
+run inside the next layer's split pass (planner.UpdateCarrier; flush() before reading the state).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+from . import kvskip as K
+from .planner import FusedPlanner, Policy, UpdateCarrier
+
+BLOCK = 64
+
+try:  # the plugin registry and the cache base classes come from transformers when it is present
+    from transformers import AttentionInterface
+    from transformers.cache_utils import Cache, DynamicLayer
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+    HAVE_TRANSFORMERS = True
+except ImportError:  # pragma: no cover - transformers is part of the image
+    HAVE_TRANSFORMERS = False
+    DynamicLayer = object
+
+
+@dataclass
+class KvskipConfig:
+    """Plugin configuration; the fields and defaults of src/kvskip_attn.py:116-140 plus ids, carry."""
+    mode: str = "dense"
+    level: float = 0.99
+    tau: float = 1e-4
+    delta: float = 0.05
+    max_age: int = 32
+    local: int = 2
+    dense_layers: tuple = (0,)
+    dense_heads: tuple = ()          # (layer, kv_head) pairs refreshed on every step
+    index_heads: tuple = ()          # (layer, kv_head) pairs on the token index
+    index_union: bool = False
+    idx_blocks: object = None        # this step's token-index blocks [B, >= nb] bool (set by the driver)
+    calib: float | None = None
+    calib_hold: int = 0
+    calib_warm: tuple = ()
+    calib_free: bool = False
+    calib_kind: str = "logit"
+    calib_auto_ix: float | None = None
+    count: bool = True
+    record: bool = False             # refresh modes: append each step's read mask to plans[layer]
+    ids: object = None               # token ids [B, >= T] int32 on the device (index found on the device)
+    carry: bool = True               # updates ride on the next layer's split pass
+    state: dict = field(default_factory=dict)
+    log: dict = field(default_factory=dict)
+    plans: dict = field(default_factory=dict)
+    carrier: UpdateCarrier = field(default_factory=UpdateCarrier)
+
+    def policy(self, layer: int) -> Policy:
+        """The planner policy of one layer (its dense and index KV heads)."""
+        return Policy(delta=self.delta, max_age=self.max_age, level=self.level, local=self.local,
+                      calib=self.calib, calib_kind=self.calib_kind, calib_hold=self.calib_hold,
+                      calib_warm=tuple(self.calib_warm), calib_free=self.calib_free,
+                      calib_auto_ix=self.calib_auto_ix,
+                      dense_heads=tuple(h for (l, h) in self.dense_heads if l == layer),
+                      index_heads=tuple(h for (l, h) in self.index_heads if l == layer),
+                      index_union=self.index_union)
+
+    def flush(self):
+        """Launch a layer update still held by the carrier (before reading planner state)."""
+        self.carrier.flush()
+
+    def reset(self):
+        self.flush()
+        self.state.clear()
+        self.log.clear()
+
+
+KVSKIP = KvskipConfig()
+
+
+def _count(layer, key, value):
+    if not KVSKIP.count:
+        return
+    d = KVSKIP.log.setdefault(layer, {})
+    d[key] = d.get(key, 0.0) + value
+
+
+def log_totals() -> dict:
+    """Counters summed over layers, as floats (one host synchronisation per counter)."""
+    out = {}
+    for d in KVSKIP.log.values():
+        for key, val in d.items():
+            out[key] = out.get(key, 0.0) + float(val)
+    return out
+
+
+def _prefill(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
+    if HAVE_TRANSFORMERS:
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
+    G = query.shape[1] // key.shape[1]  # pragma: no cover
+    out = F.scaled_dot_product_attention(query, key.repeat_interleave(G, 1), value.repeat_interleave(G, 1),
+                                         attn_mask=attention_mask, dropout_p=dropout, scale=scaling,
+                                         is_causal=attention_mask is None and query.shape[2] > 1)
+    return out.transpose(1, 2).contiguous(), None
+
+
+def _refresh(layer, q, k, v, scale):
+    st = KVSKIP.state.setdefault(layer, {})
+    fp = st.get("planner")
+    nb = math.ceil(k.shape[2] / BLOCK)
+    if fp is None:
+        fp = st["planner"] = FusedPlanner(KVSKIP.policy(layer), count=KVSKIP.count,
+                                          carrier=KVSKIP.carrier if KVSKIP.carry else None)
+        if KVSKIP.count:
+            KVSKIP.log[layer] = fp.counters       # the planner's device counters are the layer's
+        out = fp.first(q, k, v, scale)
+    elif KVSKIP.ids is not None and fp.policy.needs_index:
+        out = fp.step(q, k, v, scale, ids=KVSKIP.ids)
+    else:
+        out = fp.step(q, k, v, scale, idx=KVSKIP.idx_blocks if fp.policy.needs_index else None)
+    if KVSKIP.record:
+        KVSKIP.plans.setdefault(layer, []).append(fp.read_mask(nb))
+    return out
+
+
+def kvskip_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """AttentionInterface forward (src/kvskip_attn.py:481-515): query [B, Hq, Sq, D], key / value
+    [B, Hkv, T, D] (the cache's views); returns ([B, Sq, Hq, D], None)."""
+    if query.shape[2] != 1:
+        return _prefill(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
+    layer = module.layer_idx
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    q = query[:, :, 0]
+    mode = "dense" if layer in KVSKIP.dense_layers else KVSKIP.mode
+    if mode == "dense":
+        out = K.decode(q, key, value, scaling)["out"]
+    elif mode == "vskip2":
+        out = K.vskip_two_pass(q, key, value, scaling, rule="topp", value=KVSKIP.level, local=KVSKIP.local,
+                               sync=False)["out"]
+    elif mode in ("vskip1", "vskip1sink"):
+        st = KVSKIP.state.setdefault(layer, {})
+        r = K.vskip_one_pass(q, key, value, scaling, tau=KVSKIP.tau, local=KVSKIP.local,
+                             lse_prev=st.get("lse") if mode == "vskip1" else None, count=KVSKIP.count, sync=False)
+        st["lse"] = r["lse"]
+        out = r["out"]
+        if KVSKIP.count:
+            _count(layer, "v_tiles", r["v_tiles"].sum())
+            _count(layer, "blocks_total", r["v_tiles"].numel() * math.ceil(key.shape[2] / BLOCK))
+    elif mode in ("refresh_fused", "refresh_pre"):
+        out = _refresh(layer, q, key, value, scaling)
+    elif mode == "replay":
+        st = KVSKIP.state.setdefault(layer, {"t": 0})
+        out = K.decode(q, key, value, scaling, plan=KVSKIP.plans[layer][st["t"]], stats=True)["out"]
+        st["t"] += 1
+    elif mode == "refresh":
+        raise ValueError("mode 'refresh' (the host-side torch planner) is not provided; use 'refresh_fused'")
+    else:
+        raise ValueError(f"unknown kvskip mode {mode!r}")
+    return out[:, None], None
+
+
+def register():
+    """Register the forward and its mask under the name "kvskip" (src/kvskip_attn.py:518-520)."""
+    if not HAVE_TRANSFORMERS:
+        raise RuntimeError("transformers is not importable: nothing to register with")
+    AttentionInterface.register("kvskip", kvskip_attention_forward)
+    AttentionMaskInterface.register("kvskip", sdpa_mask)
+
+
+class GrowingLayer(DynamicLayer):
+    """One layer of the growing cache: keys and values live in a [B, H, capacity, D] buffer whose
+    capacity is a whole number of 64-token blocks; the layer exposes views of its first n tokens
+    (head stride capacity * D, which every kvskip entry point takes). Growth at least doubles the
+    capacity, so appends cost amortised O(1) copies."""
+
+    capacity = 0        # tokens allocated at the first update (the class attribute of GrowingCache(capacity))
+    headroom = 512      # tokens beyond the need allocated on growth
+
+    def lazy_initialization(self, key_states, value_states):
+        super().lazy_initialization(key_states, value_states)
+        self._kbuf = self._vbuf = None
+        self._n = 0
+
+    def _reserve(self, need, like):
+        have = 0 if self._kbuf is None else self._kbuf.shape[-2]
+        if need <= have:
+            return
+        cap = max(need + self.headroom, 2 * have, self.capacity)
+        cap = (cap + BLOCK - 1) // BLOCK * BLOCK
+        B, H, _, D = like.shape
+        kb = torch.empty(B, H, cap, D, dtype=like.dtype, device=like.device)
+        vb = torch.empty_like(kb)
+        if self._n:
+            kb[:, :, :self._n].copy_(self._kbuf[:, :, :self._n])
+            vb[:, :, :self._n].copy_(self._vbuf[:, :, :self._n])
+        self._kbuf, self._vbuf = kb, vb
+
+    def _views(self):
+        self.keys = self._kbuf[:, :, :self._n]
+        self.values = self._vbuf[:, :, :self._n]
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        t = key_states.shape[-2]
+        self._reserve(self._n + t, key_states)
+        self._kbuf[:, :, self._n:self._n + t].copy_(key_states)
+        self._vbuf[:, :, self._n:self._n + t].copy_(value_states)
+        self._n += t
+        self._views()
+        return self.keys, self.values
+
+    def get_seq_length(self) -> int:
+        return self._n if self.is_initialized else 0
+
+    def crop(self, tokens_to_remove: int) -> None:
+        """A negative count drops that many tokens; a positive one is the length to keep (the legacy
+        form of DynamicLayer.crop)."""
+        if not self.is_initialized:
+            return
+        keep = max(0, min(self._n, tokens_to_remove)) if tokens_to_remove > 0 else max(0, self._n + tokens_to_remove)
+        self._n = keep
+        if self._kbuf is not None:
+            self._views()
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        if self.get_seq_length() > 0:
+            self._kbuf = self._kbuf.repeat_interleave(repeats, dim=0)
+            self._vbuf = self._vbuf.repeat_interleave(repeats, dim=0)
+            self._views()
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        if self.get_seq_length() > 0:
+            self._kbuf = self._kbuf[indices].contiguous()
+            self._vbuf = self._vbuf[indices].contiguous()
+            self._views()
+
+
+def GrowingCache(capacity: int = 0):
+    """A transformers Cache of GrowingLayers; capacity: tokens allocated at the first update
+    (src/kvskip_attn.py:110-113)."""
+    if not HAVE_TRANSFORMERS:
+        raise RuntimeError("transformers is not importable")
+    layer = GrowingLayer if not capacity else type("GrowingLayerCap", (GrowingLayer,), {"capacity": int(capacity)})
+    return Cache(layer_class_to_replicate=layer)

@@ -1,0 +1,156 @@
+"""GPU: the attention plugin's decode modes (kvskip_amd.attention.kvskip_attention_forward, the
+reference's src/kvskip_attn.py:481-515) driven the way a model drives them: one call per layer per
+step on the growing cache's strided views. Each mode must give what its kernels give when called
+directly (the same launches: bit for bit), the refresh loop with carried updates the same lists as
+without, and a replay of the recorded lists the refresh loop's outputs within the attention
+tolerance."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from kvskip_amd import attention as A
+from kvskip_amd import kvskip as K
+from kvskip_amd.planner import FusedPlanner
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, B, HQ, HKV, D, T0, STEPS = 3, 1, 16, 4, 128, 1500, 6
+SCALE = D ** -0.5
+
+
+def _data(seed):
+    """Per layer: a prefix K/V [B, Hkv, T0, D] with a few hot blocks, the appended rows and the
+    queries of every step; token ids with repeats for the index heads."""
+    g = torch.Generator().manual_seed(seed)
+    T = T0 + STEPS
+    ks, vs, qs = [], [], []
+    for _ in range(LAYERS):
+        k = torch.randn(B, HKV, T, D, generator=g)
+        qd = torch.randn(B, HKV, 1, D, generator=g)
+        for blk in torch.randint(1, T0 // 64, (3,), generator=g).tolist():
+            k[:, :, blk * 64:(blk + 1) * 64] += 0.4 * qd
+        ks.append(k.to(torch.bfloat16).cuda())
+        vs.append(torch.randn(B, HKV, T, D, generator=g).to(torch.bfloat16).cuda())
+        qs.append([(qd.repeat_interleave(HQ // HKV, 1) + 0.3 * torch.randn(B, HQ, 1, D, generator=g))
+                   .to(torch.bfloat16).cuda() for _ in range(STEPS)])
+    ids = torch.randint(0, 50, (B, T), generator=g, dtype=torch.int32).cuda()
+    return ks, vs, qs, ids
+
+
+def _drive(cfg, ks, vs, qs, ids=None):
+    """Run the plugin over every layer and step (cache appends included); outputs [step][layer]."""
+    A.KVSKIP = cfg
+    cache = A.GrowingCache(capacity=T0 + 64)
+    mods = [SimpleNamespace(layer_idx=l) for l in range(LAYERS)]
+    for l in range(LAYERS):
+        cache.update(ks[l][:, :, :T0 - 1], vs[l][:, :, :T0 - 1], l)
+    outs = []
+    for t in range(STEPS):
+        row = []
+        n = T0 + t
+        if ids is not None:
+            cfg.ids = ids[:, :n].contiguous()
+        for l in range(LAYERS):
+            kk, vv = cache.update(ks[l][:, :, n - 1:n], vs[l][:, :, n - 1:n], l)
+            o, _ = A.kvskip_attention_forward(mods[l], qs[l][t], kk, vv, None, scaling=SCALE)
+            assert o.shape == (B, 1, HQ, D)
+            row.append(o[:, 0].clone())
+        outs.append(row)
+    cfg.flush()
+    return outs, cache
+
+
+def test_dense_and_vskip_modes_match_direct_calls():
+    ks, vs, qs, _ = _data(31)
+    for mode in ("dense", "vskip2", "vskip1", "vskip1sink"):
+        outs, cache = _drive(A.KvskipConfig(mode=mode, dense_layers=(), count=False), ks, vs, qs)
+        lse = [None] * LAYERS
+        for t in range(STEPS):
+            n = T0 + t
+            for l in range(LAYERS):
+                k, v = cache.layers[l]._kbuf[:, :, :n], cache.layers[l]._vbuf[:, :, :n]
+                q = qs[l][t][:, :, 0]
+                if mode == "dense":
+                    ref = K.decode(q, k, v, SCALE)["out"]
+                elif mode == "vskip2":
+                    ref = K.vskip_two_pass(q, k, v, SCALE, rule="topp", value=0.99, local=2, sync=False)["out"]
+                else:
+                    r = K.vskip_one_pass(q, k, v, SCALE, tau=1e-4, local=2,
+                                         lse_prev=lse[l] if mode == "vskip1" else None, sync=False)
+                    lse[l] = r["lse"]
+                    ref = r["out"]
+                assert torch.equal(outs[t][l], ref), (mode, t, l)
+
+
+@pytest.mark.parametrize("index", [False, True])
+def test_refresh_fused_matches_planner_loop(index):
+    """refresh_fused without carried updates is FusedPlanner's own loop (layer 0 dense); with them,
+    the same block lists and triggers on every step and outputs within the merge's summation order."""
+    ks, vs, qs, ids = _data(32)
+    kw = dict(calib=0.05, calib_kind="peak", calib_warm=(4, 2), dense_heads=((2, 1),))
+    if index:
+        kw.update(index_heads=((1, 2),), calib_auto_ix=0.1)
+    cfg = A.KvskipConfig(mode="refresh_fused", carry=False, count=False, record=True, **kw)
+    outs, _ = _drive(cfg, ks, vs, qs, ids if index else None)
+    plain_state = {l: cfg.state[l]["planner"].state for l in range(1, LAYERS)}
+    masks = cfg.plans
+
+    fps = {l: FusedPlanner(cfg.policy(l), count=False) for l in range(1, LAYERS)}
+    for t in range(STEPS):
+        n = T0 + t
+        for l in range(LAYERS):
+            k, v = ks[l][:, :, :n], vs[l][:, :, :n]
+            q = qs[l][t][:, :, 0]
+            if l == 0:
+                ref = K.decode(q, k, v, SCALE)["out"]
+            elif t == 0:
+                ref = fps[l].first(q, k, v, SCALE)
+            else:
+                ref = fps[l].step(q, k, v, SCALE, ids=ids[:, :n].contiguous() if index else None)
+            assert torch.equal(outs[t][l], ref), (t, l)
+    for l in range(1, LAYERS):
+        for key in ("block_idx", "block_cnt", "trig", "age", "keep", "lse_att", "calib", "aix"):
+            assert torch.equal(plain_state[l][key], fps[l].state[key]), (l, key)
+
+    cfg2 = A.KvskipConfig(mode="refresh_fused", carry=True, count=False, record=True, **kw)
+    outs2, _ = _drive(cfg2, ks, vs, qs, ids if index else None)
+    for t in range(STEPS):
+        for l in range(1, LAYERS):
+            assert torch.equal(masks[l][t], cfg2.plans[l][t]), (t, l)
+            a, b = outs[t][l].float(), outs2[t][l].float()
+            assert ((a - b).norm() / a.norm()).item() <= 1e-6, (t, l)
+    for l in range(1, LAYERS):
+        for key in ("block_idx", "block_cnt", "trig", "age", "keep", "lse_att", "calib", "aix"):
+            assert torch.equal(plain_state[l][key], cfg2.state[l]["planner"].state[key]), (l, key)
+
+
+def test_replay_of_recorded_lists():
+    """replay: the masked + statistics decode over the lists recorded by refresh_fused gives that
+    run's outputs (split count may differ: within 2e-3 relative)."""
+    ks, vs, qs, _ = _data(33)
+    cfg = A.KvskipConfig(mode="refresh_fused", count=False, record=True)
+    outs, _ = _drive(cfg, ks, vs, qs)
+    plans = {l: [K.make_plan(m) for m in cfg.plans[l]] for l in cfg.plans}
+    assert sorted(plans) == list(range(1, LAYERS)) and all(len(p) == STEPS for p in plans.values())
+    cfg_r = A.KvskipConfig(mode="replay", count=False, plans=plans)
+    outs_r, _ = _drive(cfg_r, ks, vs, qs)
+    for t in range(STEPS):
+        for l in range(LAYERS):
+            a, b = outs[t][l].float(), outs_r[t][l].float()
+            assert ((a - b).norm() / a.norm()).item() <= 2e-3, (t, l)
+
+
+def test_counters():
+    """Per-layer counters as device tensors; log_totals sums them (blocks read <= blocks total)."""
+    ks, vs, qs, _ = _data(34)
+    cfg = A.KvskipConfig(mode="refresh_fused", count=True)
+    _drive(cfg, ks, vs, qs)
+    tot = A.log_totals()
+    assert tot["blocks_total"] > 0 and 0 < tot["blocks_read"] <= tot["blocks_total"]
+    assert tot["dense_heads"] >= (LAYERS - 1) * B * HKV                     # the first step reads everything
+    cfg = A.KvskipConfig(mode="vskip1", dense_layers=(), count=True)
+    _drive(cfg, ks, vs, qs)
+    tot = A.log_totals()
+    assert 0 < tot["v_tiles"] <= tot["blocks_total"]
