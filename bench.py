@@ -202,17 +202,23 @@ def main():
     log(f"dense split pass: {t_split:.2f} us per launch ({bytes_split / t_split / 1e3:.0f} GB/s), merge "
         f"{t_merge:.2f} us; per-call event medians {ev_split:.2f} / {ev_merge:.2f} us")
     del ops
-    # the read-ceiling kernel over the same bytes, timed the same way (8 buffers of the split pass's
-    # read size, launches back to back): a pure stream of these bytes at this size, launch ramp and
-    # tail included (best of 512 and 768 workgroups)
-    o_r = torch.zeros(1, dtype=torch.int32, device=dev)
-    xr = [torch.ones(bytes_split // 2, dtype=torch.bfloat16, device=dev) for _ in range(NCOPY)]
-    t_read = min(events_region(lambda i: E.read_bw(xr[i], o_r, nblk), args.steps, args.warmup) for nblk in (512, 768))
-    del xr
-    res["dense"].update(read_same_bytes_us=t_read, split_pass_vs_read=t_read / t_split)
-    log(f"read kernel over the same {bytes_split / 1e6:.1f} MB: {t_read:.2f} us per launch "
-        f"({bytes_split / t_read / 1e3:.0f} GB/s); split pass at {100 * t_read / t_split:.1f}% of it")
+
+    def read_same_bytes():
+        # the read-ceiling kernel over the same bytes, timed the same way (8 buffers of the split
+        # pass's read size, launches back to back): a pure stream of these bytes at this size,
+        # launch ramp and tail included (best of 512 and 768 workgroups). Run after the headline
+        # steps: a burst of full-bandwidth reads right before them slows the next ones.
+        o_r = torch.zeros(1, dtype=torch.int32, device=dev)
+        xr = [torch.ones(bytes_split // 2, dtype=torch.bfloat16, device=dev) for _ in range(NCOPY)]
+        t = min(events_region(lambda i: E.read_bw(xr[i], o_r, nblk), args.steps, args.warmup) for nblk in (512, 768))
+        del xr
+        res["dense"].update(read_same_bytes_us=t, split_pass_vs_read=t / t_split)
+        log(f"read kernel over the same {bytes_split / 1e6:.1f} MB: {t:.2f} us per launch "
+            f"({bytes_split / t / 1e3:.0f} GB/s); split pass at {100 * t / t_split:.1f}% of it")
+        return t
+
     if args.roofline_only:
+        t_read = read_same_bytes()
         print(json.dumps({"roofline_only": True, "split_pass_us": t_split, "merge_us": t_merge,
                           "GBs": bytes_split / t_split / 1e3, "read_same_bytes_us": t_read}), flush=True)
         return
@@ -230,6 +236,7 @@ def main():
                                num_splits=S_mask)
     log(f"dense: {us_step:.2f} us/step, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak); "
         f"masked: {us_m:.2f} us/step (x{us_m / us_step:.3f} of dense)")
+    t_read = read_same_bytes()
 
     # ---- two-pass V-skip (kernels/kvskip.py:157-179) on config 2's layer (flat N(0, 1) keys: top-p
     # 0.99 keeps every block, so the path can only show its cost) and on a layer of the config-4

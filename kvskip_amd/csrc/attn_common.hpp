@@ -448,21 +448,16 @@ __device__ __forceinline__ void qk_block_mf(float (&s)[4][4], const u32x4 (&kr)[
 // parameter so every load is unconditional, clamped to S - 1, and in flight together), the
 // classes agree on the max through LDS, then weight (2^(m_s - M), log-sum-exp mode; 1, plain
 // mode for the two-pass pass 2) and add in LDS. WITH_V = false (stats-only): only lse.
-// Body of one merge workgroup (query head hq, dims [32 slice, 32 slice + 32)). A workgroup wider
-// than 256 threads (the fused merge + update launch) runs it with its first 256; the others only
-// pass the barriers.
+// Body of one merge workgroup (query head hq, dims [32 slice, 32 slice + 32)) over its Sv <= 8 U
+// partials. A workgroup wider than 256 threads (the fused merge + update launch) runs it with its
+// first 256; the others only pass the barriers.
 template <int D, int U, bool WITH_V>
-__device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq, int slice) {
+__device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq, int slice, int Sv) {
   constexpr int NC = 8;
   const int tid = threadIdx.x, cls = (tid / 32) % NC, dl = tid % 32;
   const bool act = tid < 256;
   const int d = slice * 32 + dl;
   const int S = p.num_splits;
-  // ragged: (b, hq) has ragged_chunks partials (0: nothing attended, out 0 and lse -inf)
-  const int Sv = p.seq_lens == nullptr
-                     ? S
-                     : ragged_chunks(p, static_cast<int>(hq / p.Hq), static_cast<int>(hq % p.Hq) / (p.Hq / p.Hkv),
-                                     p.block_idx != nullptr);
   const float* ml = p.part_ml + hq * S * 2;
   __shared__ float rA[NC][32], rL[NC], rM[NC];
   float ms[U], ls[U], as[U];
@@ -513,21 +508,38 @@ __device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq
   }
 }
 
-template <int D, int U, bool WITH_V>
-__global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
-  merge_body<D, U, WITH_V>(p, plain, blockIdx.x, blockIdx.y);
+// Partials of query head hq: S, or in a ragged batch its (sequence, KV head)'s chunk count (0:
+// nothing attended, out 0 and lse -inf). Uniform over the workgroup.
+__device__ __forceinline__ int merge_count(const AttnP& p, int64_t hq) {
+  if (p.seq_lens == nullptr) return p.num_splits;
+  return ragged_chunks(p, static_cast<int>(hq / p.Hq), static_cast<int>(hq % p.Hq) / (p.Hq / p.Hkv),
+                       p.block_idx != nullptr);
 }
 
-// merge_body with U chosen at run time (U = ceil(S / 8) rounded up to the instantiated sizes).
+// merge_body with the fewest slots that hold Sv partials (U halved while 4 U still does): a ragged
+// head with few chunks issues no loads for slots it does not have (at S = 128 most heads have a
+// handful of chunks). Sv is uniform, so the choice is a uniform branch.
+template <int D, int U, bool WITH_V>
+__device__ void merge_fit(const AttnP& p, int plain, int64_t hq, int slice, int Sv) {
+  if constexpr (U > 1) {
+    if (Sv <= 8 * (U / 2)) {
+      merge_fit<D, U / 2, WITH_V>(p, plain, hq, slice, Sv);
+      return;
+    }
+  }
+  merge_body<D, U, WITH_V>(p, plain, hq, slice, Sv);
+}
+
+template <int D, int U, bool WITH_V>
+__global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
+  const int64_t hq = blockIdx.x;
+  merge_fit<D, U, WITH_V>(p, plain, hq, blockIdx.y, merge_count(p, hq));
+}
+
+// merge_body with U chosen at run time from the head's partial count.
 template <int D>
 __device__ void merge_body_rt(const AttnP& p, int64_t hq, int slice) {
-  const int u = (p.num_splits + 7) / 8;
-  if (u <= 1) merge_body<D, 1, true>(p, 0, hq, slice);
-  else if (u <= 2) merge_body<D, 2, true>(p, 0, hq, slice);
-  else if (u <= 4) merge_body<D, 4, true>(p, 0, hq, slice);
-  else if (u <= 8) merge_body<D, 8, true>(p, 0, hq, slice);
-  else if (u <= 16) merge_body<D, 16, true>(p, 0, hq, slice);
-  else merge_body<D, MAX_SPLITS / 8, true>(p, 0, hq, slice);
+  merge_fit<D, MAX_SPLITS / 8, true>(p, 0, hq, slice, merge_count(p, hq));
 }
 
 template <int D, bool WITH_V>

@@ -235,6 +235,15 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   const int Tb = seq_T(p.seq_lens, b, p.T);
   const int nb = (Tb + BLK - 1) / BLK;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  if (c * WCB >= nb) {  // a chunk past the sequence's blocks (ragged batch): the empty partial
+    float* part = p.part + (bh * C + c) * SP;
+    if (tid < G) {
+      part[tid] = NEG_INF;
+      part[G + tid] = 0.f;
+    }
+    if (tid == 0) part[2 * G] = __uint_as_float(0u);
+    return;
+  }
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;
   float* csum = p.csum + bh * p.NBC * D;
   const uint8_t* keep = p.keep + bh * p.NBC;
