@@ -7,6 +7,16 @@
 namespace kvs {
 namespace {
 
+// Blocks strictly between list entries prev and cur, clipped to [0, nb): [a, a + len), none if
+// len <= 0. Both entries are clamped first, so no entry value (a caller's list is not validated
+// on the device) can overflow the arithmetic or reach outside the head's statistics.
+__host__ __device__ __forceinline__ void gap_range(int prev, int cur, int nb, int& a, int& len) {
+  prev = prev < -1 ? -1 : (prev > nb - 1 ? nb - 1 : prev);
+  cur = cur < 0 ? 0 : (cur > nb ? nb : cur);
+  a = prev + 1;
+  len = cur - a;
+}
+
 // Masked statistics of the blocks the list skips: (-inf, 0), so the outputs need no fill. The
 // split holding list positions [i0, i0 + n) writes the gap before each of its entries (from the
 // previous entry, or from block 0) and, if it holds the list's last entry, the tail up to nb;
@@ -37,7 +47,8 @@ __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, i
       cur = __builtin_amdgcn_readfirstlane(list(k));
       prev = __builtin_amdgcn_readfirstlane(list(k - 1));
     }
-    const int a = max(prev, -1) + 1, len = min(cur, p.nb) - a;
+    int a, len;
+    gap_range(prev, cur, p.nb, a, len);
     for (int x = lane; x < G * len; x += WAVE) put(x / len, a + x % len);
   }
   if (n > 0 && i0 + n == n_items) {
@@ -79,13 +90,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       if (!t) {
         const int per = (cnt + p.num_splits - 1) / p.num_splits;
         const int a0 = min(cnt, split * per), a1 = min(cnt, a0 + per);
-#pragma unroll
-        for (int j = 0; j < DCL; ++j) {
-          int pos = pre[j];
-          if (pos + __popc(pmk[j]) <= a0 - 1 || pos >= a1) continue;
-          for (uint32_t m = pmk[j]; m != 0; m &= m - 1, ++pos)
-            if (pos >= a0 - 1 && pos < a1) sPl[pos - a0 + 1] = (lane + WAVE * j) * WCB + __ffs(m) - 1;
-        }
+        slice_positions<DCL>(pmk, pre, lane, a0, a1, sPl);
         if (lane == 0 && a0 == 0) sPl[0] = -1;
       }
       if (lane == 0) {

@@ -140,6 +140,24 @@ __device__ __forceinline__ int mask_prefix(const uint32_t (&mk)[DCL], int lane, 
   return base;
 }
 
+// List positions [a0 - 1, a1) of the ascending attended blocks whose chunk masks this lane holds
+// (chunk lane + 64 j: mask mk[j], exclusive prefix pre[j] from mask_prefix) into
+// out[pos - a0 + 1]; position -1 (before the list) is the caller's. Signed arithmetic throughout:
+// with an unsigned popcount in the range test, a0 = 0 made a0 - 1 the largest unsigned value and
+// split 0 skipped every chunk, leaving its slice unwritten.
+template <int NCL>
+__host__ __device__ __forceinline__ void slice_positions(const uint32_t (&mk)[NCL], const int (&pre)[NCL], int lane,
+                                                         int a0, int a1, int* out) {
+#pragma unroll
+  for (int j = 0; j < NCL; ++j) {
+    int pos = pre[j];
+    const int n = static_cast<int>(__builtin_popcount(mk[j]));
+    if (pos + n <= a0 - 1 || pos >= a1) continue;
+    for (uint32_t m = mk[j]; m != 0; m &= m - 1, ++pos)
+      if (pos >= a0 - 1 && pos < a1) out[pos - a0 + 1] = (lane + WAVE * j) * WCB + __builtin_ctz(m);
+  }
+}
+
 // The head's block list and count from its decision: every block (refresh) or the ascending
 // attended blocks of the chunk masks. One wavefront.
 __device__ __forceinline__ void write_block_list(const kvskip_plan_args& p, int64_t bh, int nb, bool tr,

@@ -4,11 +4,13 @@ device too (the reference runs its Python planner for it, src/kvskip_attn.py:445
 
 Per decode step: plan (estimate, refresh decision, block list) -> masked + block-statistics
 attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
-Four launches per layer-step (plan: scores + decide; the split pass; the split merge and update
-together), all on the current stream, no host synchronisation, no allocation after the first step
-of a capacity: the pass writes into buffers the planner owns. With an UpdateCarrier shared by the
-planners of a model's layers, a layer's update instead runs inside the next layer's split pass
-(one launch, kvskip_decode_splits_update) and the merge runs alone.
+Three launches per layer-step without seq_lens (plan's scores pass; the split pass, whose
+workgroups also make plan's decision from the scores partials, kvskip_decode_splits_planned; the
+split merge and update together), four with them (plan's decision in a launch of its own), all on
+the current stream, no host synchronisation, no allocation after the first step of a capacity: the
+pass writes into buffers the planner owns. With an UpdateCarrier shared by the planners of a
+model's layers, a layer's update instead runs inside the next layer's split pass and the merge runs
+alone.
 
 The policy fields follow KvskipConfig (src/kvskip_attn.py:116-147) for one layer.
 """
@@ -112,11 +114,11 @@ class FusedPlanner:
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
-                 decide_in_pass: bool = False):
+                 decide_in_pass: bool = True):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
-        # plan's decision inside the masked pass (not ragged): off, its first GPU run faulted and
-        # the cause is not found yet
+        # plan's decision inside the masked pass (batches without seq_lens): one launch fewer per
+        # step, the same decisions and lists as plan's own decision launch
         self.decide_in_pass = decide_in_pass
         self._pargs = None
         self.state = None

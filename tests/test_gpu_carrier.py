@@ -102,8 +102,6 @@ def test_decode_splits_update_rejects_group_mismatch(gpu):
         E.decode_splits_update(q2, k, k, 0.125, bufs, bi, bc, 2, u)
 
 
-@pytest.mark.skip(reason="decision-in-pass path (kvskip_decode_splits_planned) switched off: its first GPU run "
-                         "faulted and the cause is not found yet")
 @pytest.mark.parametrize("G,D,heads", [(4, 128, {}), (8, 64, {"dense_heads": (1,), "index_heads": (0,)}),
                                        (7, 128, {"index_heads": (2,), "index_union": True})])
 def test_decision_in_pass_matches_plan(gpu, G, D, heads):
