@@ -58,11 +58,12 @@ __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, i
 }
 
 // The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads. PLANNED (masked,
-// not ragged): the list is the plan's decision for (b, h), made in this workgroup's prologue from
-// the scores pass's partials (pa): wavefront 0 decides (as plan_decide; every workgroup of the
-// head reaches the same result from the same partials) and puts the list positions of this split
-// into LDS; split 0 also stores trig, est and, at its end, the head's block list and count (the
-// age is advanced by the update).
+// unragged partition): the list is the plan's decision for (b, h), made in this workgroup's
+// prologue from the scores pass's partials (pa): wavefront 0 decides (as plan_decide; every
+// workgroup of the head reaches the same result from the same partials) and puts the list
+// positions of this split into LDS; split 0 also stores trig, est and, at its end, the head's block
+// list and count (the age is advanced by the update). With seq_lens (one sequence) its length
+// comes from device memory; the grid is still num_splits x Hkv x B.
 template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
   static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
@@ -83,10 +84,14 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   bool dense = false;                             // planned: a refresh (every block, in order)
   if constexpr (PLANNED) {
     work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
+    if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
+      Tb = seq_len(p, b);
+      nbb = (Tb + BLK - 1) / BLK;
+    }
     if (wave == 0) {
       int pre[DCL];
       const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0, false);
-      const int cnt = t ? p.nb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
+      const int cnt = t ? nbb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
       if (!t) {
         const int per = (cnt + p.num_splits - 1) / p.num_splits;
         const int a0 = min(cnt, split * per), a1 = min(cnt, a0 + per);
@@ -384,7 +389,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
   if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
   if constexpr (PLANNED) {
-    if (split == 0 && wave == 0) write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, p.nb, dense, pmk, lane);
+    if (split == 0 && wave == 0) write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, nbb, dense, pmk, lane);
   }
   if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
     if (nbb < p.nb && i0 + n == n_items) {

@@ -309,8 +309,11 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
   if (rc != KVSKIP_OK) return rc;
   if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
   if (pl->part == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_planned needs the plan's part workspace");
-  if (pl->seq_lens != nullptr || a->seq_lens != nullptr)
-    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: no ragged batches (plan and decide separately)");
+  if (pl->seq_lens != a->seq_lens)
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: the plan and the pass must share seq_lens");
+  if (a->seq_lens != nullptr && a->B != 1)
+    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: seq_lens only for one sequence (B 1; plan and decide "
+                                      "separately for a ragged batch)");
   if (a->B != pl->B || a->Hq != pl->Hq || a->Hkv != pl->Hkv || a->T != pl->T || a->D != pl->D)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
   kvskip_attn_args am = *a;  // the pass's list is the plan's

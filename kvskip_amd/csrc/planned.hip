@@ -24,15 +24,18 @@ __global__ void __launch_bounds__(NT, 2) planned_split_kernel(const AttnP a, con
   decode_body<D, G, true, true, true, true, false, true>(a, i - n_update, &pa);
 }
 
+// The pass's grid is num_splits x Hkv x B workgroups whether or not seq_lens is given (B is 1 then):
+// the list of a (b, KV head) is cut into num_splits slices as in the unragged pass.
 template <int D, int G>
 hipError_t launch_planned_t(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, hipStream_t s) {
   const dim3 blk(NT);
+  const int n_pass = a.num_splits * a.Hkv * a.B;
   if (u == nullptr) {
-    hipLaunchKernelGGL((planned_split_kernel<D, G, 0>), attn_grid(a), blk, 0, s, a, pa, kvskip_update_args{});
+    hipLaunchKernelGGL((planned_split_kernel<D, G, 0>), dim3(n_pass), blk, 0, s, a, pa, kvskip_update_args{});
     return hipGetLastError();
   }
   const int nb = (u->T + BLK - 1) / BLK;
-  const dim3 grid(attn_grid(a).x + u->B * u->Hkv);
+  const dim3 grid(n_pass + u->B * u->Hkv);
   if (nb <= 2 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 2>), grid, blk, 0, s, a, pa, *u);
   else if (nb <= 4 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 4>), grid, blk, 0, s, a, pa, *u);
   else if (nb <= 8 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 8>), grid, blk, 0, s, a, pa, *u);

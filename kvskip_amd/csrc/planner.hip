@@ -235,6 +235,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   const int Tb = seq_T(p.seq_lens, b, p.T);
   const int nb = (Tb + BLK - 1) / BLK;
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  if (p.seq_lens_out != nullptr && c == 0 && h == 0 && tid == 0) p.seq_lens_out[b] = Tb;  // also when decided in the pass
   if (c * WCB >= nb) {  // a chunk past the sequence's blocks (ragged batch): the empty partial
     float* part = p.part + (bh * C + c) * SP;
     if (tid < G) {

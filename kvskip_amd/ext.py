@@ -334,10 +334,12 @@ def plan_scores(pargs: PlanArgs, device):
         _native.check(_native.lib().kvskip_plan_scores(ctypes.byref(pargs), _stream(dev)))
 
 
-def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None):
+def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None,
+                          seq_lens=None):
     """plan's decision and the masked + statistics split pass in one launch (kvskip_decode_splits_planned;
     after plan_scores(pargs)); the whole op when num_splits == 1. The layer's update must advance the
-    age (update_struct(..., age=...)). update: another layer's update to carry, or None."""
+    age (update_struct(..., age=...)). update: another layer's update to carry, or None. seq_lens: the
+    plan's (one sequence, B 1)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -354,7 +356,7 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
         _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
                  "bufs: split partials")
     a = _decode_args(q, k, v, scale, None, None, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None, None,
-                     part_acc, part_ml, None)
+                     part_acc, part_ml, seq_lens)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(pargs),

@@ -4,9 +4,10 @@ device too (the reference runs its Python planner for it, src/kvskip_attn.py:445
 
 Per decode step: plan (estimate, refresh decision, block list) -> masked + block-statistics
 attention over the list -> update (top-p union, references, calibration, attended log-sum-exp).
-Three launches per layer-step without seq_lens (plan's scores pass; the split pass, whose
-workgroups also make plan's decision from the scores partials, kvskip_decode_splits_planned; the
-split merge and update together), four with them (plan's decision in a launch of its own), all on
+Three launches per layer-step unless the batch is ragged (plan's scores pass; the split pass,
+whose workgroups also make plan's decision from the scores partials, kvskip_decode_splits_planned;
+the split merge and update together), four for a ragged batch (plan's decision in a launch of its
+own; seq_lens with one sequence is not ragged), all on
 the current stream, no host synchronisation, no allocation after the first step of a capacity: the
 pass writes into buffers the planner owns. With an UpdateCarrier shared by the planners of a
 model's layers, a layer's update instead runs inside the next layer's split pass and the merge runs
@@ -190,7 +191,7 @@ class FusedPlanner:
         self._S = S
         carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         if self._pargs is not None:
-            E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried)
+            E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens)
         elif carried is not None:
             E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens)
         else:
@@ -219,10 +220,10 @@ class FusedPlanner:
             E.update(*update_args, **update_kwargs)
 
     def _plan(self, q, plan_args, plan_kwargs, seq_lens):
-        """plan (scores + decision), or, with decide_in_pass and no ragged batch, its scores pass
-        alone: the decision then runs in the masked pass (kvskip_decode_splits_planned) and the
-        update advances the age."""
-        if self.decide_in_pass and seq_lens is None:
+        """plan (scores + decision), or, with decide_in_pass and no ragged batch (seq_lens absent or
+        one sequence), its scores pass alone: the decision then runs in the masked pass
+        (kvskip_decode_splits_planned) and the update advances the age."""
+        if self.decide_in_pass and (seq_lens is None or q.shape[0] == 1):
             self._pargs = E.plan_struct(*plan_args, **plan_kwargs)
             E.plan_scores(self._pargs, q.device)
         else:

@@ -117,19 +117,22 @@ def test_decision_in_pass_matches_plan(gpu, G, D, heads):
     qps = [W.QueryProcess(run, l, p_jump=0.1, revert=True) for l in range(layers)]
     qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
     pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1, **heads)
-    for carry in (False, True):
+    for carry, dyn in ((False, False), (True, False), (True, True)):
+        # dyn: the step's length in device memory (seq_lens, one sequence) over full-capacity views
         ref = [FusedPlanner(pol(), count=False, decide_in_pass=False) for _ in range(layers)]
         cr = UpdateCarrier() if carry else None
         dut = [FusedPlanner(pol(), count=False, carrier=cr, decide_in_pass=True) for _ in range(layers)]
         for t in range(steps):
             T = T0 + t + 1
+            sl = torch.tensor([T], dtype=torch.int32, device="cuda") if dyn else None
             for l in range(layers):
-                kv = (ks[l][:, :, :T], vs[l][:, :, :T])
+                kv = (ks[l], vs[l]) if dyn else (ks[l][:, :, :T], vs[l][:, :, :T])
                 outs = []
                 for fp in (ref[l], dut[l]):
-                    o = fp.first(qs[t][l], *kv, run.scale) if t == 0 else fp.step(qs[t][l], *kv, run.scale, ids=ids)
+                    o = (fp.first(qs[t][l], *kv, run.scale, seq_lens=sl) if t == 0
+                         else fp.step(qs[t][l], *kv, run.scale, ids=ids, seq_lens=sl))
                     outs.append(o.clone())
-                assert torch.equal(outs[0], outs[1]), (carry, t, l)
+                assert torch.equal(outs[0], outs[1]), (carry, dyn, t, l)
             if cr is not None:
                 cr.flush()
             _same_state(ref, dut, t)

@@ -233,7 +233,7 @@ def test_merge_update_matches_separate_launches(gpu):
     pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8))
     qp = W.QueryProcess(run, 0, p_jump=0.3)
     k, v = run.k[0].cuda(), run.v[0].cuda()
-    fp = FusedPlanner(dpolicy(pol))
+    fp = FusedPlanner(dpolicy(pol), decide_in_pass=False)     # the test plans with plan() itself
     T = run.T0[0] + 1
     fp.first(qp.next().cuda(), k[:, :, :T], v[:, :, :T], run.scale)
     T += 1
