@@ -85,6 +85,16 @@ typedef struct kvskip_attn_args {
    * so every workgroup gets at most C whatever the lengths; needs num_splits >= 2, B <= 256, and
    * part_acc / part_ml of [B, Hq, num_splits, ...]. */
   const int32_t* seq_lens;
+
+  /* Paged cache (not in the reference; the split pass of kvskip_decode / kvskip_decode_splits, with
+   * V, MFMA engine): k and v point to page pools of 64-token pages; token t of sequence b, KV head h
+   * is row t % 64 of page block_table[b * bt_stride + t / 64], at k + page * k_sb + h * k_sh +
+   * (t % 64) * k_st (k_sb, v_sb: the page stride). T is the sequences' length (or capacity with
+   * seq_lens); bt_stride >= ceil(T / 64). A page id outside [0, num_pages) makes its block empty
+   * (scores -inf, statistics (-inf, 0)); no memory outside the pools is read. */
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int32_t num_pages;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block

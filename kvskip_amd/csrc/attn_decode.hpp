@@ -64,9 +64,11 @@ __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, i
 // positions of this split into LDS; split 0 also stores trig, est and, at its end, the head's block
 // list and count (the age is advanced by the update). With seq_lens (one sequence) its length
 // comes from device memory; the grid is still num_splits x Hkv x B.
-template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false>
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false,
+          bool PAGED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
   static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
+  static_assert(!PAGED || (MF && LOAD_V && !PLANNED), "a paged cache is read by the MFMA pass with V");
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
@@ -153,6 +155,23 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
     else
       return glist[pos];
   };
+  // Paged cache: the page (and, with a list, the block) of each of this workgroup's items i0 + t,
+  // t < n, gathered into LDS once, so the streaming loop reads them without a vector-memory wait.
+  // Blocks outside the sequence and page ids outside [0, num_pages) become -1 (an empty block).
+  __shared__ int sPg[PAGED ? MAX_NB : 1];
+  __shared__ int sBk[PAGED && MASKED ? MAX_NB : 1];
+  if constexpr (PAGED) {
+    const int* tbl = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+    for (int t = tid; t < n; t += NT) {
+      int blk = MASKED ? glist[i0 + t] : i0 + t;
+      if (blk < 0 || blk >= nbb) blk = -1;
+      int pg = blk >= 0 ? tbl[blk] : -1;
+      if (pg < 0 || pg >= p.num_pages) pg = -1;
+      sPg[t] = pg;
+      if constexpr (MASKED) sBk[t] = blk;
+    }
+    __syncthreads();
+  }
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
   int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this lane's gap
   if constexpr (MASKED && STATS) {
@@ -217,10 +236,11 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       mr[i] = NEG_INF;
       lr[i] = 0.f;
     }
-    auto process = [&](int blk, const u32x4 (&kr)[4][KS], float (&alpha)[G]) {
+    // block blk's scores (tokens >= lim masked: lim = Tb, or 0 for an empty block), statistics and P
+    auto process = [&](int blk, int lim, const u32x4 (&kr)[4][KS], float (&alpha)[G]) {
       const int t0 = blk >= 0 ? blk * BLK : 0;
       float s[4][4];
-      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, blk >= 0 ? Tb : 0, lane);
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, lim, lane);
       float pv[4][4], ar[4];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -280,7 +300,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
         __builtin_amdgcn_sched_barrier(0);
         if (k < nw) {
           float alpha[G];
-          process(bac, ac, alpha);
+          process(bac, bac >= 0 ? Tb : 0, ac, alpha);
         }
         __builtin_amdgcn_sched_barrier(0);
       };
@@ -288,6 +308,52 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
         step(kb, b1, ka, b0, k);
         step(ka, b0, kb, b1, k + 1);
       }
+    } else if (nw > 0 && PAGED) {
+      // item k: LDS slot wave + NWAVE k; each block's K / V resource spans its page's rows of this
+      // head that hold tokens (zeros beyond), an empty block's spans nothing
+      u32x4 kr[4][KS];
+      u32x4 vr[Lay<D>::VN];
+      auto item = [&](int k, int& blk, int& pg) {
+        const int t = wave + NWAVE * k;
+        pg = __builtin_amdgcn_readfirstlane(sPg[t]);
+        if constexpr (MASKED)
+          blk = __builtin_amdgcn_readfirstlane(sBk[t]);
+        else
+          blk = i0 + t;
+      };
+      // the resource's base is placed blk * 64 rows before the page, so the block's loads use the
+      // same offsets (token t0 = 64 blk) as in a contiguous cache; its range ends at the block's last
+      // token, and no offset below the page is ever formed
+      auto page_rsrc = [&](const uint16_t* pool, int64_t psb, int64_t sh, int64_t st, int blk, int pg) {
+        if (blk < 0 || pg < 0) return make_rsrc(pool, 0u);
+        return make_rsrc(pool + static_cast<int64_t>(pg) * psb + static_cast<int64_t>(h) * sh -
+                             static_cast<int64_t>(blk) * BLK * st,
+                         head_bytes(min(Tb, blk * BLK + BLK), st, D));
+      };
+      auto lim_of = [&](int blk, int pg) { return (blk >= 0 && pg >= 0) ? Tb : 0; };
+      int blk, pg;
+      item(0, blk, pg);
+      load_k_block_mf<D>(kr, page_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, blk, pg), koffm, p.k_st, max(blk, 0) * BLK);
+      load_v_block<D>(vr, page_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, blk, pg), voff, p.v_st, max(blk, 0) * BLK);
+      for (int k = 0; k + 1 < nw; ++k) {
+        int blk_n, pg_n;
+        item(k + 1, blk_n, pg_n);
+        const rsrc_t rk_n = page_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, blk_n, pg_n);
+        const rsrc_t rv_n = page_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, blk_n, pg_n);
+        float alpha[G];
+        process(blk, lim_of(blk, pg), kr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k_block_mf<D>(kr, rk_n, koffm, p.k_st, max(blk_n, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        accumulate(vr, alpha);
+        __builtin_amdgcn_sched_barrier(0);
+        load_v_block<D>(vr, rv_n, voff, p.v_st, max(blk_n, 0) * BLK);
+        blk = blk_n;
+        pg = pg_n;
+      }
+      float alpha[G];
+      process(blk, lim_of(blk, pg), kr, alpha);
+      accumulate(vr, alpha);
     } else if (nw > 0) {
       u32x4 kr[4][KS];
       u32x4 vr[Lay<D>::VN];
@@ -300,7 +366,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
         const int blk_n = block_of(e_n, k + 1);
         e_n = e_nn;
         float alpha[G];
-        process(blk, kr, alpha);
+        process(blk, blk >= 0 ? Tb : 0, kr, alpha);
         __builtin_amdgcn_sched_barrier(0);
         load_k_block_mf<D>(kr, rk, koffm, p.k_st, max(blk_n, 0) * BLK);
         __builtin_amdgcn_sched_barrier(0);
@@ -312,7 +378,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
         blk = blk_n;
       }
       float alpha[G];
-      process(blk, kr, alpha);
+      process(blk, blk >= 0 ? Tb : 0, kr, alpha);
       if constexpr (LOAD_V) accumulate(vr, alpha);
     }
 #pragma unroll

@@ -90,6 +90,9 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->vcount = a->vcount;
   p->lse_prev = a->lse_prev;
   p->seq_lens = a->seq_lens;
+  p->block_table = a->block_table;
+  p->bt_stride = a->bt_stride;
+  p->num_pages = a->num_pages;
   return KVSKIP_OK;
 }
 
@@ -139,6 +142,20 @@ static int check_decode(const kvskip_attn_args* a, int stats, int load_v, int ph
     if (a->B > kvs::MAX_RAGGED_B) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: B <= %d", kvs::MAX_RAGGED_B);
     if (a->p_out != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: no fp16 P output");
   }
+  if (a->block_table != nullptr && (phase & 1)) {  // paged cache (the merge alone reads no K / V)
+    if (!load_v || a->p_out != nullptr)
+      return fail(KVSKIP_E_UNSUPPORTED, "paged cache: the pass with V only (no stats-only pass, no fp16 P)");
+    if (!kvs::qk_use_mfma()) return fail(KVSKIP_E_UNSUPPORTED, "paged cache: MFMA engine only");
+    if (a->num_pages < 1) return fail(KVSKIP_E_INVALID, "paged cache: num_pages >= 1");
+    if (a->bt_stride < p->nb) return fail(KVSKIP_E_INVALID, "paged cache: block_table rows must hold ceil(T / 64) pages");
+    // the pages of one workgroup's items are gathered into LDS: at most MAX_NB of them
+    const int64_t items = masked ? a->max_blocks : p->nb;
+    const int64_t per = a->seq_lens != nullptr ? (a->B * items + a->num_splits - 1) / a->num_splits
+                                               : (items + a->num_splits - 1) / a->num_splits;
+    if (per > kvs::planner_max_blocks(1))
+      return fail(KVSKIP_E_UNSUPPORTED, "paged cache: at most %d blocks per split (raise num_splits)",
+                  kvs::planner_max_blocks(1));
+  }
   if (!load_v) p->out = nullptr;
   return KVSKIP_OK;
 }
@@ -170,6 +187,7 @@ int kvskip_pv(const kvskip_attn_args* a, void* stream) {
   int rc = prepare_attn(a, false, false, true, &p);
   if (rc != KVSKIP_OK) return rc;
   if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "pv: seq_lens is not supported");
+  if (a->block_table != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "pv: paged caches are not supported");
   if (a->p_in == nullptr) return fail(KVSKIP_E_INVALID, "P: fp16 [B, Hq, t_pad]");
   if (!aligned16(a->p_in)) return fail(KVSKIP_E_INVALID, "P must be 16-byte aligned");
   if (a->blk_scale == nullptr) return fail(KVSKIP_E_INVALID, "blk_scale: contiguous fp32 [B, Hkv, nb, G]");
@@ -187,6 +205,7 @@ int kvskip_vskip1(const kvskip_attn_args* a, void* stream) {
   int rc = prepare_attn(a, true, true, true, &p);
   if (rc != KVSKIP_OK) return rc;
   if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "vskip1: seq_lens is not supported");
+  if (a->block_table != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "vskip1: paged caches are not supported");
   if (!(a->tau > 0.f) || a->local < 0) return fail(KVSKIP_E_INVALID, "tau > 0, local >= 0, num_splits >= 1");
   if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
   if (a->num_splits > 1 && a->part_acc == nullptr)
@@ -296,6 +315,8 @@ int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_a
   kvs::AttnP p;
   int rc = check_decode(a, 1, 1, a != nullptr && a->num_splits > 1 ? 1 : 3, &p);
   if (rc != KVSKIP_OK) return rc;
+  if (a->block_table != nullptr)
+    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_update: paged caches are not supported (update separately)");
   if ((rc = check_update(u)) != KVSKIP_OK) return rc;
   if (a->block_idx == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_update: the pass needs a block list");
   if (a->Hq / a->Hkv != u->Hq / u->Hkv)
@@ -308,6 +329,8 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
   int rc = check_plan(pl);
   if (rc != KVSKIP_OK) return rc;
   if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (a->block_table != nullptr)
+    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: paged caches are not supported (plan and decide first)");
   if (pl->part == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_planned needs the plan's part workspace");
   if (pl->seq_lens != a->seq_lens)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: the plan and the pass must share seq_lens");

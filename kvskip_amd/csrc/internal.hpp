@@ -39,6 +39,9 @@ struct AttnP {
   int* vcount;
   const float* lse_prev;
   const int* seq_lens;  // [B] or null: sequence b uses tokens [0, clamp(seq_lens[b], 1, T))
+  const int* block_table;  // [B, bt_stride] or null: paged K / V (page stride k_sb / v_sb)
+  int64_t bt_stride;
+  int num_pages;
 };
 
 constexpr int MAX_RAGGED_B = 256;  // batch bound of the ragged partition (one scan per 64)

@@ -77,8 +77,29 @@ def _attn_args(q, k, v, scale, B, Hq, Hkv, T, D) -> AttnArgs:
     return a
 
 
+def _kv_dims(q, k, v, block_table=None, T=None):
+    """(B, Hq, D, Hkv, T) of an attention call over views [B, Hkv, T, D], or (block_table given, not
+    in the reference) over page pools k, v [num_pages, Hkv, 64, D] whose page block_table[b, j] holds
+    tokens 64 j .. 64 j + 63 of sequence b; T is then required (the tokens, or the capacity with
+    seq_lens)."""
+    B, Hq, D = q.shape
+    Hkv = k.shape[1]
+    if block_table is None:
+        return B, Hq, D, Hkv, k.shape[2]
+    _require(T is not None and int(T) >= 1, "paged cache: T (tokens per sequence, or the capacity) is required")
+    T = int(T)
+    _require(k.dim() == 4 and v.dim() == 4 and k.shape[2] == TILE and v.shape[2] == TILE and v.shape[0] == k.shape[0]
+             and v.shape[1] == Hkv and k.shape[3] == D and v.shape[3] == D,
+             "paged cache: k, v must be page pools [num_pages, Hkv, 64, D]")
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+             and block_table.shape[0] == B and block_table.stride(1) == 1
+             and block_table.shape[1] >= (T + TILE - 1) // TILE,
+             "block_table: int32 [B, >= ceil(T / 64)] on the device, rows contiguous")
+    return B, Hq, D, Hkv, T
+
+
 def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
-           want_f32=False, write_p=False, seq_lens=None):
+           want_f32=False, write_p=False, seq_lens=None, block_table=None, T=None):
     """Split-K decode attention (kernels/kvskip_ext.cpp:25-101).
 
     Returns [out bf16 [B,Hq,D], lse fp32 [B,Hq], blk_max, blk_sum ([B,Hq,nb] or None), out_f32 (or None),
@@ -86,14 +107,15 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
 
     seq_lens (not in the reference): int32 [B] on the device, a ragged batch; sequence b attends
     tokens [0, clamp(seq_lens[b], 1, T)) of its view; num_splits is then the per-KV-head split
-    budget over the whole batch (>= 2)."""
+    budget over the whole batch (>= 2).
+    block_table, T (not in the reference): a paged cache, see _kv_dims (the pass with V, MFMA engine)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
-    _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
-             and v.shape[2] == T, "shape mismatch between q, k, v")
+    B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
+    if block_table is None:
+        _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
+                 and v.shape[2] == T, "shape mismatch between q, k, v")
     _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
     _require(1 <= num_splits <= 256, "num_splits in 1..256")
     _require(load_v or stats, "load_v=false only makes sense with stats=true")
@@ -115,22 +137,22 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
         part_acc = torch.empty(B, Hq, num_splits, D, **f32) if load_v else None
         part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens)
+                   pbuf, part_acc, part_ml, seq_lens, block_table=block_table, T=T)
     return [out, lse, bmax, bsum, out32, pbuf]
 
 
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,
-                seq_lens=None, phase=3):
+                seq_lens=None, phase=3, block_table=None, T=None):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
     [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
     (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way.
-    phase: 3 = the whole op, 1 = the split pass only (its merge left to merge_splits / merge_update)."""
+    phase: 3 = the whole op, 1 = the split pass only (its merge left to merge_splits / merge_update).
+    block_table, T: a paged cache (see _kv_dims)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
     _require(1 <= num_splits <= 256, "num_splits in 1..256")
     nb = (T + TILE - 1) // TILE
     out, lse = bufs["out"], bufs["lse"]
@@ -148,7 +170,7 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
         _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
-                   part_acc, part_ml, seq_lens, phase)
+                   part_acc, part_ml, seq_lens, phase, block_table, T)
 
 
 class DecodeOp:
@@ -193,10 +215,11 @@ class DecodeOp:
 
 
 def _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
-                 part_ml, seq_lens=None) -> AttnArgs:
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+                 part_ml, seq_lens=None, block_table=None, T=None) -> AttnArgs:
+    B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
+    if block_table is not None:          # page pools: k_sb / v_sb (their dim-0 strides) are the page strides
+        a.block_table, a.bt_stride, a.num_pages = block_table.data_ptr(), block_table.stride(0), k.shape[0]
     if seq_lens is not None:
         _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
                  and seq_lens.numel() == B, "seq_lens: contiguous CUDA int32 [B]")
@@ -221,9 +244,9 @@ _PHASES = {3: "kvskip_decode", 1: "kvskip_decode_splits", 2: "kvskip_merge_split
 
 
 def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens=None, phase=3):
+                   pbuf, part_acc, part_ml, seq_lens=None, phase=3, block_table=None, T=None):
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
-                     part_ml, seq_lens)
+                     part_ml, seq_lens, block_table, T)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(getattr(_native.lib(), _PHASES[phase])(ctypes.byref(a), int(bool(stats)), int(bool(load_v)),

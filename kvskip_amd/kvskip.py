@@ -82,22 +82,25 @@ def make_plan(keep: torch.Tensor, sync: bool = True) -> Plan:
 
 def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = False, load_v: bool = True,
            num_splits: int | None = None, stages: int = 2, out_f32: bool = False, write_p: bool = False,
-           seq_lens: torch.Tensor | None = None) -> dict:
+           seq_lens: torch.Tensor | None = None, block_table: torch.Tensor | None = None,
+           T: int | None = None) -> dict:
     """Decode attention for one layer (kernels/kvskip.py:88-113). Returns dict(out [B, Hq, D] bf16,
     lse [B, Hq] fp32, blk_max / blk_sum [B, Hq, nb] fp32 (stats), out_f32 (if asked), p (write_p:
-    fp16 [B, Hq, nb*64] = exp(s - blk_max))). seq_lens (int32 [B] on the device, not in the
-    reference): a ragged batch over views of capacity T, with the split budget shared by the batch."""
+    fp16 [B, Hq, nb*64] = exp(s - blk_max))). Not in the reference: seq_lens (int32 [B] on the
+    device): a ragged batch over views of capacity T, with the split budget shared by the batch;
+    block_table (int32 [B, >= ceil(T / 64)]) with T: k, v are page pools [num_pages, Hkv, 64, D]."""
     if q.dim() == 4:
         q = q.squeeze(2)
     B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
     nb = math.ceil(T / TILE)
     n_items = nb if plan is None else plan.max_cnt
     if num_splits is None:
         num_splits = num_splits_for(B * Hkv, n_items) if seq_lens is None else ragged_splits(B, Hkv, n_items)
+    paged = {} if block_table is None else dict(block_table=block_table, T=T)
     res = ext().decode(q, k, v, float(scale), None if plan is None else plan.block_idx,
                        None if plan is None else plan.block_cnt, stats, load_v, int(num_splits), int(stages),
-                       out_f32, write_p, seq_lens)
+                       out_f32, write_p, seq_lens, **paged)
     out, lse, bmax, bsum, o32, pbuf = res
     d = {"out": out if load_v else None, "lse": lse, "num_splits": num_splits}
     if stats:

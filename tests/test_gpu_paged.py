@@ -1,0 +1,140 @@
+"""GPU: the attention pass over a paged KV cache (kvskip_attn_args.block_table: 64-token pages in a
+pool, a block table per sequence) against the same pass over the contiguous cache. Only the
+addresses differ, so outputs, log-sum-exps and block statistics must be bit-identical. The pools are
+built from the contiguous cache in a random page order, and every byte the pass must not read
+(unused pages, rows past a sequence's last token, pages of other sequences) holds NaN, so a wrong
+page or a read past the sequence shows up in the results."""
+
+import math
+
+import pytest
+import torch
+
+from kvskip_amd import ext as E
+from kvskip_amd import kvskip as K
+
+pytestmark = pytest.mark.gpu
+
+NAN = float("nan")
+
+
+def _cache(B, Hq, Hkv, D, T, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).cuda()
+    k[:, :, :64] += 0.3 * torch.randn(B, Hkv, 1, D, generator=g).to(torch.bfloat16).cuda()   # some structure
+    return q, k, v
+
+
+def _paginate(k, v, lens, seed, extra=5, width_pad=3):
+    """Pools [P, Hkv, 64, D] holding sequence b's tokens [0, lens[b]) in random pages, NaN elsewhere,
+    and the block table [B, ceil(max(lens) / 64) + width_pad] (-1 past each sequence)."""
+    B, Hkv, _, D = k.shape
+    nbs = [math.ceil(n / 64) for n in lens]
+    P = sum(nbs) + extra
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(seed)).tolist()
+    kp = torch.full((P, Hkv, 64, D), NAN, dtype=torch.bfloat16, device="cuda")
+    vp = torch.full((P, Hkv, 64, D), NAN, dtype=torch.bfloat16, device="cuda")
+    table = torch.full((B, max(nbs) + width_pad), -1, dtype=torch.int32)
+    i = 0
+    for b in range(B):
+        for j in range(nbs[b]):
+            pg = perm[i]
+            i += 1
+            rows = min(64, lens[b] - 64 * j)
+            kp[pg, :, :rows] = k[b, :, 64 * j:64 * j + rows]
+            vp[pg, :, :rows] = v[b, :, 64 * j:64 * j + rows]
+            table[b, j] = pg
+    return kp, vp, table.cuda()
+
+
+def _same(a, b, what):
+    assert a is not None and b is not None
+    assert torch.equal(a, b), (what, (a.float() - b.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("G,D", [(4, 128), (7, 128), (8, 64), (1, 64)])
+@pytest.mark.parametrize("T", [4096, 3001])
+def test_paged_dense_and_stats_match_contiguous(G, D, T):
+    Hkv = 2
+    q, k, v = _cache(2, Hkv * G, Hkv, D, T, seed=41 + G + T)
+    kp, vp, table = _paginate(k, v, [T, T], seed=T)
+    for S in (1, 8, 32):
+        for stats in (False, True):
+            ref = K.decode(q, k, v, D ** -0.5, stats=stats, num_splits=S)
+            got = K.decode(q, kp, vp, D ** -0.5, stats=stats, num_splits=S, block_table=table, T=T)
+            _same(got["out"], ref["out"], ("out", S, stats))
+            _same(got["lse"], ref["lse"], ("lse", S, stats))
+            if stats:
+                _same(got["blk_max"], ref["blk_max"], ("blk_max", S))
+                _same(got["blk_sum"], ref["blk_sum"], ("blk_sum", S))
+
+
+@pytest.mark.parametrize("G,D", [(4, 128), (7, 128)])
+def test_paged_masked_stats_match_contiguous(G, D):
+    Hkv, T = 3, 5000
+    q, k, v = _cache(2, Hkv * G, Hkv, D, T, seed=51 + G)
+    kp, vp, table = _paginate(k, v, [T, T], seed=7)
+    nb = math.ceil(T / 64)
+    g = torch.Generator().manual_seed(52)
+    keep = torch.rand(2, Hkv, nb, generator=g) < 0.35
+    keep[..., 0] = True
+    keep[0, 1] = False                                  # an empty list
+    keep[1, 2] = True                                   # a full list
+    plan = K.make_plan(keep.cuda())
+    for S in (4, 16):
+        ref = K.decode(q, k, v, D ** -0.5, plan=plan, stats=True, num_splits=S)
+        got = K.decode(q, kp, vp, D ** -0.5, plan=plan, stats=True, num_splits=S, block_table=table, T=T)
+        for key in ("out", "lse", "blk_max", "blk_sum"):
+            _same(got[key], ref[key], (key, S))
+
+
+def test_paged_ragged_batch_matches_contiguous():
+    """seq_lens with a paged cache: each sequence's table row covers only its own pages (-1 past)."""
+    G, D, Hkv, Tcap = 4, 128, 2, 6000
+    lens = [6000, 700, 64, 3333]
+    q, k, v = _cache(4, Hkv * G, Hkv, D, Tcap, seed=61)
+    kp, vp, table = _paginate(k, v, lens, seed=62)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    for stats in (False, True):
+        ref = K.decode(q, k, v, D ** -0.5, stats=stats, seq_lens=sl)
+        got = K.decode(q, kp, vp, D ** -0.5, stats=stats, seq_lens=sl, block_table=table, T=Tcap)
+        _same(got["out"], ref["out"], ("out", stats))
+        _same(got["lse"], ref["lse"], ("lse", stats))
+        if stats:
+            _same(got["blk_max"], ref["blk_max"], "blk_max")
+            _same(got["blk_sum"], ref["blk_sum"], "blk_sum")
+
+
+def test_paged_invalid_page_reads_as_empty_block():
+    """A page id outside [0, num_pages) makes its block empty: statistics (-inf, 0) there, and the
+    output equals the pass over a list without that block (within the split-order tolerance)."""
+    G, D, Hkv, T = 4, 128, 2, 2048
+    q, k, v = _cache(1, Hkv * G, Hkv, D, T, seed=71)
+    kp, vp, table = _paginate(k, v, [T], seed=72)
+    bad = 5
+    table[0, bad] = kp.shape[0] + 3
+    got = K.decode(q, kp, vp, D ** -0.5, stats=True, num_splits=8, block_table=table, T=T)
+    assert torch.isfinite(got["out"].float()).all()
+    assert torch.isinf(got["blk_max"][0, :, bad]).all() and (got["blk_max"][0, :, bad] < 0).all()
+    assert (got["blk_sum"][0, :, bad] == 0).all()
+    keep = torch.ones(1, Hkv, T // 64, dtype=torch.bool)
+    keep[..., bad] = False
+    ref = K.decode(q, k, v, D ** -0.5, plan=K.make_plan(keep.cuda()), stats=True, num_splits=8)
+    a, b = got["out"].float(), ref["out"].float()
+    assert ((a - b).norm() / b.norm()).item() <= 2e-3
+    torch.testing.assert_close(got["lse"], ref["lse"], rtol=0, atol=1e-5)
+
+
+def test_paged_rejections():
+    """Paths without paged support refuse a block table instead of reading wrong memory."""
+    G, D, Hkv, T = 4, 128, 1, 256
+    q, k, v = _cache(1, Hkv * G, Hkv, D, T, seed=81)
+    kp, vp, table = _paginate(k, v, [T], seed=82)
+    with pytest.raises(RuntimeError, match="paged cache"):
+        E.decode(q, kp, vp, 0.1, None, None, True, False, 1, 2, False, False, None, block_table=table, T=T)
+    with pytest.raises(RuntimeError, match="T .* is required"):
+        E.decode(q, kp, vp, 0.1, block_table=table)
+    with pytest.raises(RuntimeError, match="block_table"):
+        E.decode(q, kp, vp, 0.1, block_table=table[:, :2].contiguous(), T=T)
