@@ -176,6 +176,11 @@ typedef struct kvskip_plan_args {
   const int32_t* ids;
   int64_t ids_sb;
   uint8_t* idx_out;
+  /* Optional paged cache for the appended key row (not in the reference), as in kvskip_attn_args:
+   * k a page pool, k_sb its page stride; an invalid page leaves the key sums as they are. */
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int32_t num_pages;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
@@ -247,9 +252,12 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
 /* Per-block key sums of the first T tokens: csum[b, h, blk, :] = sum of k rows of the block
  * (fp32), blocks >= nb up to NBC zeroed. The device form of _centroid_sums
  * (src/kvskip_attn.py:170-179), used to initialise the planner state on the device. seq_lens: optional
- * [B] int32 device array (ragged batch: sequence b sums its first clamp(seq_lens[b], 1, T) rows). */
+ * [B] int32 device array (ragged batch: sequence b sums its first clamp(seq_lens[b], 1, T) rows).
+ * block_table, bt_stride, num_pages: optional paged cache, as in kvskip_attn_args (k a page pool,
+ * k_sb its page stride); a block on an invalid page sums to zero. */
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv,
-                      int32_t T, int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens, void* stream);
+                      int32_t T, int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens,
+                      const int32_t* block_table, int64_t bt_stride, int32_t num_pages, void* stream);
 
 /* Token index of a decode step: idx[b, blk] = 1 if block blk (of the first T tokens) holds an
  * earlier copy of ids[b, T-1] or the position right after one; blocks >= nb up to NBC are

@@ -48,6 +48,7 @@ class PlanArgs(ctypes.Structure):
         ("scale", c_float), ("delta", c_float),
         ("part", c_void_p), ("seq_lens", c_void_p), ("seq_lens_out", c_void_p),
         ("ids", c_void_p), ("ids_sb", c_int64), ("idx_out", c_void_p),
+        ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32),
     ]
 
 
@@ -80,7 +81,7 @@ SIGNATURES = {
     "kvskip_plan_scores": ([POINTER(PlanArgs), c_void_p], c_int),
     "kvskip_decode_splits_planned": ([POINTER(AttnArgs), POINTER(PlanArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
-                           c_int32, c_void_p, c_void_p], c_int),
+                           c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p], c_int),
     "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),
     "kvskip_last_error": ([], c_char_p),
     "kvskip_version": ([], c_char_p),

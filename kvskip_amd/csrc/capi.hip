@@ -248,6 +248,8 @@ static int check_plan(const kvskip_plan_args* p) {
   }
   if (p->aix != nullptr && p->idx == nullptr && p->ids == nullptr) return fail(KVSKIP_E_INVALID, "aix needs idx");
   if (p->calib_kind < 0 || p->calib_kind > 2) return fail(KVSKIP_E_INVALID, "calib_kind in {0, 1, 2}");
+  if (p->block_table != nullptr && (p->num_pages < 1 || p->bt_stride < nb))
+    return fail(KVSKIP_E_INVALID, "paged cache: num_pages >= 1 and block_table rows of ceil(T / 64) pages");
   return KVSKIP_OK;
 }
 
@@ -351,15 +353,18 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,
-                      int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens, void* stream) {
+                      int32_t D, float* csum, int32_t NBC, const int32_t* seq_lens, const int32_t* block_table,
+                      int64_t bt_stride, int32_t num_pages, void* stream) {
   if (k == nullptr || csum == nullptr) return fail(KVSKIP_E_INVALID, "block_sums: null tensor");
   if (B < 1 || Hkv < 1 || T < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
   if (D != 64 && D != 128) return fail(KVSKIP_E_UNSUPPORTED, "block_sums: D in {64, 128}");
   if ((T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK > NBC) return fail(KVSKIP_E_INVALID, "block capacity exceeded");
   if (k_st % 8 != 0 || k_sh % 8 != 0 || k_sb % 8 != 0 || !aligned16(k))
     return fail(KVSKIP_E_INVALID, "k strides must be multiples of 8 elements (16-byte rows)");
-  return launched(kvs::launch_block_sums(k, k_sb, k_sh, k_st, B, Hkv, T, D, csum, NBC, seq_lens,
-                                         static_cast<hipStream_t>(stream)),
+  if (block_table != nullptr && (num_pages < 1 || bt_stride < (T + KVSKIP_BLOCK - 1) / KVSKIP_BLOCK))
+    return fail(KVSKIP_E_INVALID, "paged cache: num_pages >= 1 and block_table rows of ceil(T / 64) pages");
+  return launched(kvs::launch_block_sums(k, k_sb, k_sh, k_st, B, Hkv, T, D, csum, NBC, seq_lens, block_table,
+                                         bt_stride, num_pages, static_cast<hipStream_t>(stream)),
                   "kvskip_block_sums");
 }
 

@@ -75,7 +75,8 @@ hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, cons
 // The plan's first launch alone (the scores pass; needs part).
 hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s);
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
-                             int D, float* csum, int NBC, const int32_t* seq_lens, hipStream_t s);
+                             int D, float* csum, int NBC, const int32_t* seq_lens, const int32_t* tbl, int64_t bt,
+                             int npages, hipStream_t s);
 hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,
                               const int32_t* seq_lens, hipStream_t s);
 

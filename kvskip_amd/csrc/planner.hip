@@ -116,10 +116,11 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   const bool add = p.add_token != 0;
   uint2 kx[DW];
   if (add) {
-    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
-                         static_cast<int64_t>(Tb - 1) * p.k_st;
+    const uint16_t* kr = key_row(reinterpret_cast<const uint16_t*>(p.k), p.k_sb, p.k_sh, p.k_st, b, h, Tb - 1,
+                                 p.block_table, p.bt_stride, p.num_pages);
 #pragma unroll
-    for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
+    for (int w = 0; w < DW; ++w)
+      kx[w] = kr != nullptr ? *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16) : make_uint2(0u, 0u);
   }
   const int gl = min(c16, G - 1);
   float em = NEG_INF, es = 0.f;
@@ -298,10 +299,11 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
         for (int j = 0; j < 4; ++j)
           qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
     }
-    const uint16_t* kr = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + h * p.k_sh +
-                         static_cast<int64_t>(Tb - 1) * p.k_st;
+    const uint16_t* kr = key_row(reinterpret_cast<const uint16_t*>(p.k), p.k_sb, p.k_sh, p.k_st, b, h, Tb - 1,
+                                 p.block_table, p.bt_stride, p.num_pages);
 #pragma unroll
-    for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16);
+    for (int w = 0; w < DW; ++w)
+      kx[w] = kr != nullptr ? *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16) : make_uint2(0u, 0u);
   }
   const bool add = p.add_token != 0 && !ixh;
 
@@ -500,18 +502,21 @@ __global__ void __launch_bounds__(fused_threads(G)) merge_update_kernel(const At
 template <int D>
 __global__ void __launch_bounds__(256) block_sums_kernel(const uint16_t* k, int64_t k_sb, int64_t k_sh,
                                                          int64_t k_st, int Hkv, int T, float* csum, int NBC,
-                                                         const int32_t* seq_lens) {
+                                                         const int32_t* seq_lens, const int32_t* tbl, int64_t bt,
+                                                         int npages) {
   constexpr int DL = D / 4, RG = 256 / DL, RPT = BLK / RG;
   const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, rg = tid / DL, c = tid % DL;
   const int Tb = seq_T(seq_lens, b, T);
-  const uint16_t* kb = k + b * k_sb + h * k_sh + 4 * c;
+  // the block's first row (its page's, with a block table; an invalid page sums to zero)
+  const uint16_t* kb = blk * BLK < Tb ? key_row(k, k_sb, k_sh, k_st, b, h, blk * BLK, tbl, bt, npages) : nullptr;
   __shared__ float part[RG][D];
   uint2 x[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
-    const int t = blk * BLK + rg + RG * i;
-    x[i] = t < Tb ? *reinterpret_cast<const uint2*>(kb + static_cast<int64_t>(t) * k_st) : make_uint2(0u, 0u);
+    const int r = rg + RG * i;
+    x[i] = (kb != nullptr && blk * BLK + r < Tb) ? *reinterpret_cast<const uint2*>(kb + 4 * c + static_cast<int64_t>(r) * k_st)
+                                               : make_uint2(0u, 0u);
   }
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
@@ -656,15 +661,16 @@ hipError_t launch_update(const kvskip_update_args& p, hipStream_t s) {
 }
 
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
-                             int D, float* csum, int NBC, const int32_t* seq_lens, hipStream_t s) {
+                             int D, float* csum, int NBC, const int32_t* seq_lens, const int32_t* tbl, int64_t bt,
+                             int npages, hipStream_t s) {
   const dim3 grid(NBC, Hkv, B);
   const uint16_t* kk = reinterpret_cast<const uint16_t*>(k);
   if (D == 128)
     hipLaunchKernelGGL((block_sums_kernel<128>), grid, dim3(256), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC,
-                       seq_lens);
+                       seq_lens, tbl, bt, npages);
   else if (D == 64)
     hipLaunchKernelGGL((block_sums_kernel<64>), grid, dim3(256), 0, s, kk, k_sb, k_sh, k_st, Hkv, T, csum, NBC,
-                       seq_lens);
+                       seq_lens, tbl, bt, npages);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -13,6 +13,17 @@ __device__ __forceinline__ int seq_T(const int32_t* seq_lens, int b, int T) {
   return seq_lens != nullptr ? min(max(seq_lens[b], 1), T) : T;
 }
 
+// Row t of KV head h of sequence b: in a view (k + b k_sb + h k_sh + t k_st) or, with a block table
+// (paged cache, k_sb the page stride), row t % 64 of page tbl[b bt + t / 64]; null for a page id
+// outside [0, npages).
+__device__ __forceinline__ const uint16_t* key_row(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int b,
+                                                   int h, int t, const int32_t* tbl, int64_t bt, int npages) {
+  if (tbl == nullptr) return k + b * k_sb + h * k_sh + static_cast<int64_t>(t) * k_st;
+  const int pg = tbl[static_cast<int64_t>(b) * bt + t / BLK];
+  if (pg < 0 || pg >= npages) return nullptr;
+  return k + static_cast<int64_t>(pg) * k_sb + h * k_sh + static_cast<int64_t>(t % BLK) * k_st;
+}
+
 __device__ __forceinline__ float clamped_logit(float x) {
   x = fminf(fmaxf(x, 1e-6f), 1.f - 1e-6f);
   return __logf(x) - __logf(1.f - x);

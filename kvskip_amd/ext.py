@@ -325,7 +325,7 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None):
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None):
     """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
 
     part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
@@ -335,10 +335,11 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     seq_lens_out (not in the reference): int32 [B] on the device; receives each sequence's length
     this step (for the step's update, which may run later).
     ids, idx_out (not in the reference; need part, and idx None): token ids int32 [B, >= T]; the
-    plan finds this step's token-index blocks itself and writes them to idx_out (uint8 [B, NBC])."""
+    plan finds this step's token-index blocks itself and writes them to idx_out (uint8 [B, NBC]).
+    block_table, T (not in the reference): k is the page pool of a paged cache (see _kv_dims)."""
     p = _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale,
                    delta, max_age, local, add_token, idx, calib, est, calib_on, calib_kind, aix, part, seq_lens,
-                   seq_lens_out, ids, idx_out)
+                   seq_lens_out, ids, idx_out, block_table, T)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
@@ -389,12 +390,15 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
 
 def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None):
-    """kvskip_plan_args of plan(), validated."""
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None):
+    """kvskip_plan_args of plan(), validated. block_table, T: a paged cache (see _kv_dims)."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    if block_table is None:
+        Hkv, T = k.shape[1], k.shape[2]
+    else:
+        _, _, _, Hkv, T = _kv_dims(q, k, k, block_table, T)
     for t, n in ((csum, "csum"), (lse_ref, "lse_ref"), (cs_ref, "cs_ref"), (lse_att, "lse_att"), (cs_now, "cs_now")):
         check_f32(t, n)
     NBC = keep.shape[2]
@@ -439,6 +443,8 @@ def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, t
         _require(part.numel() >= plan_part_floats(B, Hq, Hkv, NBC), "part: too small")
         p.part = part.data_ptr()
     p.seq_lens = _seq_lens_ptr(seq_lens, B)
+    if block_table is not None:
+        p.block_table, p.bt_stride, p.num_pages = block_table.data_ptr(), block_table.stride(0), k.shape[0]
     if seq_lens_out is not None:
         _require(seq_lens_out.is_cuda and seq_lens_out.dtype == torch.int32 and seq_lens_out.is_contiguous()
                  and seq_lens_out.numel() == B, "seq_lens_out: contiguous int32 [B] on the device")
@@ -525,14 +531,14 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
 
 
 def merge_update(q, k, v, scale, bufs: dict, num_splits, update_args: tuple, update_kwargs: dict,
-                 block_idx=None, block_cnt=None, seq_lens=None):
+                 block_idx=None, block_cnt=None, seq_lens=None, block_table=None, T=None):
     """The split merge of a decode_into(..., phase=1) pass (same q, k, v, bufs, list, num_splits >= 2)
     and update(*update_args, **update_kwargs), in one launch (kvskip_merge_update; not in the
-    reference)."""
+    reference). block_table, T: the pass's paged cache (see _kv_dims)."""
     B, Hq, D = q.shape
     _require(num_splits >= 2, "merge_update needs num_splits >= 2")
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], None, None, None,
-                     None, bufs["part_acc"], bufs["part_ml"], seq_lens)
+                     None, bufs["part_acc"], bufs["part_ml"], seq_lens, block_table, T)
     u = _update_args(*update_args, **update_kwargs)
     dev = q.device
     with torch.cuda.device(dev):
@@ -597,11 +603,20 @@ def _seq_lens_ptr(seq_lens, B):
     return seq_lens.data_ptr()
 
 
-def block_sums(k, NBC, out=None, seq_lens=None):
+def block_sums(k, NBC, out=None, seq_lens=None, block_table=None, T=None):
     """Per-block key sums [B, Hkv, NBC, D] fp32 of k [B, Hkv, T, D] (blocks >= nb are zero);
-    seq_lens: ragged batch (sequence b sums its first seq_lens[b] rows)."""
+    seq_lens: ragged batch (sequence b sums its first seq_lens[b] rows). block_table, T (not in the
+    reference): k is a page pool [num_pages, Hkv, 64, D] of a paged cache (see _kv_dims)."""
     check_kv(k, "k")
-    B, Hkv, T, D = k.shape
+    if block_table is None:
+        B, Hkv, T, D = k.shape
+        bt = (None, 0, 0)
+    else:
+        _require(T is not None and k.dim() == 4 and k.shape[2] == TILE, "paged cache: k [num_pages, Hkv, 64, D] and T")
+        _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
+                 and block_table.stride(1) == 1, "block_table: int32 [B, >= ceil(T / 64)] on the device, rows contiguous")
+        B, (Hkv, D), T = block_table.shape[0], (k.shape[1], k.shape[3]), int(T)
+        bt = (block_table.data_ptr(), block_table.stride(0), k.shape[0])
     _require((T + TILE - 1) // TILE <= NBC, "block capacity exceeded")
     if out is None:
         out = torch.empty(B, Hkv, NBC, D, dtype=torch.float32, device=k.device)
@@ -609,7 +624,7 @@ def block_sums(k, NBC, out=None, seq_lens=None):
     _require(tuple(out.shape) == (B, Hkv, NBC, D), "csum: [B, Hkv, NBC, D]")
     with torch.cuda.device(k.device):
         _native.check(_native.lib().kvskip_block_sums(k.data_ptr(), k.stride(0), k.stride(1), k.stride(2), B, Hkv, T, D,
-                                                      out.data_ptr(), NBC, _seq_lens_ptr(seq_lens, B),
+                                                      out.data_ptr(), NBC, _seq_lens_ptr(seq_lens, B), *bt,
                                                       _stream(k.device)))
     return out
 

@@ -122,6 +122,7 @@ class FusedPlanner:
         # step, the same decisions and lists as plan's own decision launch
         self.decide_in_pass = decide_in_pass
         self._pargs = None
+        self._pg = {}               # this step's paged cache (block_table, T), if any
         self.state = None
         self.t = 0
         self.T = 0
@@ -172,6 +173,7 @@ class FusedPlanner:
         self.NBC = NBC
 
     def _attend(self, q, k, v, scale, nb, seq_lens=None):
+        pg = self._pg
         """Split pass (masked + statistics) over the plan's lists into the planner's buffers.
         Returns out [B, Hq, D] (valid until the next step; written by _finish when the pass is
         split) and the [B, Hq, nb] statistics views."""
@@ -189,14 +191,15 @@ class FusedPlanner:
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
         self._S = S
-        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
+        # a paged cache: the pass alone (the carried-update and in-pass-decision kernels read views)
+        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None and not pg else None
         if self._pargs is not None:
             E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens)
         elif carried is not None:
             E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens)
         else:
             E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S,
-                          seq_lens=seq_lens, phase=1 if S > 1 else 3)
+                          seq_lens=seq_lens, phase=1 if S > 1 else 3, **pg)
         n = B * Hq * nb
         return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
 
@@ -208,14 +211,14 @@ class FusedPlanner:
         if self.carrier is not None:
             if self._S > 1:
                 E.decode_into(q, k, v, scale, self.bufs, s["block_idx"], s["block_cnt"], stats=True,
-                              num_splits=self._S, seq_lens=seq_lens, phase=2)
+                              num_splits=self._S, seq_lens=seq_lens, phase=2, **self._pg)
             G = q.shape[1] // k.shape[1]
             self.carrier.put(self, G, E.update_struct(*update_args, **update_kwargs),
                              (dict(s), self.bufs, update_args, update_kwargs))
             return
         if self._S > 1:
             E.merge_update(q, k, v, scale, self.bufs, self._S, update_args, update_kwargs, s["block_idx"],
-                           s["block_cnt"], seq_lens)
+                           s["block_cnt"], seq_lens, **self._pg)
         else:
             E.update(*update_args, **update_kwargs)
 
@@ -223,7 +226,7 @@ class FusedPlanner:
         """plan (scores + decision), or, with decide_in_pass and no ragged batch (seq_lens absent or
         one sequence), its scores pass alone: the decision then runs in the masked pass
         (kvskip_decode_splits_planned) and the update advances the age."""
-        if self.decide_in_pass and (seq_lens is None or q.shape[0] == 1):
+        if self.decide_in_pass and not self._pg and (seq_lens is None or q.shape[0] == 1):
             self._pargs = E.plan_struct(*plan_args, **plan_kwargs)
             E.plan_scores(self._pargs, q.device)
         else:
@@ -260,27 +263,31 @@ class FusedPlanner:
         return s["idx"]
 
     # -- steps
-    def first(self, q, k, v, scale, seq_lens=None):
+    def first(self, q, k, v, scale, seq_lens=None, block_table=None, T=None):
         """First decode step: dense + block statistics and the state initialisation
         (src/kvskip_attn.py:339-354), on the device: per-block key sums of the prefix, a plan that
         refreshes every head, the attention pass, and an update without calibration.
         seq_lens (int32 [B] on the device): a ragged batch; k, v are then views of a common
-        capacity and sequence b holds seq_lens[b] tokens (every later step appends one to each)."""
+        capacity and sequence b holds seq_lens[b] tokens (every later step appends one to each).
+        block_table, T (not in the reference): a paged cache, k, v page pools [num_pages, Hkv, 64, D]
+        and block_table int32 [B, >= ceil(T / 64)] on the device, T the tokens (the capacity with
+        seq_lens); its layer-steps run the pass alone (no carried update, no in-pass decision)."""
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape
-        Hkv, T = k.shape[1], k.shape[2]
+        self._pg = {} if block_table is None else dict(block_table=block_table, T=int(T))
+        Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
         nb = math.ceil(T / TILE)
         self.flush()
         self._alloc(q, k, nb + MARGIN)
         s = self.state
-        E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens)
+        E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens, **self._pg)
         every = torch.ones(Hkv, dtype=torch.int32, device=q.device)      # refresh all, no index heads
         pol = self.policy
         self._plan(q, (q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], every,
                        s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale), float(pol.delta),
                        int(pol.max_age), int(pol.local), False),
-                   dict(part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens)), seq_lens)
+                   dict(part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens), **self._pg), seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,
@@ -295,17 +302,19 @@ class FusedPlanner:
             self._count("blocks_total", total)
         return out
 
-    def step(self, q, k, v, scale, idx=None, ids=None, seq_lens=None):
+    def step(self, q, k, v, scale, idx=None, ids=None, seq_lens=None, block_table=None, T=None):
         """One later decode step (src/kvskip_attn.py:451-478): plan -> masked + stats attention ->
         update. idx: this step's token-index blocks (bool [B, >= nb], or a uint8 [B, NBC] device
         buffer used as is) or ids: token ids [B, >= T] int32 (index heads / auto index only).
-        seq_lens: the ragged batch's lengths after this step's token (one more per sequence)."""
+        seq_lens: the ragged batch's lengths after this step's token (one more per sequence).
+        block_table, T: a paged cache, as in first()."""
         if self.state is None:
             return self.first(q, k, v, scale, seq_lens)
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape
-        Hkv, T = k.shape[1], k.shape[2]
+        self._pg = {} if block_table is None else dict(block_table=block_table, T=int(T))
+        Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
         nb = math.ceil(T / TILE)
         self.flush()                                                  # this layer's last update
         if nb > self.NBC:
@@ -317,7 +326,7 @@ class FusedPlanner:
         else:
             add_token = T == self.T + 1
             if not add_token and T != self.T:
-                E.block_sums(k, self.NBC, out=s["csum"])              # several tokens appended: resum
+                E.block_sums(k, self.NBC, out=s["csum"], **self._pg)  # several tokens appended: resum
         self.t += 1
         self.T = T
         fuse_ix = pol.needs_index and ids is not None and idx is None     # the plan finds the index itself
@@ -334,7 +343,7 @@ class FusedPlanner:
                        s["calib"] if cal else None, s["est"], cal and self.t >= pol.calib_hold, kind,
                        s["aix"] if pol.calib_auto_ix is not None else None),
                    dict(part=s["part"], seq_lens=seq_lens, seq_lens_out=self._tlen(seq_lens),
-                        ids=ids if fuse_ix else None, idx_out=ix if fuse_ix else None), seq_lens)
+                        ids=ids if fuse_ix else None, idx_out=ix if fuse_ix else None, **self._pg), seq_lens)
         out, bmax, bsum = self._attend(q, k, v, scale, nb, seq_lens)
         self._finish(q, k, v, scale, seq_lens,
                      (bmax, bsum, s["trig"], s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T,

@@ -96,7 +96,7 @@ def test_planner_validation():
     assert lib.kvskip_plan(ctypes.byref(p), None) == -2
     u = UpdateArgs()
     assert lib.kvskip_update(ctypes.byref(u), None) == -1
-    assert lib.kvskip_block_sums(0, 0, 0, 0, 1, 1, 1, 128, 0, 1, None, None) == -1
+    assert lib.kvskip_block_sums(0, 0, 0, 0, 1, 1, 1, 128, 0, 1, None, None, 0, 0, None) == -1
     assert lib.kvskip_token_index(0x1000, 10, 1, 20, 0x2000, 1, None, None) == -1
 
 

@@ -138,3 +138,44 @@ def test_paged_rejections():
         E.decode(q, kp, vp, 0.1, block_table=table)
     with pytest.raises(RuntimeError, match="block_table"):
         E.decode(q, kp, vp, 0.1, block_table=table[:, :2].contiguous(), T=T)
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_paged_planner_loop_matches_contiguous(ragged):
+    """The device planner loop (key sums, plan with the appended key, masked pass, update) over a
+    paged cache gives the contiguous loop's outputs and state bit for bit."""
+    from kvskip_amd import workloads as W
+    from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+
+    G, D, Hkv, steps = 4, 128, 2, 8
+    lens0 = [2600, 900, 1700] if ragged else [2600]
+    B = len(lens0)
+    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=max(lens0), steps=steps, seed=91,
+                        ragged=lens0 if ragged else None)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    Tcap = k.shape[2]
+    qp = W.QueryProcess(run, 0, p_jump=0.2, revert=True)
+    qs = [qp.next().cuda() for _ in range(steps)]
+    ids = run.ids.to(torch.int32).cuda()
+    kp, vp, table = _paginate(k, v, [Tcap] * B, seed=92)        # every page of the capacity, random order
+    pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
+    ref, dut = FusedPlanner(pol(), count=False), FusedPlanner(pol(), count=False, carrier=UpdateCarrier())
+    for t in range(steps):
+        if ragged:
+            sl = torch.tensor([n + t + 1 for n in lens0], dtype=torch.int32, device="cuda")
+            kv, T = (k, v), Tcap
+        else:
+            sl, T = None, lens0[0] + t + 1
+            kv = (k[:, :, :T], v[:, :, :T])
+        if t == 0:
+            a = ref.first(qs[t], *kv, run.scale, seq_lens=sl)
+            b = dut.first(qs[t], kp, vp, run.scale, seq_lens=sl, block_table=table, T=T)
+        else:
+            a = ref.step(qs[t], *kv, run.scale, ids=ids, seq_lens=sl)
+            b = dut.step(qs[t], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
+        a, b = a.clone(), b.clone()
+        dut.flush()
+        assert torch.equal(a, b), t
+        for key in ("csum", "keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt",
+                    "calib", "est", "aix"):
+            assert torch.equal(ref.state[key], dut.state[key]), (t, key)
