@@ -106,10 +106,13 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
     for (int g = 0; g < G; ++g) {
       const uint16_t* qp = q + b * p.q_sb + (static_cast<int64_t>(h) * G + g) * p.q_sh;
 #pragma unroll
-      for (int w = 0; w < DW; ++w)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
+      for (int w = 0; w < DW; ++w) {  // 4 adjacent dims per 8-byte load
+        const uint2 t = *reinterpret_cast<const uint2*>(qp + 64 * w + 4 * c16);
+        qf[g][4 * w] = bf_lo(t.x) * p.scale;
+        qf[g][4 * w + 1] = bf_hi(t.x) * p.scale;
+        qf[g][4 * w + 2] = bf_lo(t.y) * p.scale;
+        qf[g][4 * w + 3] = bf_hi(t.y) * p.scale;
+      }
     }
   }
   // The key appended by this step (row T-1, block nb-1) joins its block's sum, in registers.
@@ -294,10 +297,13 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
     for (int g = 0; g < G; ++g) {
       const uint16_t* qp = q + b * p.q_sb + (static_cast<int64_t>(h) * G + g) * p.q_sh;
 #pragma unroll
-      for (int w = 0; w < DW; ++w)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          qf[g][4 * w + j] = __uint_as_float(static_cast<uint32_t>(qp[64 * w + 4 * c16 + j]) << 16) * p.scale;
+      for (int w = 0; w < DW; ++w) {  // 4 adjacent dims per 8-byte load
+        const uint2 t = *reinterpret_cast<const uint2*>(qp + 64 * w + 4 * c16);
+        qf[g][4 * w] = bf_lo(t.x) * p.scale;
+        qf[g][4 * w + 1] = bf_hi(t.x) * p.scale;
+        qf[g][4 * w + 2] = bf_lo(t.y) * p.scale;
+        qf[g][4 * w + 3] = bf_hi(t.y) * p.scale;
+      }
     }
     const uint16_t* kr = key_row(reinterpret_cast<const uint16_t*>(p.k), p.k_sb, p.k_sh, p.k_st, b, h, Tb - 1,
                                  p.block_table, p.bt_stride, p.num_pages);
