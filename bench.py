@@ -249,6 +249,19 @@ def main():
     del run_p
     res["vskip2_peaked"] = bench_two_pass(E, K, q_p, ks_p, vs_p, L.scale, S_dense, us_step, args, flush,
                                           "vskip2 peaked")
+    # single-pass V-skip on the same peaked layer (config 3's rule: tau 1e-4, local 2, the exact lse
+    # perturbed +-5% as lse_prev): the V blocks it skips, and its time against the dense pass
+    lp_p = W.perturbed_lse(K.decode(q_p, ks_p[0], vs_p[0], L.scale)["lse"], seed=45).contiguous()
+    cnt_p = E.vskip1(q_p, ks_p[0], vs_p[0], L.scale, 1e-4, 2, S_dense, False, True, lp_p)[3]
+    vfrac = float(cnt_p.sum()) / (Hkv * (T // 64))
+    t_v1 = events_region(lambda i: E.vskip1(q_p, ks_p[i], vs_p[i], L.scale, 1e-4, 2, S_dense, False, False, lp_p),
+                         args.steps // 2, args.warmup)
+    t_d1 = events_region(lambda i: E.decode(q_p, ks_p[i], vs_p[i], L.scale, None, None, False, True, S_dense, 2, False,
+                                            False), args.steps // 2, args.warmup)
+    res["vskip1_peaked"] = {"v_block_frac": vfrac, "us_per_op": t_v1, "dense_us_per_op": t_d1,
+                            "time_vs_dense": t_v1 / t_d1, "bytes_vs_dense": 0.5 + 0.5 * vfrac, "num_splits": S_dense}
+    log(f"vskip1 peaked: V read {vfrac:.3f}; {t_v1:.2f} us vs dense {t_d1:.2f} us (x{t_v1 / t_d1:.3f}; bytes "
+        f"x{0.5 + 0.5 * vfrac:.3f})")
     del ks_p, vs_p
 
     # ---- config 3: single-pass V-skip at T 65536 with a +-5% lse_prev
