@@ -125,7 +125,7 @@ def main():
     ap.add_argument("--no-planner", action="store_true", help="skip the config-4 planner loop")
     ap.add_argument("--planner-layers", type=int, default=32)
     ap.add_argument("--planner-steps", type=int, default=128)
-    ap.add_argument("--cfg5-steps", type=int, default=32, help="decode steps of the config-5 ragged loop")
+    ap.add_argument("--cfg5-steps", type=int, default=64, help="decode steps of the config-5 ragged loop (its 64)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant kernel's timed region (the rocprofv3 --stats target), then exit")
     ap.add_argument("--pmc-target", action="store_true",
