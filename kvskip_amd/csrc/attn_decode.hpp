@@ -68,7 +68,7 @@ template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG,
           bool PAGED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
   static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
-  static_assert(!PAGED || (MF && LOAD_V && !PLANNED), "a paged cache is read by the MFMA pass with V");
+  static_assert(!PAGED || (MF && LOAD_V), "a paged cache is read by the MFMA pass with V");
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
@@ -163,7 +163,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   if constexpr (PAGED) {
     const int* tbl = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
     for (int t = tid; t < n; t += NT) {
-      int blk = MASKED ? glist[i0 + t] : i0 + t;
+      int blk = MASKED ? list(i0 + t) : i0 + t;
       if (blk < 0 || blk >= nbb) blk = -1;
       int pg = blk >= 0 ? tbl[blk] : -1;
       if (pg < 0 || pg >= p.num_pages) pg = -1;

@@ -317,8 +317,6 @@ int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_a
   kvs::AttnP p;
   int rc = check_decode(a, 1, 1, a != nullptr && a->num_splits > 1 ? 1 : 3, &p);
   if (rc != KVSKIP_OK) return rc;
-  if (a->block_table != nullptr)
-    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_update: paged caches are not supported (update separately)");
   if ((rc = check_update(u)) != KVSKIP_OK) return rc;
   if (a->block_idx == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_update: the pass needs a block list");
   if (a->Hq / a->Hkv != u->Hq / u->Hkv)
@@ -331,8 +329,6 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
   int rc = check_plan(pl);
   if (rc != KVSKIP_OK) return rc;
   if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
-  if (a->block_table != nullptr)
-    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: paged caches are not supported (plan and decide first)");
   if (pl->part == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_planned needs the plan's part workspace");
   if (pl->seq_lens != a->seq_lens)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: the plan and the pass must share seq_lens");

@@ -359,7 +359,7 @@ def plan_scores(pargs: PlanArgs, device):
 
 
 def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None,
-                          seq_lens=None):
+                          seq_lens=None, block_table=None, T=None):
     """plan's decision and the masked + statistics split pass in one launch (kvskip_decode_splits_planned;
     after plan_scores(pargs)); the whole op when num_splits == 1. The layer's update must advance the
     age (update_struct(..., age=...)). update: another layer's update to carry, or None. seq_lens: the
@@ -368,7 +368,7 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
     check_kv(k, "k")
     check_kv(v, "v")
     B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    _, _, _, Hkv, T = _kv_dims(q, k, v, block_table, T)
     _require(1 <= num_splits <= 256, "num_splits in 1..256")
     nb = (T + TILE - 1) // TILE
     bmax, bsum = bufs["blk_max"], bufs["blk_sum"]
@@ -380,7 +380,7 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
         _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
                  "bufs: split partials")
     a = _decode_args(q, k, v, scale, None, None, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None, None,
-                     part_acc, part_ml, seq_lens)
+                     part_acc, part_ml, seq_lens, block_table, T)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(pargs),
@@ -559,15 +559,14 @@ def launch_update(update: UpdateArgs, device):
 
 
 def decode_splits_update(q, k, v, scale, bufs: dict, block_idx, block_cnt, num_splits, update: UpdateArgs,
-                         seq_lens=None):
+                         seq_lens=None, block_table=None, T=None):
     """decode_into(..., stats=True, phase=1) over a block list (the whole op when num_splits == 1)
     and the update of ANOTHER layer (an update_struct), in one launch (kvskip_decode_splits_update;
-    not in the reference). The update reads only its own layer's buffers."""
+    not in the reference). The update reads only its own layer's buffers. block_table, T: a paged cache."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
     _require(1 <= num_splits <= 256, "num_splits in 1..256")
     nb = (T + TILE - 1) // TILE
     bmax, bsum = bufs["blk_max"], bufs["blk_sum"]
@@ -579,7 +578,7 @@ def decode_splits_update(q, k, v, scale, bufs: dict, block_idx, block_cnt, num_s
         _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
                  "bufs: split partials")
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None,
-                     None, part_acc, part_ml, seq_lens)
+                     None, part_acc, part_ml, seq_lens, block_table, T)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode_splits_update(ctypes.byref(a), ctypes.byref(update), _stream(dev)))

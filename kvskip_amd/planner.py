@@ -191,12 +191,11 @@ class FusedPlanner:
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
         self._S = S
-        # a paged cache: the pass alone (the carried-update and in-pass-decision kernels read views)
-        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None and not pg else None
+        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         if self._pargs is not None:
-            E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens)
+            E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens, **pg)
         elif carried is not None:
-            E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens)
+            E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens, **pg)
         else:
             E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S,
                           seq_lens=seq_lens, phase=1 if S > 1 else 3, **pg)
@@ -226,7 +225,7 @@ class FusedPlanner:
         """plan (scores + decision), or, with decide_in_pass and no ragged batch (seq_lens absent or
         one sequence), its scores pass alone: the decision then runs in the masked pass
         (kvskip_decode_splits_planned) and the update advances the age."""
-        if self.decide_in_pass and not self._pg and (seq_lens is None or q.shape[0] == 1):
+        if self.decide_in_pass and (seq_lens is None or q.shape[0] == 1):
             self._pargs = E.plan_struct(*plan_args, **plan_kwargs)
             E.plan_scores(self._pargs, q.device)
         else:
@@ -271,7 +270,7 @@ class FusedPlanner:
         capacity and sequence b holds seq_lens[b] tokens (every later step appends one to each).
         block_table, T (not in the reference): a paged cache, k, v page pools [num_pages, Hkv, 64, D]
         and block_table int32 [B, >= ceil(T / 64)] on the device, T the tokens (the capacity with
-        seq_lens); its layer-steps run the pass alone (no carried update, no in-pass decision)."""
+        seq_lens)."""
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape

@@ -142,40 +142,47 @@ def test_paged_rejections():
 
 @pytest.mark.parametrize("ragged", [False, True])
 def test_paged_planner_loop_matches_contiguous(ragged):
-    """The device planner loop (key sums, plan with the appended key, masked pass, update) over a
-    paged cache gives the contiguous loop's outputs and state bit for bit."""
+    """The device planner loop (key sums, plan with the appended key, the pass with the decision in it
+    or not, updates carried by the other layer's pass) over paged caches gives the contiguous loop's
+    outputs and state bit for bit; two layers share the carrier."""
     from kvskip_amd import workloads as W
     from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
 
-    G, D, Hkv, steps = 4, 128, 2, 8
+    G, D, Hkv, steps, layers = 4, 128, 2, 8, 2
     lens0 = [2600, 900, 1700] if ragged else [2600]
     B = len(lens0)
-    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=max(lens0), steps=steps, seed=91,
+    run = W.planner_run(layers=layers, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=max(lens0), steps=steps, seed=91,
                         ragged=lens0 if ragged else None)
-    k, v = run.k[0].cuda(), run.v[0].cuda()
-    Tcap = k.shape[2]
-    qp = W.QueryProcess(run, 0, p_jump=0.2, revert=True)
-    qs = [qp.next().cuda() for _ in range(steps)]
+    ks = [k.cuda() for k in run.k]
+    vs = [v.cuda() for v in run.v]
+    Tcap = ks[0].shape[2]
+    qps = [W.QueryProcess(run, l, p_jump=0.2, revert=True) for l in range(layers)]
+    qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
     ids = run.ids.to(torch.int32).cuda()
-    kp, vp, table = _paginate(k, v, [Tcap] * B, seed=92)        # every page of the capacity, random order
+    pools = [_paginate(ks[l], vs[l], [Tcap] * B, seed=92 + l) for l in range(layers)]   # random page order
     pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
-    ref, dut = FusedPlanner(pol(), count=False), FusedPlanner(pol(), count=False, carrier=UpdateCarrier())
+    cr = UpdateCarrier()
+    ref = [FusedPlanner(pol(), count=False) for _ in range(layers)]
+    dut = [FusedPlanner(pol(), count=False, carrier=cr) for _ in range(layers)]
+    keys = ("csum", "keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt", "calib", "est",
+            "aix")
     for t in range(steps):
         if ragged:
             sl = torch.tensor([n + t + 1 for n in lens0], dtype=torch.int32, device="cuda")
-            kv, T = (k, v), Tcap
+            T = Tcap
         else:
             sl, T = None, lens0[0] + t + 1
-            kv = (k[:, :, :T], v[:, :, :T])
-        if t == 0:
-            a = ref.first(qs[t], *kv, run.scale, seq_lens=sl)
-            b = dut.first(qs[t], kp, vp, run.scale, seq_lens=sl, block_table=table, T=T)
-        else:
-            a = ref.step(qs[t], *kv, run.scale, ids=ids, seq_lens=sl)
-            b = dut.step(qs[t], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
-        a, b = a.clone(), b.clone()
-        dut.flush()
-        assert torch.equal(a, b), t
-        for key in ("csum", "keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt",
-                    "calib", "est", "aix"):
-            assert torch.equal(ref.state[key], dut.state[key]), (t, key)
+        for l in range(layers):
+            kv = (ks[l], vs[l]) if ragged else (ks[l][:, :, :T], vs[l][:, :, :T])
+            kp, vp, table = pools[l]
+            if t == 0:
+                a = ref[l].first(qs[t][l], *kv, run.scale, seq_lens=sl)
+                b = dut[l].first(qs[t][l], kp, vp, run.scale, seq_lens=sl, block_table=table, T=T)
+            else:
+                a = ref[l].step(qs[t][l], *kv, run.scale, ids=ids, seq_lens=sl)
+                b = dut[l].step(qs[t][l], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
+            assert torch.equal(a.clone(), b.clone()), (t, l)
+        cr.flush()
+        for l in range(layers):
+            for key in keys:
+                assert torch.equal(ref[l].state[key], dut[l].state[key]), (t, l, key)
