@@ -86,8 +86,9 @@ typedef struct kvskip_attn_args {
    * part_acc / part_ml of [B, Hq, num_splits, ...]. */
   const int32_t* seq_lens;
 
-  /* Paged cache (not in the reference; the split pass of kvskip_decode / kvskip_decode_splits, with
-   * V, MFMA engine): k and v point to page pools of 64-token pages; token t of sequence b, KV head h
+  /* Paged cache (not in the reference; every pass that reads K or V: kvskip_decode and its split
+   * entry points, kvskip_pv, kvskip_vskip1; MFMA engine; at most 4096 blocks per split): k and v
+   * point to page pools of 64-token pages; token t of sequence b, KV head h
    * is row t % 64 of page block_table[b * bt_stride + t / 64], at k + page * k_sb + h * k_sh +
    * (t % 64) * k_st (k_sb, v_sb: the page stride). T is the sequences' length (or capacity with
    * seq_lens); bt_stride >= ceil(T / 64). A page id outside [0, num_pages) makes its block empty

@@ -155,6 +155,38 @@ __device__ __forceinline__ uint32_t head_bytes(int T, int64_t st, int D) {
   return static_cast<uint32_t>((static_cast<int64_t>(T - 1) * st + D) * 2);
 }
 
+// ---- Paged cache: block blk of a sequence's KV head h is page pg of a pool (page stride psb
+// elements, head stride sh, row stride st). The resource's base is placed 64 blk rows before the
+// page, so the block's loads use the offsets of a view (token t0 = 64 blk); its range ends at the
+// block's last token below Tb (rows past it read zero) and is empty for an empty block (blk or pg
+// < 0). No offset below the page is ever formed.
+__device__ __forceinline__ rsrc_t block_rsrc(const uint16_t* pool, int64_t psb, int64_t sh, int64_t st, int h,
+                                             int blk, int pg, int Tb, int D) {
+  if (blk < 0 || pg < 0) return make_rsrc(pool, 0u);
+  return make_rsrc(pool + static_cast<int64_t>(pg) * psb + static_cast<int64_t>(h) * sh -
+                       static_cast<int64_t>(blk) * BLK * st,
+                   head_bytes(min(Tb, blk * BLK + BLK), st, D));
+}
+
+// The pages of a workgroup's items t < n (block blk_of(t)) of sequence b into LDS sPg (and the
+// blocks into sBk, if given): -1 for blocks outside [0, nb) and page ids outside [0, num_pages).
+// One pass of the workgroup's threads, then a barrier; the streaming loops read these without a
+// vector-memory wait.
+template <class BlockOf>
+__device__ __forceinline__ void gather_pages(const AttnP& p, int b, int n, int nb, BlockOf blk_of, int* sPg,
+                                             int* sBk) {
+  const int* tbl = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    int blk = blk_of(t);
+    if (blk < 0 || blk >= nb) blk = -1;
+    int pg = blk >= 0 ? tbl[blk] : -1;
+    if (pg < 0 || pg >= p.num_pages) pg = -1;
+    sPg[t] = pg;
+    if (sBk != nullptr) sBk[t] = blk;
+  }
+  __syncthreads();
+}
+
 // K block at token t0: lane (r8, sub) gets rows t0 + 8 rg + r8, 16-byte chunks sub (+8).
 // koff = r8 * k_st * 2 + 16 * sub (per lane, fixed).
 template <int D>

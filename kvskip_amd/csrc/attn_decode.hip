@@ -5,24 +5,17 @@
 namespace kvs {
 namespace {
 
-template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PAGED = false>
+template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG>
 __global__ void __launch_bounds__(NT, 2) decode_kernel(const AttnP p) {
-  decode_body<D, G, MASKED, STATS, LOAD_V, MF, RAG, false, PAGED>(p, blockIdx.x);
+  decode_body<D, G, MASKED, STATS, LOAD_V, MF, RAG>(p, blockIdx.x);
 }
 
 template <int D, int G, bool M, bool ST, bool LV>
 hipError_t launch_decode_t(const AttnP& p, bool mf, int phase, hipStream_t s) {
   if (phase & 1) {
-    if (p.block_table != nullptr) {  // paged cache: MFMA pass with V (checked by the caller)
-      if constexpr (LV) {
-        if (p.seq_lens != nullptr)
-          hipLaunchKernelGGL((decode_kernel<D, G, M, ST, true, true, true, true>), attn_grid(p), dim3(NT), 0, s, p);
-        else
-          hipLaunchKernelGGL((decode_kernel<D, G, M, ST, true, true, false, true>), attn_grid(p), dim3(NT), 0, s, p);
-      } else {
-        return hipErrorInvalidValue;
-      }
-    } else if (p.seq_lens != nullptr)  // ragged batches: MFMA engine only
+    if (p.block_table != nullptr)  // paged cache: MFMA engine (checked by the caller), own translation unit
+      return launch_decode_paged(p, D, G, M, ST, LV, phase, s);
+    if (p.seq_lens != nullptr)  // ragged batches: MFMA engine only
       hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true, true>), attn_grid(p), dim3(NT), 0, s, p);
     else if (mf)
       hipLaunchKernelGGL((decode_kernel<D, G, M, ST, LV, true, false>), attn_grid(p), dim3(NT), 0, s, p);

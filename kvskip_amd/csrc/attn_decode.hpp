@@ -68,7 +68,7 @@ template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG,
           bool PAGED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
   static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
-  static_assert(!PAGED || (MF && LOAD_V), "a paged cache is read by the MFMA pass with V");
+  static_assert(!PAGED || MF, "a paged cache is read by the MFMA engine");
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
@@ -160,18 +160,17 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   // Blocks outside the sequence and page ids outside [0, num_pages) become -1 (an empty block).
   __shared__ int sPg[PAGED ? MAX_NB : 1];
   __shared__ int sBk[PAGED && MASKED ? MAX_NB : 1];
-  if constexpr (PAGED) {
-    const int* tbl = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-    for (int t = tid; t < n; t += NT) {
-      int blk = MASKED ? list(i0 + t) : i0 + t;
-      if (blk < 0 || blk >= nbb) blk = -1;
-      int pg = blk >= 0 ? tbl[blk] : -1;
-      if (pg < 0 || pg >= p.num_pages) pg = -1;
-      sPg[t] = pg;
-      if constexpr (MASKED) sBk[t] = blk;
-    }
-    __syncthreads();
-  }
+  if constexpr (PAGED)
+    gather_pages(p, b, n, nbb, [&](int t) { return MASKED ? list(i0 + t) : i0 + t; }, sPg, MASKED ? sBk : nullptr);
+  // paged: item k of this wavefront (LDS slot wave + NWAVE k): its block and page
+  auto paged_item = [&](int k, int& blk, int& pg) {
+    const int t = wave + NWAVE * k;
+    pg = __builtin_amdgcn_readfirstlane(sPg[t]);
+    if constexpr (MASKED)
+      blk = __builtin_amdgcn_readfirstlane(sBk[t]);
+    else
+      blk = i0 + t;
+  };
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;  // this wavefront's items
   int gap_prev = -1, gap_cur = 0;  // masked stats: the list entries around this lane's gap
   if constexpr (MASKED && STATS) {
@@ -283,7 +282,34 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
 #pragma unroll
       for (int g = 0; g < G; ++g) alpha[g] = lane_value(ar[g % 4], 16 * (g / 4));
     };
-    if (nw > 0 && !LOAD_V) {
+    if (nw > 0 && !LOAD_V && PAGED) {
+      // K only over a paged cache: two blocks in flight as below, each through its page's resource
+      u32x4 ka[4][KS], kb[4][KS];
+      int b0, g0, b1 = -1, g1 = -1;
+      paged_item(0, b0, g0);
+      load_k_block_mf<D>(ka, block_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, h, b0, g0, Tb, D), koffm, p.k_st,
+                         max(b0, 0) * BLK);
+      auto step = [&](u32x4 (&ld)[4][KS], int& bld, int& gld, const u32x4 (&ac)[4][KS], int bac, int gac, int k) {
+        if (k + 1 < nw) {
+          paged_item(k + 1, bld, gld);
+        } else {
+          bld = -1;
+          gld = -1;
+        }
+        load_k_block_mf<D>(ld, block_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, h, bld, gld, Tb, D), koffm, p.k_st,
+                           max(bld, 0) * BLK);
+        __builtin_amdgcn_sched_barrier(0);
+        if (k < nw) {
+          float alpha[G];
+          process(bac, (bac >= 0 && gac >= 0) ? Tb : 0, ac, alpha);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      for (int k = 0; k < nw; k += 2) {
+        step(kb, b1, g1, ka, b0, g0, k);
+        step(ka, b0, g0, kb, b1, g1, k + 1);
+      }
+    } else if (nw > 0 && !LOAD_V) {
       // K only: two blocks in flight while one is scored (the V registers are free). Step k loads
       // item k + 1 and scores item k; past the last item the load reads beyond the head's buffer
       // range (zeros, no memory access), so every step issues the same loads.
@@ -309,35 +335,22 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
         step(ka, b0, kb, b1, k + 1);
       }
     } else if (nw > 0 && PAGED) {
-      // item k: LDS slot wave + NWAVE k; each block's K / V resource spans its page's rows of this
-      // head that hold tokens (zeros beyond), an empty block's spans nothing
+      // each block's K / V resource spans its page's rows of this head that hold tokens (zeros
+      // beyond), an empty block's spans nothing; both are built before the block ahead is scored
+      // (built after it, the compiler spilled the freshly loaded K block)
       u32x4 kr[4][KS];
       u32x4 vr[Lay<D>::VN];
-      auto item = [&](int k, int& blk, int& pg) {
-        const int t = wave + NWAVE * k;
-        pg = __builtin_amdgcn_readfirstlane(sPg[t]);
-        if constexpr (MASKED)
-          blk = __builtin_amdgcn_readfirstlane(sBk[t]);
-        else
-          blk = i0 + t;
-      };
-      // the resource's base is placed blk * 64 rows before the page, so the block's loads use the
-      // same offsets (token t0 = 64 blk) as in a contiguous cache; its range ends at the block's last
-      // token, and no offset below the page is ever formed
       auto page_rsrc = [&](const uint16_t* pool, int64_t psb, int64_t sh, int64_t st, int blk, int pg) {
-        if (blk < 0 || pg < 0) return make_rsrc(pool, 0u);
-        return make_rsrc(pool + static_cast<int64_t>(pg) * psb + static_cast<int64_t>(h) * sh -
-                             static_cast<int64_t>(blk) * BLK * st,
-                         head_bytes(min(Tb, blk * BLK + BLK), st, D));
+        return block_rsrc(pool, psb, sh, st, h, blk, pg, Tb, D);
       };
       auto lim_of = [&](int blk, int pg) { return (blk >= 0 && pg >= 0) ? Tb : 0; };
       int blk, pg;
-      item(0, blk, pg);
+      paged_item(0, blk, pg);
       load_k_block_mf<D>(kr, page_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, blk, pg), koffm, p.k_st, max(blk, 0) * BLK);
       load_v_block<D>(vr, page_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, blk, pg), voff, p.v_st, max(blk, 0) * BLK);
       for (int k = 0; k + 1 < nw; ++k) {
         int blk_n, pg_n;
-        item(k + 1, blk_n, pg_n);
+        paged_item(k + 1, blk_n, pg_n);
         const rsrc_t rk_n = page_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, blk_n, pg_n);
         const rsrc_t rv_n = page_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, blk_n, pg_n);
         float alpha[G];

@@ -1,6 +1,7 @@
 // Single-pass V-skip (both QK engines), two-pass V-skip pass 2, and the streaming read
 // ceiling; see attn_common.hpp for the shared decomposition and layouts.
 #include "attn_common.hpp"
+#include "planner_common.hpp"
 
 namespace kvs {
 namespace {
@@ -9,9 +10,13 @@ namespace {
 // group's vote -> only then the V loads of that block; the next block's K loads are issued
 // right after, so V(i) overlaps QK(i+1)'s loads. The softmax update and P of a block are
 // computed as if the block were kept and committed only if the group keeps it.
-template <int D, int G, bool MF>
+// PAGED (MFMA engine only): K / V in pages of a pool through p.block_table; an invalid page reads as
+// an empty block.
+template <int D, int G, bool MF, bool PAGED = false>
 __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
+  static_assert(!PAGED || MF, "a paged cache is read by the MFMA engine");
   constexpr int GP = gpad<G>();
+  __shared__ int sPg[PAGED ? MAX_NB : 1];
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
   __shared__ float sLse0[G];
@@ -55,20 +60,32 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
     u32x4 qa[KS];
     load_q_mf<D, G>(qa, p, b, h, lane);
     u32x4 kr[4][KS];
+    // paged: block blk's K / V resource (item t's page from LDS) and its token limit (0: empty)
+    auto page_at = [&](int t) { return PAGED ? __builtin_amdgcn_readfirstlane(sPg[t]) : 0; };
+    auto krs = [&](int blk, int pg) { return PAGED ? block_rsrc(p.k, p.k_sb, p.k_sh, p.k_st, h, blk, pg, p.T, D) : rk; };
+    auto vrs = [&](int blk, int pg) { return PAGED ? block_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, h, blk, pg, p.T, D) : rv; };
+    auto lim_of = [&](int pg) { return pg >= 0 ? p.T : 0; };
+    if constexpr (PAGED) gather_pages(p, b, n, nb, [&](int t) { return i0 + t; }, sPg, nullptr);
     // normaliser estimate (log2 units) per head: lse_prev, or the block-0 log-sum-exp
     if (p.lse_prev != nullptr) {
       if (tid < G) sLse0[tid] = p.lse_prev[hq0 + tid] * LOG2E;
     } else if (wave == 0) {
-      load_k_block_mf<D>(kr, rk, koffm, p.k_st, 0);
+      int pg0 = 0;
+      if constexpr (PAGED) {
+        pg0 = __builtin_amdgcn_readfirstlane(p.block_table[static_cast<int64_t>(b) * p.bt_stride]);
+        if (pg0 < 0 || pg0 >= p.num_pages) pg0 = -1;
+      }
+      load_k_block_mf<D>(kr, krs(0, pg0), koffm, p.k_st, 0);
       float s[4][4];
-      qk_block_mf<D>(s, kr, qa, p.scale_log2, 0, p.T, lane);
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, 0, lim_of(pg0), lane);
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const float mt = row16_max(fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i])));
+        const float mtu = mt == NEG_INF ? 0.f : mt;  // an empty block 0 (paged): -inf, every block kept
         float sum = 0.f;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) sum += fexp2(s[nt][i] - mt);
-        const float lse0 = mt + flog2(row16_sum(sum));
+        for (int nt = 0; nt < 4; ++nt) sum += fexp2(s[nt][i] - mtu);
+        const float lse0 = mtu + flog2(row16_sum(sum));
         const int g = 4 * j4 + i;
         if (c16 == 0 && g < G) sLse0[g] = lse0;
       }
@@ -82,13 +99,18 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
       mr[i] = NEG_INF;
       lr[i] = 0.f;
     }
-    if (nw > 0) load_k_block_mf<D>(kr, rk, koffm, p.k_st, (i0 + wave) * BLK);
+    int pg = nw > 0 ? page_at(wave) : -1;
+    if (nw > 0) load_k_block_mf<D>(kr, krs(i0 + wave, pg), koffm, p.k_st, (i0 + wave) * BLK);
     for (int k = 0; k < nw; ++k) {
       const int blk = i0 + wave + NWAVE * k;
       const int t0 = blk * BLK;
       const bool more = k + 1 < nw;
+      // this block's V and the next block's K resources, built before the scores
+      const int pg_n = more ? page_at(wave + NWAVE * (k + 1)) : -1;
+      const rsrc_t rv_c = vrs(blk, pg), rk_n = krs(blk + NWAVE, pg_n);
       float s[4][4];
-      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, p.T, lane);
+      qk_block_mf<D>(s, kr, qa, p.scale_log2, t0, lim_of(pg), lane);
+      pg = pg_n;
       float tm[4], tl[4], ta[4], pv4[4][4];
       bool vote = false;
 #pragma unroll
@@ -133,12 +155,12 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
           for (int u = 0; u < 8; ++u) acc[g][u] *= a;
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_v_block<D>(vr, rv, voff, p.v_st, t0);
-        if (more) load_k_block_mf<D>(kr, rk, koffm, p.k_st, (blk + NWAVE) * BLK);
+        load_v_block<D>(vr, rv_c, voff, p.v_st, t0);
+        if (more) load_k_block_mf<D>(kr, rk_n, koffm, p.k_st, (blk + NWAVE) * BLK);
         __builtin_amdgcn_sched_barrier(0);
         pv();
       } else if (more) {
-        load_k_block_mf<D>(kr, rk, koffm, p.k_st, (blk + NWAVE) * BLK);
+        load_k_block_mf<D>(kr, rk_n, koffm, p.k_st, (blk + NWAVE) * BLK);
       }
     }
 #pragma unroll
@@ -244,9 +266,12 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
 
 // Two-pass V-skip, pass 2: acc = sum over listed blocks of (blk_scale * P) . V; the weights
 // are normalised already, so no softmax and the splits simply add up.
-template <int D, int G>
+// PAGED: V in pages of a pool through p.block_table; the listed blocks' pages are gathered into LDS.
+template <int D, int G, bool PAGED = false>
 __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
   constexpr int GP = gpad<G>();
+  __shared__ int sPg[PAGED ? MAX_NB : 1];
+  __shared__ int sBk[PAGED ? MAX_NB : 1];
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
 
@@ -292,9 +317,12 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
   // unconditional: out-of-range entries load block 0; past the last item (blk == PAST) V reads
   // beyond the head's buffer range (zeros, no memory access) and P / scale of block 0
   constexpr int PAST = -2;
-  auto load = [&](Item& it, int blk) {
+  auto load = [&](Item& it, int blk, int pgv = -1) {
     const int t0 = max(blk, 0) * BLK;
-    load_v_block<D>(it.vr, rv, voff, p.v_st, blk == PAST ? p.nb * BLK : t0);
+    if constexpr (PAGED)  // an empty block (blk < 0 or no page) reads zeros
+      load_v_block<D>(it.vr, block_rsrc(p.v, p.v_sb, p.v_sh, p.v_st, h, blk, pgv, p.T, D), voff, p.v_st, t0);
+    else
+      load_v_block<D>(it.vr, rv, voff, p.v_st, blk == PAST ? p.nb * BLK : t0);
     const int g = pg < G ? pg : 0;
     it.f = p.blk_scale[((static_cast<int64_t>(b) * p.Hkv + h) * p.nb + max(blk, 0)) * G + g];
     it.raw = ld16(p.p_in + (hq0 + g) * p.t_pad + t0 + 8 * ppart);
@@ -314,7 +342,35 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
     pv_block<D, G>(acc, it.vr, sPw, lane);
     __builtin_amdgcn_wave_barrier();
   };
-  if (nw > 0) {
+  if constexpr (PAGED) gather_pages(p, b, n, p.nb, [&](int t) { return list[i0 + t]; }, sPg, sBk);
+  if (PAGED && nw > 0) {
+    // the same ring over the LDS copy of this split's entries and their pages
+    Item I0, I1;
+    auto item = [&](int k, int& blk, int& pgv) {
+      if (k < nw) {
+        const int t = wave + NWAVE * k;
+        blk = __builtin_amdgcn_readfirstlane(sBk[t]);
+        pgv = __builtin_amdgcn_readfirstlane(sPg[t]);
+      } else {
+        blk = PAST;
+        pgv = -1;
+      }
+    };
+    int b0, g0, b1 = PAST, g1 = -1;
+    item(0, b0, g0);
+    load(I0, b0, g0);
+    auto step = [&](Item& ld, int& bld, int& gld, const Item& ac, int bac, int k) {
+      item(k + 1, bld, gld);
+      load(ld, bld, gld);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k < nw) accumulate(ac, bac);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int k = 0; k < nw; k += 2) {
+      step(I1, b1, g1, I0, b0, k);
+      step(I0, b0, g0, I1, b1, k + 1);
+    }
+  } else if (nw > 0) {
     Item I0, I1, I2;
     int ea = entry_of(R - 1), eb = entry_of(R);
     int b0 = block_of(entry_of(0)), b1 = R > 2 && nw > 1 ? block_of(entry_of(1)) : PAST, b2 = PAST;
@@ -372,7 +428,9 @@ __global__ void __launch_bounds__(256) read_kernel(const u32x4* __restrict__ x, 
 
 template <int D, int G>
 hipError_t launch_vskip1_t(const AttnP& p, bool mf, hipStream_t s) {
-  if (mf)
+  if (p.block_table != nullptr)  // paged: MFMA engine (checked by the caller)
+    hipLaunchKernelGGL((vskip1_kernel<D, G, true, true>), attn_grid(p), dim3(NT), 0, s, p);
+  else if (mf)
     hipLaunchKernelGGL((vskip1_kernel<D, G, true>), attn_grid(p), dim3(NT), 0, s, p);
   else
     hipLaunchKernelGGL((vskip1_kernel<D, G, false>), attn_grid(p), dim3(NT), 0, s, p);
@@ -384,7 +442,10 @@ hipError_t launch_vskip1_t(const AttnP& p, bool mf, hipStream_t s) {
 
 template <int D, int G>
 hipError_t launch_pv_t(const AttnP& p, hipStream_t s) {
-  hipLaunchKernelGGL((pv_kernel<D, G>), attn_grid(p), dim3(NT), 0, s, p);
+  if (p.block_table != nullptr)
+    hipLaunchKernelGGL((pv_kernel<D, G, true>), attn_grid(p), dim3(NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((pv_kernel<D, G>), attn_grid(p), dim3(NT), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.num_splits > 1) e = launch_combine(p, D, true, s);

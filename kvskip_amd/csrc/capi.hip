@@ -121,6 +121,20 @@ int kvskip_struct_size(int which) {
 }
 
 // Checks of a decode launch (phase: 3 the op, 1 its split pass, 2 its merge) into *p.
+// A paged cache (block_table set): the MFMA engine, a table row per sequence of >= nb pages, and at
+// most MAX_NB items per workgroup (their pages are gathered into LDS); `items` per (b, head).
+static int check_paged(const kvskip_attn_args* a, int nb, int64_t items) {
+  if (!kvs::qk_use_mfma()) return fail(KVSKIP_E_UNSUPPORTED, "paged cache: MFMA engine only");
+  if (a->num_pages < 1) return fail(KVSKIP_E_INVALID, "paged cache: num_pages >= 1");
+  if (a->bt_stride < nb) return fail(KVSKIP_E_INVALID, "paged cache: block_table rows must hold ceil(T / 64) pages");
+  const int64_t per = a->seq_lens != nullptr ? (a->B * items + a->num_splits - 1) / a->num_splits
+                                             : (items + a->num_splits - 1) / a->num_splits;
+  if (per > kvs::planner_max_blocks(1))
+    return fail(KVSKIP_E_UNSUPPORTED, "paged cache: at most %d blocks per split (raise num_splits)",
+                kvs::planner_max_blocks(1));
+  return KVSKIP_OK;
+}
+
 static int check_decode(const kvskip_attn_args* a, int stats, int load_v, int phase, kvs::AttnP* p) {
   int rc = prepare_attn(a, true, true, load_v != 0, p);
   if (rc != KVSKIP_OK) return rc;
@@ -143,18 +157,8 @@ static int check_decode(const kvskip_attn_args* a, int stats, int load_v, int ph
     if (a->p_out != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: no fp16 P output");
   }
   if (a->block_table != nullptr && (phase & 1)) {  // paged cache (the merge alone reads no K / V)
-    if (!load_v || a->p_out != nullptr)
-      return fail(KVSKIP_E_UNSUPPORTED, "paged cache: the pass with V only (no stats-only pass, no fp16 P)");
-    if (!kvs::qk_use_mfma()) return fail(KVSKIP_E_UNSUPPORTED, "paged cache: MFMA engine only");
-    if (a->num_pages < 1) return fail(KVSKIP_E_INVALID, "paged cache: num_pages >= 1");
-    if (a->bt_stride < p->nb) return fail(KVSKIP_E_INVALID, "paged cache: block_table rows must hold ceil(T / 64) pages");
-    // the pages of one workgroup's items are gathered into LDS: at most MAX_NB of them
-    const int64_t items = masked ? a->max_blocks : p->nb;
-    const int64_t per = a->seq_lens != nullptr ? (a->B * items + a->num_splits - 1) / a->num_splits
-                                               : (items + a->num_splits - 1) / a->num_splits;
-    if (per > kvs::planner_max_blocks(1))
-      return fail(KVSKIP_E_UNSUPPORTED, "paged cache: at most %d blocks per split (raise num_splits)",
-                  kvs::planner_max_blocks(1));
+    const int rc = check_paged(a, p->nb, masked ? a->max_blocks : p->nb);
+    if (rc != KVSKIP_OK) return rc;
   }
   if (!load_v) p->out = nullptr;
   return KVSKIP_OK;
@@ -187,7 +191,10 @@ int kvskip_pv(const kvskip_attn_args* a, void* stream) {
   int rc = prepare_attn(a, false, false, true, &p);
   if (rc != KVSKIP_OK) return rc;
   if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "pv: seq_lens is not supported");
-  if (a->block_table != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "pv: paged caches are not supported");
+  if (a->block_table != nullptr) {
+    rc = check_paged(a, p.nb, a->max_blocks);
+    if (rc != KVSKIP_OK) return rc;
+  }
   if (a->p_in == nullptr) return fail(KVSKIP_E_INVALID, "P: fp16 [B, Hq, t_pad]");
   if (!aligned16(a->p_in)) return fail(KVSKIP_E_INVALID, "P must be 16-byte aligned");
   if (a->blk_scale == nullptr) return fail(KVSKIP_E_INVALID, "blk_scale: contiguous fp32 [B, Hkv, nb, G]");
@@ -205,7 +212,10 @@ int kvskip_vskip1(const kvskip_attn_args* a, void* stream) {
   int rc = prepare_attn(a, true, true, true, &p);
   if (rc != KVSKIP_OK) return rc;
   if (a->seq_lens != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "vskip1: seq_lens is not supported");
-  if (a->block_table != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "vskip1: paged caches are not supported");
+  if (a->block_table != nullptr) {
+    rc = check_paged(a, p.nb, p.nb);
+    if (rc != KVSKIP_OK) return rc;
+  }
   if (!(a->tau > 0.f) || a->local < 0) return fail(KVSKIP_E_INVALID, "tau > 0, local >= 0, num_splits >= 1");
   if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
   if (a->num_splits > 1 && a->part_acc == nullptr)

@@ -58,6 +58,9 @@ bool attn_supported(int D, int G);
 // launch_decode phase: bit 0 the split pass, bit 1 the split merge (3: both, as one op).
 hipError_t launch_decode(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, int phase,
                          hipStream_t s);
+// launch_decode over a paged cache (p.block_table set; the MFMA engine), same phases.
+hipError_t launch_decode_paged(const AttnP& p, int D, int G, bool masked, bool stats, bool load_v, int phase,
+                               hipStream_t s);
 hipError_t launch_vskip1(const AttnP& p, int D, int G, hipStream_t s);
 hipError_t launch_pv(const AttnP& p, int D, int G, hipStream_t s);
 hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, hipStream_t s);

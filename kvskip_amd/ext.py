@@ -86,16 +86,25 @@ def _kv_dims(q, k, v, block_table=None, T=None):
     Hkv = k.shape[1]
     if block_table is None:
         return B, Hq, D, Hkv, k.shape[2]
+    return B, Hq, D, Hkv, _pool_tokens((k, v), B, Hkv, D, block_table, T)
+
+
+def _pool_tokens(pools, B, Hkv, D, block_table, T) -> int:
+    """T of a paged call, after checking the page pools [num_pages, Hkv, 64, D] and the table."""
     _require(T is not None and int(T) >= 1, "paged cache: T (tokens per sequence, or the capacity) is required")
     T = int(T)
-    _require(k.dim() == 4 and v.dim() == 4 and k.shape[2] == TILE and v.shape[2] == TILE and v.shape[0] == k.shape[0]
-             and v.shape[1] == Hkv and k.shape[3] == D and v.shape[3] == D,
-             "paged cache: k, v must be page pools [num_pages, Hkv, 64, D]")
+    _require(all(x.dim() == 4 and tuple(x.shape[1:]) == (Hkv, TILE, D) and x.shape[0] == pools[0].shape[0]
+                 for x in pools), "paged cache: k, v must be page pools [num_pages, Hkv, 64, D]")
     _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2
              and block_table.shape[0] == B and block_table.stride(1) == 1
              and block_table.shape[1] >= (T + TILE - 1) // TILE,
              "block_table: int32 [B, >= ceil(T / 64)] on the device, rows contiguous")
-    return B, Hq, D, Hkv, T
+    return T
+
+
+def _set_pages(a, block_table, pool):
+    if block_table is not None:          # page pools: the dim-0 strides of k / v are the page strides
+        a.block_table, a.bt_stride, a.num_pages = block_table.data_ptr(), block_table.stride(0), pool.shape[0]
 
 
 def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
@@ -218,8 +227,7 @@ def _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bma
                  part_ml, seq_lens=None, block_table=None, T=None) -> AttnArgs:
     B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
-    if block_table is not None:          # page pools: k_sb / v_sb (their dim-0 strides) are the page strides
-        a.block_table, a.bt_stride, a.num_pages = block_table.data_ptr(), block_table.stride(0), k.shape[0]
+    _set_pages(a, block_table, k)
     if seq_lens is not None:
         _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
                  and seq_lens.numel() == B, "seq_lens: contiguous CUDA int32 [B]")
@@ -253,13 +261,16 @@ def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_spli
                                                               _stream(dev)))
 
 
-def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
-    """Two-pass V-skip, pass 2 (kernels/kvskip_ext.cpp:106-146). Returns [out bf16, out_f32 or None]."""
+def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False, block_table=None, T=None):
+    """Two-pass V-skip, pass 2 (kernels/kvskip_ext.cpp:106-146). Returns [out bf16, out_f32 or None].
+    block_table, T (not in the reference): v is the page pool of a paged cache (see _kv_dims)."""
     check_kv(v, "v")
     _require(P.is_cuda and P.dtype == torch.float16 and P.dim() == 3 and P.is_contiguous(), "P: fp16 [B, Hq, t_pad]")
     _require(blk_scale.is_cuda and blk_scale.dtype == torch.float32 and blk_scale.dim() == 4
              and blk_scale.is_contiguous(), "blk_scale: contiguous fp32 [B, Hkv, nb, G]")
-    B, Hkv, T, D = v.shape
+    B, Hkv, T, D = v.shape if block_table is None else (P.shape[0], v.shape[1], T, v.shape[3])
+    if block_table is not None:
+        T = _pool_tokens((v,), B, Hkv, D, block_table, T)
     Hq = P.shape[1]
     _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
     G = Hq // Hkv
@@ -283,21 +294,24 @@ def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False):
     a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
     a.out, a.out_f32 = out.data_ptr(), _ptr(out32)
     a.p_in, a.blk_scale = P.data_ptr(), blk_scale.data_ptr()
+    _set_pages(a, block_table, v)
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_pv(ctypes.byref(a), _stream(dev)))
     return [out, out32]
 
 
-def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=False, lse_prev=None):
-    """Single-pass V-skip (kernels/kvskip_ext.cpp:149-195). Returns [out, lse, out_f32 or None, vcount or None]."""
+def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=False, lse_prev=None,
+           block_table=None, T=None):
+    """Single-pass V-skip (kernels/kvskip_ext.cpp:149-195). Returns [out, lse, out_f32 or None, vcount or None].
+    block_table, T (not in the reference): a paged cache (see _kv_dims; the MFMA engine)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
     _require(tau > 0.0 and local >= 0 and num_splits >= 1, "tau > 0, local >= 0, num_splits >= 1")
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
-    _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
-             and v.shape[2] == T, "shape mismatch between q, k, v")
+    B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
+    if block_table is None:
+        _require(k.shape[0] == B and v.shape[0] == B and k.shape[3] == D and v.shape[3] == D and v.shape[1] == Hkv
+                 and v.shape[2] == T, "shape mismatch between q, k, v")
     _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
     dev = q.device
     f32 = dict(dtype=torch.float32, device=dev)
@@ -318,6 +332,7 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
         _require(lse_prev.is_cuda and lse_prev.dtype == torch.float32 and lse_prev.is_contiguous()
                  and lse_prev.numel() == B * Hq, "lse_prev: contiguous fp32 [B, Hq]")
         a.lse_prev = lse_prev.data_ptr()
+    _set_pages(a, block_table, k)
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_vskip1(ctypes.byref(a), _stream(dev)))
     return [out, lse, out32, vcount]

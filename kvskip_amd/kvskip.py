@@ -147,23 +147,29 @@ def select_blocks(logw: torch.Tensor, G: int, rule: str, value: float, local: in
     return keep | always_keep(nb, local, logw.device)
 
 
-def pv(P, v, blk_scale, plan: Plan, num_splits: int | None = None, out_f32: bool = False):
-    B, Hkv = v.shape[0], v.shape[1]
+def pv(P, v, blk_scale, plan: Plan, num_splits: int | None = None, out_f32: bool = False,
+       block_table: torch.Tensor | None = None, T: int | None = None):
+    """Two-pass V-skip pass 2 (kernels/kvskip.py:150-154); block_table, T: v is a page pool."""
+    B, Hkv = P.shape[0], v.shape[1]
     if num_splits is None:
         num_splits = num_splits_for(B * Hkv, plan.max_cnt)
-    return ext().pv(P, v, blk_scale, plan.block_idx, plan.block_cnt, int(num_splits), out_f32)
+    paged = {} if block_table is None else dict(block_table=block_table, T=T)
+    return ext().pv(P, v, blk_scale, plan.block_idx, plan.block_cnt, int(num_splits), out_f32, **paged)
 
 
 def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.99, local: int = 2,
-                   sync: bool = True, out_f32: bool = False) -> dict:
+                   sync: bool = True, out_f32: bool = False, block_table: torch.Tensor | None = None,
+                   T: int | None = None) -> dict:
     """Two-pass V-skip (kernels/kvskip.py:157-179): pass 1 reads all of K once and writes block stats
-    and P (fp16); the GQA-union selection picks blocks; pass 2 reads P and V of the kept blocks only."""
+    and P (fp16); the GQA-union selection picks blocks; pass 2 reads P and V of the kept blocks only.
+    block_table, T (not in the reference): k, v are page pools of a paged cache."""
     if q.dim() == 4:
         q = q.squeeze(2)
     B, Hq, D = q.shape
     Hkv = k.shape[1]
     G = Hq // Hkv
-    r1 = decode(q, k, v, scale, stats=True, load_v=False, write_p=True)
+    paged = {} if block_table is None else dict(block_table=block_table, T=T)
+    r1 = decode(q, k, v, scale, stats=True, load_v=False, write_p=True, **paged)
     logw = r1["blk_max"] + torch.log(r1["blk_sum"])                    # [B, Hq, nb]
     keep = select_blocks(logw, G, rule, value, local)                   # [B, Hkv, nb]
     keep_h = keep.repeat_interleave(G, dim=1)                           # [B, Hq, nb]
@@ -171,7 +177,7 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
     scale_b = torch.exp(r1["blk_max"] - lse_kept).masked_fill(~keep_h, 0.0)
     scale_b = scale_b.view(B, Hkv, G, -1).transpose(2, 3).contiguous()  # [B, Hkv, nb, G]
     plan = make_plan(keep, sync=sync)
-    out, o32 = pv(r1["p"], v, scale_b, plan, out_f32=out_f32)
+    out, o32 = pv(r1["p"], v, scale_b, plan, out_f32=out_f32, **paged)
     d = {"out": out, "keep": keep, "kept_frac": keep.float().mean().item() if sync else None}
     if out_f32:
         d["out_f32"] = o32
@@ -180,19 +186,21 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
 
 def vskip_one_pass(q, k, v, scale: float, tau: float = 1e-4, local: int = 2, num_splits: int | None = None,
                    out_f32: bool = False, count: bool = False, lse_prev: torch.Tensor | None = None,
-                   sync: bool = True) -> dict:
+                   sync: bool = True, block_table: torch.Tensor | None = None, T: int | None = None) -> dict:
     """Single-pass V-skip (kernels/kvskip.py:182-208): K read once, V of a block read only if some
     head of the group has estimated weight >= tau there (normaliser: lse_prev, else the sink
-    block's log-sum-exp, a lower bound). With count=True "v_tiles" [B, Hkv] counts V blocks read."""
+    block's log-sum-exp, a lower bound). With count=True "v_tiles" [B, Hkv] counts V blocks read.
+    block_table, T (not in the reference): k, v are page pools of a paged cache."""
     if q.dim() == 4:
         q = q.squeeze(2)
     B, Hq, D = q.shape
-    Hkv, T = k.shape[1], k.shape[2]
+    Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
+    paged = {} if block_table is None else dict(block_table=block_table, T=T)
     nb = math.ceil(T / TILE)
     if num_splits is None:
         num_splits = num_splits_for(B * Hkv, nb)
     out, lse, o32, cnt = ext().vskip1(q, k, v, float(scale), float(tau), int(local), int(num_splits),
-                                      out_f32, count, lse_prev)
+                                      out_f32, count, lse_prev, **paged)
     d = {"out": out, "lse": lse, "num_splits": num_splits}
     if out_f32:
         d["out_f32"] = o32

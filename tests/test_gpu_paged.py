@@ -1,5 +1,5 @@
-"""GPU: the attention pass over a paged KV cache (kvskip_attn_args.block_table: 64-token pages in a
-pool, a block table per sequence) against the same pass over the contiguous cache. Only the
+"""GPU: the attention passes over a paged KV cache (kvskip_attn_args.block_table: 64-token pages in a
+pool, a block table per sequence) against the same passes over the contiguous cache. Only the
 addresses differ, so outputs, log-sum-exps and block statistics must be bit-identical. The pools are
 built from the contiguous cache in a random page order, and every byte the pass must not read
 (unused pages, rows past a sequence's last token, pages of other sequences) holds NaN, so a wrong
@@ -127,13 +127,78 @@ def test_paged_invalid_page_reads_as_empty_block():
     torch.testing.assert_close(got["lse"], ref["lse"], rtol=0, atol=1e-5)
 
 
+@pytest.mark.parametrize("G,D", [(4, 128), (8, 64), (7, 128)])
+def test_paged_stats_only_pass_matches_contiguous(G, D):
+    """The K-only pass (statistics, fp16 P, no V) over pages: lse, statistics and P bit-identical."""
+    Hkv, T = 2, 4000
+    q, k, v = _cache(2, Hkv * G, Hkv, D, T, seed=101 + G)
+    kp, vp, table = _paginate(k, v, [T, T], seed=102)
+    nb = math.ceil(T / 64)
+    keep = torch.rand(2, Hkv, nb, generator=torch.Generator().manual_seed(103)) < 0.4
+    for plan in (None, K.make_plan(keep.cuda())):
+        for S in (1, 16):
+            ref = K.decode(q, k, v, D ** -0.5, plan=plan, stats=True, load_v=False, write_p=True, num_splits=S)
+            got = K.decode(q, kp, vp, D ** -0.5, plan=plan, stats=True, load_v=False, write_p=True, num_splits=S,
+                           block_table=table, T=T)
+            assert got["out"] is None
+            for key in ("lse", "blk_max", "blk_sum"):
+                _same(got[key], ref[key], (key, S, plan is None))
+            # P of a skipped block is left unwritten (an uninitialised buffer, as in the reference)
+            listed = torch.ones_like(keep) if plan is None else keep
+            tok = listed.cuda().repeat_interleave(G, 1).repeat_interleave(64, 2)
+            _same(got["p"][tok], ref["p"][tok], ("p", S, plan is None))
+
+
+@pytest.mark.parametrize("G,D", [(4, 128), (8, 64)])
+@pytest.mark.parametrize("T", [4096, 2501])
+def test_paged_vskip_two_pass_matches_contiguous(G, D, T):
+    """Two-pass V-skip over pages (K-only pass with P, selection, pass 2 over the kept blocks' V pages)
+    gives the contiguous selection and output bit for bit."""
+    Hkv = 2
+    q, k, v = _cache(2, Hkv * G, Hkv, D, T, seed=111 + T)
+    kp, vp, table = _paginate(k, v, [T, T], seed=112)
+    # random scores give blocks of nearly equal weight: a small top-p mass, or tau just above the mean
+    # weight, leaves blocks out of the group union
+    for rule, value in (("topp", 0.3), ("tau", 1.2 / math.ceil(T / 64))):
+        ref = K.vskip_two_pass(q, k, v, D ** -0.5, rule=rule, value=value)
+        got = K.vskip_two_pass(q, kp, vp, D ** -0.5, rule=rule, value=value, block_table=table, T=T)
+        assert torch.equal(got["keep"], ref["keep"]), rule
+        assert 0 < ref["kept_frac"] < 1, (rule, ref["kept_frac"])
+        _same(got["out"], ref["out"], ("out", rule))
+
+
+@pytest.mark.parametrize("G,D", [(4, 128), (8, 64), (1, 64)])
+@pytest.mark.parametrize("T", [4096, 3001])
+def test_paged_vskip_one_pass_matches_contiguous(G, D, T):
+    """Single-pass V-skip over pages: output, log-sum-exp and V blocks read bit-identical, with the
+    block-0 estimate and with lse_prev."""
+    Hkv = 2
+    q, k, v = _cache(2, Hkv * G, Hkv, D, T, seed=121 + G)
+    kp, vp, table = _paginate(k, v, [T, T], seed=122)
+    lse_prev = K.decode(q, k, v, D ** -0.5)["lse"]
+    nb = math.ceil(T / 64)
+    for S in (1, 8):
+        # random scores give blocks of nearly equal weight: tau just above the mean weight skips some
+        for lp, tau in ((None, 1.2), (lse_prev, 1.2 / nb)):
+            ref = K.vskip_one_pass(q, k, v, D ** -0.5, tau=tau, num_splits=S, count=True, lse_prev=lp)
+            got = K.vskip_one_pass(q, kp, vp, D ** -0.5, tau=tau, num_splits=S, count=True, lse_prev=lp,
+                                   block_table=table, T=T)
+            for key in ("out", "lse", "v_tiles"):
+                _same(got[key], ref[key], (key, S, lp is None))
+            assert ref["v_tiles"].sum().item() < 2 * Hkv * nb, (S, lp is None)      # some V blocks skipped
+
+
 def test_paged_rejections():
-    """Paths without paged support refuse a block table instead of reading wrong memory."""
+    """Calls a paged cache cannot serve are refused instead of reading wrong memory."""
     G, D, Hkv, T = 4, 128, 1, 256
     q, k, v = _cache(1, Hkv * G, Hkv, D, T, seed=81)
     kp, vp, table = _paginate(k, v, [T], seed=82)
-    with pytest.raises(RuntimeError, match="paged cache"):
-        E.decode(q, kp, vp, 0.1, None, None, True, False, 1, 2, False, False, None, block_table=table, T=T)
+    big = 4097 * 64                                          # one split would gather > 4096 pages
+    wide = torch.full((1, 4097), -1, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="blocks per split"):
+        E.decode(q, kp, vp, 0.1, num_splits=1, block_table=wide, T=big)
+    with pytest.raises(RuntimeError, match="blocks per split"):
+        E.vskip1(q, kp, vp, 0.1, 1e-3, num_splits=1, block_table=wide, T=big)
     with pytest.raises(RuntimeError, match="T .* is required"):
         E.decode(q, kp, vp, 0.1, block_table=table)
     with pytest.raises(RuntimeError, match="block_table"):
