@@ -236,6 +236,20 @@ def main():
                                num_splits=S_mask)
     log(f"dense: {us_step:.2f} us/step, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of peak); "
         f"masked: {us_m:.2f} us/step (x{us_m / us_step:.3f} of dense)")
+    # the dense op over a paged cache: each copy's K / V as 64-token pages of a pool in a random
+    # order, with a block table; the same bytes as the dense op, timed the same way
+    table, kps, vps = W.paged_pools(ks, vs, seed=21)
+
+    def dense_paged(i):
+        return E.decode(q, kps[i], vps[i], L.scale, None, None, False, True, S_dense, 2, False, False,
+                        block_table=table, T=T)
+
+    elp = timed_steps(dense_paged, args.steps, args.warmup)
+    us_p = elp / args.steps * 1e6
+    res["dense_paged"] = {"us_per_step": us_p, "GBs": bytes_dense * args.steps / elp / 1e9,
+                          "time_vs_dense": us_p / us_step, "pages": int(kps[0].shape[0]), "num_splits": S_dense}
+    log(f"dense over pages: {us_p:.2f} us/step (x{us_p / us_step:.3f} of contiguous)")
+    del kps, vps, table
     t_read = read_same_bytes()
 
     # ---- two-pass V-skip (kernels/kvskip.py:157-179) on config 2's layer (flat N(0, 1) keys: top-p

@@ -140,6 +140,27 @@ def cfg3(device="cpu", seed=3, T=65536) -> Layer:
     return structured(1, 32, 8, 128, T, seed, sink="newest", device=device)
 
 
+def paged_pools(ks, vs, seed, extra=16):
+    """Paged copies of K / V views [B, Hkv, T, D]: one block table [B, ceil(T / 64)] int32 (a random
+    page order, shared by the copies) and, per copy, pools [B ceil(T / 64) + extra, Hkv, 64, D] whose
+    page table[b, j] holds tokens 64 j .. 64 j + 63 of sequence b (zeros past T and in unused pages)."""
+    B, Hkv, T, D = ks[0].shape
+    nb = (T + 63) // 64
+    P = B * nb + extra
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(seed))[: B * nb]
+    table = perm.view(B, nb).to(torch.int32).to(ks[0].device)
+    idx = perm.to(ks[0].device)
+
+    def pool(x):
+        y = torch.zeros(P, Hkv, 64, D, dtype=x.dtype, device=x.device)
+        full = torch.zeros(B, Hkv, nb * 64, D, dtype=x.dtype, device=x.device)
+        full[:, :, :T] = x
+        y[idx] = full.view(B, Hkv, nb, 64, D).permute(0, 2, 1, 3, 4).reshape(B * nb, Hkv, 64, D)
+        return y
+
+    return table, [pool(k) for k in ks], [pool(v) for v in vs]
+
+
 def perturbed_lse(lse_exact: torch.Tensor, seed: int, rel: float = 0.05) -> torch.Tensor:
     """lse_prev = lse_exact + log(1 + u), u ~ U[-rel, rel] per query head (the normaliser off by +-5%)."""
     g = _gen("cpu", seed)
