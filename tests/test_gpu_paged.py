@@ -97,14 +97,15 @@ def test_paged_ragged_batch_matches_contiguous():
     q, k, v = _cache(4, Hkv * G, Hkv, D, Tcap, seed=61)
     kp, vp, table = _paginate(k, v, lens, seed=62)
     sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
-    for stats in (False, True):
-        ref = K.decode(q, k, v, D ** -0.5, stats=stats, seq_lens=sl)
-        got = K.decode(q, kp, vp, D ** -0.5, stats=stats, seq_lens=sl, block_table=table, T=Tcap)
-        _same(got["out"], ref["out"], ("out", stats))
-        _same(got["lse"], ref["lse"], ("lse", stats))
+    for stats, load_v in ((False, True), (True, True), (True, False)):      # the last: the K-only pass
+        ref = K.decode(q, k, v, D ** -0.5, stats=stats, load_v=load_v, seq_lens=sl)
+        got = K.decode(q, kp, vp, D ** -0.5, stats=stats, load_v=load_v, seq_lens=sl, block_table=table, T=Tcap)
+        if load_v:
+            _same(got["out"], ref["out"], ("out", stats))
+        _same(got["lse"], ref["lse"], ("lse", stats, load_v))
         if stats:
-            _same(got["blk_max"], ref["blk_max"], "blk_max")
-            _same(got["blk_sum"], ref["blk_sum"], "blk_sum")
+            _same(got["blk_max"], ref["blk_max"], ("blk_max", load_v))
+            _same(got["blk_sum"], ref["blk_sum"], ("blk_sum", load_v))
 
 
 def test_paged_invalid_page_reads_as_empty_block():
