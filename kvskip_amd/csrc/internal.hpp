@@ -71,9 +71,15 @@ hipError_t launch_update(const kvskip_update_args& p, hipStream_t s);
 hipError_t launch_merge_update(const AttnP& a, const kvskip_update_args& p, int D, hipStream_t s);
 // The masked + statistics split pass of a (phase 1) and the update u of another layer, one launch.
 hipError_t launch_split_update(const AttnP& a, const kvskip_update_args& u, int D, hipStream_t s);
+// launch_split_update's fused form over a paged cache (its own translation unit).
+hipError_t launch_split_update_paged(const AttnP& a, const kvskip_update_args& u, int D, hipStream_t s);
 // The plan's decision + the masked statistics split pass of a (phase 1) in one launch, with an
 // optional carried update u of another layer.
 hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
+                                hipStream_t s);
+// launch_planned_split over a paged cache, after any unfused carried update (its own translation
+// unit).
+hipError_t launch_planned_paged(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
                                 hipStream_t s);
 // The plan's first launch alone (the scores pass; needs part).
 hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s);

@@ -1,54 +1,8 @@
-// The planner's masked statistics pass with the plan's decision inside: every workgroup's
-// prologue merges the scores pass's partials of its (b, KV head), decides as plan_decide does and
-// takes its slice of the block list from the chunk masks (decode_body PLANNED), so a layer-step is
-// scores -> this pass -> merge, one launch fewer; the first workgroups may carry the update of
-// another layer (as kvskip_decode_splits_update).
-#include "attn_decode.hpp"
+// The planned pass over a contiguous cache; the kernels are in planned.hpp, the paged-cache ones
+// in planned_paged.hip.
+#include "planned.hpp"
 
 namespace kvs {
-namespace {
-
-// The planned pass: the decision of plan_decide made in every workgroup's prologue (decode_body
-// PLANNED), optionally with a carried update (R > 0) in the first workgroups.
-template <int D, int G, int R, bool PAGED>
-__global__ void __launch_bounds__(NT, 2) planned_split_kernel(const AttnP a, const kvskip_plan_args pa,
-                                                              const kvskip_update_args u) {
-  const int n_update = R > 0 ? u.B * u.Hkv : 0;
-  const int i = blockIdx.x;
-  if constexpr (R > 0) {
-    if (i < n_update) {
-      update_body<G, R, carry_waves(G)>(u, i % u.Hkv, i / u.Hkv);
-      return;
-    }
-  }
-  decode_body<D, G, true, true, true, true, false, true, PAGED>(a, i - n_update, &pa);
-}
-
-// The pass's grid is num_splits x Hkv x B workgroups whether or not seq_lens is given (B is 1 then):
-// the list of a (b, KV head) is cut into num_splits slices as in the unragged pass.
-template <int D, int G, bool PAGED>
-hipError_t launch_planned_p(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, hipStream_t s) {
-  const dim3 blk(NT);
-  const int n_pass = a.num_splits * a.Hkv * a.B;
-  if (u == nullptr) {
-    hipLaunchKernelGGL((planned_split_kernel<D, G, 0, PAGED>), dim3(n_pass), blk, 0, s, a, pa, kvskip_update_args{});
-    return hipGetLastError();
-  }
-  const int nb = (u->T + BLK - 1) / BLK;
-  const dim3 grid(n_pass + u->B * u->Hkv);
-  if (nb <= 2 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 2, PAGED>), grid, blk, 0, s, a, pa, *u);
-  else if (nb <= 4 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 4, PAGED>), grid, blk, 0, s, a, pa, *u);
-  else if (nb <= 8 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 8, PAGED>), grid, blk, 0, s, a, pa, *u);
-  else hipLaunchKernelGGL((planned_split_kernel<D, G, CARRY_MAX_R, PAGED>), grid, blk, 0, s, a, pa, *u);
-  return hipGetLastError();
-}
-
-template <int D, int G>
-hipError_t launch_planned_t(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, hipStream_t s) {
-  return a.block_table != nullptr ? launch_planned_p<D, G, true>(a, pa, u, s) : launch_planned_p<D, G, false>(a, pa, u, s);
-}
-
-}  // namespace
 
 hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
                                 hipStream_t s) {
@@ -58,8 +12,9 @@ hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, cons
     if (e != hipSuccess) return e;
     u = nullptr;
   }
+  if (a.block_table != nullptr) return launch_planned_paged(a, pa, u, D, s);
 #define KVS_CASE(DD, GG) \
-  if (D == DD && G == GG) return launch_planned_t<DD, GG>(a, pa, u, s);
+  if (D == DD && G == GG) return launch_planned_p<DD, GG, false>(a, pa, u, s);
   KVS_FOR_G(KVS_CASE, 64)
   KVS_FOR_G(KVS_CASE, 128)
 #undef KVS_CASE
