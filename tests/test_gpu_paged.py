@@ -206,15 +206,15 @@ def test_paged_rejections():
         E.decode(q, kp, vp, 0.1, block_table=table[:, :2].contiguous(), T=T)
 
 
-@pytest.mark.parametrize("ragged", [False, True])
-def test_paged_planner_loop_matches_contiguous(ragged):
+@pytest.mark.parametrize("ragged,G,D", [(False, 4, 128), (True, 4, 128), (False, 8, 64)])
+def test_paged_planner_loop_matches_contiguous(ragged, G, D):
     """The device planner loop (key sums, plan with the appended key, the pass with the decision in it
     or not, updates carried by the other layer's pass) over paged caches gives the contiguous loop's
     outputs and state bit for bit; two layers share the carrier."""
     from kvskip_amd import workloads as W
     from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
 
-    G, D, Hkv, steps, layers = 4, 128, 2, 8, 2
+    Hkv, steps, layers = 2, 8, 2
     lens0 = [2600, 900, 1700] if ragged else [2600]
     B = len(lens0)
     run = W.planner_run(layers=layers, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=max(lens0), steps=steps, seed=91,
