@@ -27,14 +27,20 @@ __host__ __device__ __forceinline__ void gap_range(int prev, int cur, int nb, in
 template <int G, class List>
 __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, int i0, int n, int split,
                                 int64_t hq0, int wave, int lane, int prev0, int cur0) {
-  auto put = [&](int g, int blk) {
-    p.blk_max[(hq0 + g) * p.nb + blk] = NEG_INF;
-    p.blk_sum[(hq0 + g) * p.nb + blk] = 0.f;
+  // blocks a .. a + len - 1, thread t of a team of `stride`: blocks over the team, the G heads in an
+  // unrolled loop (no division by the run-time length)
+  auto put_range = [&](int a, int len, int t, int stride) {
+    for (int x = t; x < len; x += stride) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        p.blk_max[(hq0 + g) * p.nb + a + x] = NEG_INF;
+        p.blk_sum[(hq0 + g) * p.nb + a + x] = 0.f;
+      }
+    }
   };
   const int tid = wave * WAVE + lane;
   if (n_items == 0) {
-    if (split == 0)
-      for (int x = tid; x < G * p.nb; x += NT) put(x / p.nb, x % p.nb);
+    if (split == 0) put_range(0, p.nb, tid, NT);
     return;
   }
   for (int j = 0; wave + NWAVE * j < n; ++j) {  // uniform over the wavefront
@@ -49,11 +55,11 @@ __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, i
     }
     int a, len;
     gap_range(prev, cur, p.nb, a, len);
-    for (int x = lane; x < G * len; x += WAVE) put(x / len, a + x % len);
+    put_range(a, len, lane, WAVE);
   }
   if (n > 0 && i0 + n == n_items) {
     const int a = min(max(list(n_items - 1), -1), p.nb - 1) + 1, len = p.nb - a;
-    for (int x = tid; x < G * len; x += NT) put(x / len, a + x % len);
+    put_range(a, len, tid, NT);
   }
 }
 
