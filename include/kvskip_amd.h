@@ -113,6 +113,16 @@ int kvskip_decode(const kvskip_attn_args* a, int stats, int load_v, void* stream
 int kvskip_decode_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream);
 int kvskip_merge_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream);
 
+/* kvskip_decode without caller-provided split partials: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). a->part_acc and a->part_ml are ignored; the split-K partials
+ * go to a library-owned static device array of KVSKIP_SCRATCH_BYTES per GPU, so
+ * B * Hq * num_splits * (D + 2) * 4 bytes (plus alignment) must fit, else KVSKIP_E_INVALID. Every
+ * other argument, and the results, as kvskip_decode. Nothing is allocated or freed. All calls on
+ * one GPU share its array: calls that overlap in time on one GPU (two streams, two threads) race. */
+#define KVSKIP_SCRATCH_BYTES (16LL << 20)
+int kvskip_decode_scratch(const kvskip_attn_args* a, int stats, int load_v, void* stream);
+
 /* Two-pass V-skip, pass 2: out = sum over listed blocks of blk_scale * P . V (no softmax);
  * num_splits > 1 adds the plain sum of the partials.
  * Replaces kvskip::launch_pv (kernels/kvskip.h:117, kernels/kvskip_kernel.cu:754-759),

@@ -70,6 +70,7 @@ SIGNATURES = {
     "kvskip_decode": ([POINTER(AttnArgs), c_int, c_int, c_void_p], c_int),
     "kvskip_decode_splits": ([POINTER(AttnArgs), c_int, c_int, c_void_p], c_int),
     "kvskip_merge_splits": ([POINTER(AttnArgs), c_int, c_int, c_void_p], c_int),
+    "kvskip_decode_scratch": ([POINTER(AttnArgs), c_int, c_int, c_void_p], c_int),
     "kvskip_pv": ([POINTER(AttnArgs), c_void_p], c_int),
     "kvskip_vskip1": ([POINTER(AttnArgs), c_void_p], c_int),
     "kvskip_read": ([c_void_p, c_int64, c_void_p, c_int32, c_void_p], c_int),

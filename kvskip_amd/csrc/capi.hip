@@ -5,10 +5,21 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "internal.hpp"
 
 namespace {
+
+// Split-K partials of kvskip_decode_scratch: library-owned device memory, one copy per GPU (each
+// device that loads the library holds it until the process ends). Host code must never use this
+// name as an address: kvskip_decode_scratch takes each device's address from hipGetSymbolAddress.
+constexpr int64_t SCRATCH_FLOATS = KVSKIP_SCRATCH_BYTES / 4;
+__device__ __align__(256) float scratch[SCRATCH_FLOATS];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
 
 thread_local char g_err[512] = "";
 
@@ -184,6 +195,50 @@ int kvskip_decode_splits(const kvskip_attn_args* a, int stats, int load_v, void*
 
 int kvskip_merge_splits(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
   return decode_phases(a, stats, load_v, 2, stream);
+}
+
+int kvskip_decode_scratch(const kvskip_attn_args* a, int stats, int load_v, void* stream) {
+  if (a == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  // The partials live in `scratch`: part_acc [B, Hq, S, D] (with V) then part_ml [B, Hq, S, 2],
+  // each 256-byte aligned. Sizes are checked before any device call.
+  const int64_t S = a->num_splits;
+  int64_t acc_floats = 0, need = 0;
+  if (S > 1 && a->B > 0 && a->Hq > 0 && a->D > 0) {
+    const int64_t rows = static_cast<int64_t>(a->B) * a->Hq * S;
+    acc_floats = load_v ? (rows * a->D + 63) / 64 * 64 : 0;
+    need = acc_floats + rows * 2;
+    if (need > SCRATCH_FLOATS)
+      return fail(KVSKIP_E_INVALID,
+                  "kvskip_decode_scratch: split partials need %lld bytes, the scratch holds %lld "
+                  "(B * Hq * num_splits * (D + 2) * 4 bytes at most; lower num_splits or call kvskip_decode)",
+                  static_cast<long long>(need * 4), static_cast<long long>(KVSKIP_SCRATCH_BYTES));
+  }
+  kvskip_attn_args as = *a;
+  as.part_acc = nullptr;
+  as.part_ml = nullptr;
+  if (S > 1) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(KVSKIP_E_LAUNCH, "kvskip_decode_scratch: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+      return fail(KVSKIP_E_UNSUPPORTED, "kvskip_decode_scratch: device %d beyond %d", dev, SCRATCH_MAX_DEVICES);
+    float* base;
+    {
+      // first call on this device (current here): the device's own address of the array
+      std::lock_guard<std::mutex> lk(g_scratch_mu);
+      if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+          return fail(KVSKIP_E_LAUNCH, "kvskip_decode_scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+      }
+      base = g_scratch_ptr[dev];
+    }
+    as.part_acc = load_v ? base : nullptr;
+    as.part_ml = base + acc_floats;
+  }
+  return decode_phases(&as, stats, load_v, 3, stream);
 }
 
 int kvskip_pv(const kvskip_attn_args* a, void* stream) {

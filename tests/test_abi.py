@@ -110,3 +110,14 @@ def test_python_shim_messages():
         ext.check_kv(k, "k")
     with pytest.raises(RuntimeError, match="x: contiguous CUDA"):
         ext.read_bw(k, torch.zeros(1), 4)
+
+
+def test_scratch_decode_validation():
+    """kvskip_decode_scratch refuses more split partials than its static array holds, before any
+    device call, and otherwise validates like kvskip_decode."""
+    lib = _native.lib()
+    a = _args(B=64, num_splits=64)           # 64 * 32 * 64 * 130 * 4 bytes > 16 MiB
+    assert lib.kvskip_decode_scratch(ctypes.byref(a), 0, 1, None) == -1
+    assert "the scratch holds 16777216" in lib.kvskip_last_error().decode()
+    assert lib.kvskip_decode_scratch(ctypes.byref(_args(D=96)), 0, 1, None) == -2
+    assert lib.kvskip_decode_scratch(None, 0, 1, None) == -1
