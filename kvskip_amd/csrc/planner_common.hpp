@@ -359,6 +359,11 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
     if (!p.calib_free) c = fmaxf(c, 0.f);
     p.calib[bh] = c;
     if (p.aix != nullptr && c > p.aix_thr) p.aix[bh] = 1;
+  } else if (p.calib != nullptr && p.aix != nullptr && tid == 0 && cal0 > p.aix_thr) {
+    // the latch looks at every head's correction, not only the refreshing heads'
+    // (src/kvskip_attn.py:318-319): an unchanged correction above a threshold the head never
+    // crossed while refreshing (a threshold below the initial 0) latches it too
+    p.aix[bh] = 1;
   }
   uint64_t kn = kp;  // bit r: block in the stored set after this update
   if (tr) {

@@ -85,6 +85,10 @@ def _kv_dims(q, k, v, block_table=None, T=None):
     B, Hq, D = q.shape
     Hkv = k.shape[1]
     if block_table is None:
+        # every kernel reads v (and k) as [B, Hkv, T, D] of k's sizes: a shorter or narrower view
+        # would be read past its end
+        _require(k.dim() == 4 and v.dim() == 4 and k.shape[0] == B and k.shape[3] == D
+                 and tuple(v.shape) == tuple(k.shape), "shape mismatch between q, k, v")
         return B, Hq, D, Hkv, k.shape[2]
     return B, Hq, D, Hkv, _pool_tokens((k, v), B, Hkv, D, block_table, T)
 
@@ -410,10 +414,7 @@ def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, t
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
     B, Hq, D = q.shape
-    if block_table is None:
-        Hkv, T = k.shape[1], k.shape[2]
-    else:
-        _, _, _, Hkv, T = _kv_dims(q, k, k, block_table, T)
+    _, _, _, Hkv, T = _kv_dims(q, k, k, block_table, T)
     for t, n in ((csum, "csum"), (lse_ref, "lse_ref"), (cs_ref, "cs_ref"), (lse_att, "lse_att"), (cs_now, "cs_now")):
         check_f32(t, n)
     NBC = keep.shape[2]

@@ -48,12 +48,14 @@ class Policy:
     index_union: bool = False           # index blocks join the attended set instead of replacing it
 
     def flags(self, Hkv: int) -> list[int]:
-        """src/kvskip_attn.py:413-419."""
+        """Per-KV-head bits of the plan / update kernels (src/kvskip_attn.py:413-419): 1 refreshed on
+        every step, 2 token-index head (reads index + sink + local, never refreshes), 4 index union.
+        OR-ed, so a head in both lists decides as refresh_pre does (src/kvskip_attn.py:377-383)."""
         f = [0] * Hkv
         for h in self.dense_heads:
-            f[h] = 1
+            f[h] |= 1
         for h in self.index_heads:
-            f[h] = 4 if self.index_union else 2
+            f[h] |= 4 if self.index_union else 2
         return f
 
     def max_age_at(self, t: int) -> int:
@@ -308,7 +310,7 @@ class FusedPlanner:
         seq_lens: the ragged batch's lengths after this step's token (one more per sequence).
         block_table, T: a paged cache, as in first()."""
         if self.state is None:
-            return self.first(q, k, v, scale, seq_lens)
+            return self.first(q, k, v, scale, seq_lens, block_table=block_table, T=T)
         if q.dim() == 4:
             q = q.squeeze(2)
         B, Hq, D = q.shape

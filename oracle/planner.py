@@ -44,13 +44,15 @@ class Policy:
 
 
 def flags_of(policy: Policy, Hkv: int) -> list[int]:
-    """Per-KV-head flags of the fused driver (src/kvskip_attn.py:413-419): 1 always exact,
-    2 token-index head, 4 index union."""
+    """Per-KV-head flags of the fused driver (src/kvskip_attn.py:413-419): bit 0 always exact,
+    bit 1 token-index head, bit 2 index union. The bits are OR-ed: a head in both lists keeps
+    refresh_pre's decisions (forced refresh, then the index rule, src/kvskip_attn.py:377-383),
+    where _pack_fused's assignment would drop the forced refresh of an index-union head."""
     f = [0] * Hkv
     for h in policy.dense_heads:
-        f[h] = 1
+        f[h] |= 1
     for h in policy.index_heads:
-        f[h] = 4 if policy.index_union else 2
+        f[h] |= 4 if policy.index_union else 2
     return f
 
 
@@ -123,7 +125,8 @@ class State:
     t: int
     calib: torch.Tensor       # [B, Hkv]
     aix: torch.Tensor         # [B, Hkv] bool
-    topp_margin: float = math.inf
+    topp_margin: float = math.inf    # smallest top-p margin of any refresh so far
+    topp_heads: torch.Tensor | None = None   # [B, Hq] top-p margin of the last update (inf: no refresh)
     log: dict = field(default_factory=dict)
 
 
@@ -143,7 +146,7 @@ def init(q, k, v, scale, policy: Policy):
     st = State(scale=scale, G=G, T=T, csum=csum, keep=keep, lse_ref=logw, cs_ref=cs,
                lse_att=attended_lse(logw, keep | A.always_keep(nb, policy.local), G),
                age=torch.zeros(B, Hkv, dtype=torch.int64), t=0, calib=torch.zeros(B, Hkv, dtype=torch.float64),
-               aix=torch.zeros(B, Hkv, dtype=torch.bool), topp_margin=float(margin.min()))
+               aix=torch.zeros(B, Hkv, dtype=torch.bool), topp_margin=float(margin.min()), topp_heads=margin)
     return st, out
 
 
@@ -234,6 +237,7 @@ def update(st: State, pr: dict, logw, policy: Policy):
     st.lse_ref = torch.where(hq[..., None], logw, pad_blocks(st.lse_ref, nb, NEG_INF))
     st.cs_ref = torch.where(hq[..., None], pr["cs"], pad_blocks(st.cs_ref, nb, 0.0))
     st.age = torch.where(trig, torch.zeros_like(st.age), st.age)
+    st.topp_heads = margin.masked_fill(~hq, math.inf)
     if bool(trig.any()):
         st.topp_margin = min(st.topp_margin, float(margin[hq].min()))
     st.lse_att = attended_lse(logw, st.keep | A.always_keep(nb, policy.local), G)

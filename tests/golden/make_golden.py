@@ -5,11 +5,24 @@ on small seeded inputs, frozen: tests/test_golden.py checks that the oracle stil
 (CPU), tests/test_gpu_golden.py that the HIP path matches them (GPU).
 
     python tests/golden/make_golden.py          # rewrites attention_small.npz, planner_small.npz
+    python tests/golden/make_golden.py full     # rewrites planner_cfg4.npz, planner_cfg5.npz (~3 min)
+    python tests/golden/make_golden.py full 5   # only planner_cfg5.npz
+
+The full-size fixtures run the oracle's refresh_pre loop on the workloads of BASELINE configs 4
+and 5 (inputs regenerated from their seeds on the CPU by the tests, checked by a digest) and keep,
+per decode step and (sequence, KV head): the read set, the refresh decision and its margin, the
+stored set after the update and the top-p margin of a refresh, the estimate, the calibration, the
+index latch; per query head the
+attended log-sum-exp and output checksums (projections on seeded unit vectors and the norm), and
+the whole output every 64 steps (and at the last).
 """
 
 from __future__ import annotations
 
+import hashlib
+import math
 import sys
+import time
 from pathlib import Path
 
 import numpy as np
@@ -113,7 +126,143 @@ def planner_case() -> dict:
                 out=np.stack(outs), calib=st.calib.numpy(), aix=st.aix.numpy())
 
 
+# ---------------------------------------------------------------- full-size planner loops
+
+PROJ = 4              # output checksum: projections on PROJ seeded unit vectors, and the norm
+FULL_EVERY = 64       # whole outputs kept every FULL_EVERY steps (and at the last step)
+
+
+def stage4() -> OP.Policy:
+    """The stage-4 policy of configs 4 and 5 (reproduce/04-tails.sh:16,63-69)."""
+    return OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+
+
+def proj_dirs(D: int) -> torch.Tensor:
+    u = torch.randn(D, PROJ, generator=torch.Generator().manual_seed(99), dtype=torch.float64)
+    return u / u.norm(dim=0, keepdim=True)
+
+
+def full_steps(steps: int) -> list[int]:
+    return sorted(set(range(0, steps, FULL_EVERY)) | {steps - 1})
+
+
+def cfg5_lens() -> list[int]:
+    """Config 5's 16 contexts, log-uniform in [4096, 65536] from seed 5 (the bench's recipe)."""
+    g = torch.Generator().manual_seed(5)
+    return [int(round(math.exp(x))) for x in
+            (torch.rand(16, generator=g, dtype=torch.float64) * math.log(16) + math.log(4096)).tolist()]
+
+
+def loop_inputs(cfg: int):
+    """(run, planned layers, query sequences qs[layer][t] bf16 [B, Hq, D]) of config 4 (B 1, 32 / 8
+    heads, D 128, T0 32768, 128 steps, jumps 0.03; layer 0 dense, layers 1 and 2 planned) or config 5
+    (B 16 ragged contexts, 28 / 4 heads, 64 steps; one planned layer), generated on the CPU."""
+    from kvskip_amd import workloads as W
+    if cfg == 4:
+        run = W.planner_run(layers=3, B=1, Hq=32, Hkv=8, D=128, T0=32768, steps=128, seed=4)
+        layers = [1, 2]
+    elif cfg == 5:
+        run = W.planner_run(layers=1, B=16, Hq=28, Hkv=4, D=128, T0=65536, steps=64, seed=5, ragged=cfg5_lens())
+        layers = [0]
+    else:
+        raise ValueError(cfg)
+    qs = {}
+    for l in layers:
+        qp = W.QueryProcess(run, l, p_jump=0.03)
+        qs[l] = [qp.next() for _ in range(run.steps)]
+    return run, layers, qs
+
+
+def input_digest(run, layers, qs) -> str:
+    """sha256 over the planned layers' K / V, the query sequences and the token ids."""
+    h = hashlib.sha256()
+    for l in layers:
+        h.update(run.k[l].view(torch.int16).numpy().tobytes())
+        h.update(run.v[l].view(torch.int16).numpy().tobytes())
+        for q in qs[l]:
+            h.update(q.view(torch.int16).numpy().tobytes())
+    h.update(run.ids.numpy().tobytes())
+    return h.hexdigest()
+
+
+def oracle_loop(k, v, qs, ids, T0, scale, pol, steps, b=0):
+    """The oracle's refresh_pre loop for one sequence (row b of k / v / qs / ids, prefix T0, one
+    token appended per step): per-step records (see the module docstring); read sets padded to the
+    capacity of k."""
+    kb, vb, idb = k[b:b + 1], v[b:b + 1], ids[b:b + 1].numpy()
+    Hkv = kb.shape[1]
+    G = qs[0].shape[1] // Hkv
+    nbmax = O.nblocks(k.shape[2])
+    u = proj_dirs(kb.shape[3])
+    rec = {key: [] for key in ("read", "keep", "trig", "margin", "topp", "miss", "calib", "aix", "lse_att", "proj",
+                               "norm")}
+    full = []
+    st = None
+    for t in range(steps):
+        T = T0 + t + 1
+        q = qs[t][b:b + 1]
+        if t == 0:
+            st, out = OP.init(q, kb[:, :, :T], vb[:, :, :T], scale, pol)
+            read = torch.ones(1, Hkv, O.nblocks(T), dtype=torch.bool)
+            trig = torch.ones(1, Hkv, dtype=torch.bool)
+            margin = torch.full((1, Hkv), math.inf, dtype=torch.float64)
+            miss = torch.full((1, Hkv), math.nan, dtype=torch.float64)
+        else:
+            idx = torch.from_numpy(OP.index_blocks(idb, T))
+            out, pr = OP.step(st, q, kb[:, :, :T], vb[:, :, :T], pol, idx=idx)
+            read, trig, margin, miss = pr["read"], pr["trig"], pr["margin"], pr["miss"]
+        pad = np.zeros((Hkv, nbmax), dtype=bool)
+        pad[:, :read.shape[-1]] = read[0].numpy()
+        rec["read"].append(np.packbits(pad, axis=-1))
+        kp = np.zeros((Hkv, nbmax), dtype=bool)
+        kp[:, :st.keep.shape[-1]] = st.keep[0].numpy()
+        rec["keep"].append(np.packbits(kp, axis=-1))
+        rec["trig"].append(trig[0].numpy())
+        rec["margin"].append(margin[0].numpy().astype(np.float32))
+        rec["topp"].append(st.topp_heads[0].reshape(Hkv, G).amin(-1).numpy().astype(np.float32))
+        rec["miss"].append(miss[0].numpy().astype(np.float32))
+        rec["calib"].append(st.calib[0].numpy().astype(np.float32))
+        rec["aix"].append(st.aix[0].numpy())
+        rec["lse_att"].append(st.lse_att[0].numpy().astype(np.float32))
+        rec["proj"].append((out[0] @ u).numpy().astype(np.float32))
+        rec["norm"].append(out[0].norm(dim=-1).numpy().astype(np.float32))
+        if t in full_steps(steps):
+            full.append(out[0].numpy().astype(np.float32))
+    res = {key: np.stack(val) for key, val in rec.items()}
+    res["out_full"] = np.stack(full)
+    return res
+
+
+def loop_case(cfg: int, steps: int | None = None) -> dict:
+    """Config 4: records [layer, step, ...] of the two planned layers; config 5: [sequence, step, ...]
+    of the planned layer (each sequence its own oracle state, as the reference planner keeps per-row
+    decisions). steps: fewer steps (the CPU test's prefix check)."""
+    run, layers, qs = loop_inputs(cfg)
+    n = run.steps if steps is None else steps
+    pol = stage4()
+    parts = []
+    if cfg == 4:
+        for l in layers:
+            parts.append(oracle_loop(run.k[l], run.v[l], qs[l], run.ids, run.T0[0], run.scale, pol, n))
+    else:
+        for b in range(len(run.T0)):
+            parts.append(oracle_loop(run.k[0], run.v[0], qs[0], run.ids, run.T0[b], run.scale, pol, n, b=b))
+    out = {key: np.stack([p[key] for p in parts]) for key in parts[0]}
+    out["digest"] = np.array(input_digest(run, layers, qs))
+    out["T0"] = np.array(run.T0, dtype=np.int64)
+    out["layers"] = np.array(layers, dtype=np.int64)
+    out["full_steps"] = np.array(full_steps(n), dtype=np.int64)
+    return out
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "full":
+        for cfg in ((4, 5) if len(sys.argv) < 3 else (int(sys.argv[2]),)):
+            t0 = time.time()
+            name = f"planner_cfg{cfg}.npz"
+            np.savez_compressed(HERE / name, **loop_case(cfg))
+            print(name, (HERE / name).stat().st_size, "bytes", f"{time.time() - t0:.0f} s", flush=True)
+        return
     np.savez_compressed(HERE / "attention_small.npz", **attention_case())
     np.savez_compressed(HERE / "planner_small.npz", **planner_case())
     for f in ("attention_small.npz", "planner_small.npz"):

@@ -17,7 +17,7 @@ from oracle import attention as O
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-REL, LSE_TOL, BORDER = 2e-3, 2e-4, 1e-5
+REL, LSE_TOL = 2e-3, 2e-4
 
 
 def _bf16(a):
@@ -46,8 +46,7 @@ def test_attention_golden(gpu):
     logw = (bmax + torch.log(bsum))
     keep = K.select_blocks(logw, G, "topp", 0.9, local=1).cpu().numpy()
     _, margin = O.topp_heads(torch.from_numpy(d["blk_max"]) + torch.log(torch.from_numpy(d["blk_sum"])), 0.9)
-    far = (margin.reshape(keep.shape[0], keep.shape[1], G).amin(-1) >= BORDER).numpy()
-    assert np.array_equal(keep[far], d["topp_keep"][far])
+    assert np.array_equal(keep, d["topp_keep"]), f"top-p sets differ (oracle margins {margin.min():.2e} and up)"
     # single-pass V-skip: V blocks read per (b, KV head)
     lp = torch.from_numpy(d["lse_prev"]).float().cuda()
     res = K.vskip_one_pass(q, k, v, scale, tau=0.02, local=1, count=True, lse_prev=lp, num_splits=2)
@@ -72,9 +71,8 @@ def test_planner_golden(gpu):
             out = fp.step(q, k[:, :, :T], v[:, :, :T], scale, ids=ids)
         read = fp.read_mask(math.ceil(T / 64)).cpu().numpy()
         ref = d["read"][t][..., :read.shape[-1]]
-        far = d["margin"][t] >= BORDER
-        assert np.array_equal(read[far], ref[far]), f"read set at step {t}"
-        assert np.array_equal(fp.state["trig"].bool().cpu().numpy()[far], d["trig"][t][far])
+        assert np.array_equal(read, ref), f"read set at step {t} (oracle margins {d['margin'][t].tolist()})"
+        assert np.array_equal(fp.state["trig"].bool().cpu().numpy(), d["trig"][t])
         assert O.rel_err(out.float().cpu(), torch.from_numpy(d["out"][t])) <= REL, t
     assert np.abs(fp.state["calib"].cpu().double().numpy() - d["calib"]).max() <= 1e-4
     assert np.array_equal(fp.state["aix"].bool().cpu().numpy(), d["aix"])

@@ -287,3 +287,160 @@ def test_attended_lse_all_blocks_is_full_lse():
     M, S = O.block_stats(q, k, 0.25)
     full = OP.attended_lse(O.block_logw(M, S), torch.ones(1, 2, M.shape[-1], dtype=torch.bool), 4)
     assert torch.allclose(full, torch.logsumexp(O.scores(q, k, 0.25), -1), atol=1e-12)
+
+
+# ---------------------------------------------------------------- planner pieces pinned separately
+
+def brute_index(ids, T):
+    """Loops: blocks with an earlier copy of ids[T-1], or the position right after one."""
+    cur = ids[T - 1]
+    hits = set()
+    for t in range(T):
+        if (t < T - 1 and ids[t] == cur) or (1 <= t and t - 1 < T - 1 and ids[t - 1] == cur):
+            hits.add(t // 64)
+    return hits
+
+
+def test_update_csum_appended_keys():
+    """Key sums kept current by adding the appended rows (one at a time up to a full block, into a
+    new block, several at once) equal the sums of the grown cache from scratch and by loops
+    (src/kvskip_attn.py:273-279 against src/kvskip_attn.py:170-179)."""
+    B, Hkv, D = 1, 2, 5
+    k = rnd(B, Hkv, 330, D, seed=60)
+    q, v = rnd(B, 4, D, seed=61), rnd(B, Hkv, 330, D, seed=62)
+    st, _ = OP.init(q, k[:, :, :127], v[:, :, :127], 1.0, OP.Policy())
+    for T in (128, 129, 130, 192, 193, 260, 330):
+        OP.update_csum(st, k[:, :, :T])
+        assert st.T == T and st.csum.shape == (B, Hkv, O.nblocks(T), D)
+        assert torch.allclose(st.csum, OP.centroid_sums(k[:, :, :T]), atol=1e-12)
+    for h in range(Hkv):
+        for blk in range(O.nblocks(330)):
+            for d in range(D):
+                ref = sum(float(k[0, h, t, d]) for t in range(blk * 64, min(330, blk * 64 + 64)))
+                assert abs(float(st.csum[0, h, blk, d]) - ref) < 1e-12
+    # the plan's centroid scores then use the grown sums (partial last block: its own row count)
+    st2, _ = OP.init(q, k[:, :, :200], v[:, :, :200], 1.0, OP.Policy())
+    pr = OP.plan(st2, q, k[:, :, :201], OP.Policy())
+    assert torch.allclose(pr["cs"], OP.centroid_scores(q, OP.centroid_sums(k[:, :, :201]), 201, 1.0), atol=1e-12)
+
+
+def test_index_only_heads_read_the_index_and_never_refresh():
+    """A token-index head reads index blocks + sink + local only and never refreshes, whatever its
+    drift or age (src/kvskip_attn.py:381-383); the other heads refresh by age."""
+    q, k, v = _layer(seed=70)
+    T = k.shape[2]
+    nb = O.nblocks(T)
+    ids = np.random.default_rng(71).integers(0, 40, size=(1, T))
+    idx = torch.from_numpy(OP.index_blocks(ids, T))
+    hits = brute_index(ids[0], T)
+    assert 0 < len(hits) < nb - 3
+    pol = OP.Policy(max_age=2, index_heads=(1,), index_union=False)
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    keep1 = st.keep[0, 1].clone()
+    q2 = q.clone()
+    outside = int(torch.nonzero(~(st.keep[0, 1] | O.always_keep(nb, 2)))[0])
+    c = k[0, 1, outside * 64:outside * 64 + 64].mean(0)
+    q2[0, 4:8] = 40.0 * c / c.norm()                # KV head 1's queries drift far outside its set
+    for t in range(1, 5):
+        out, pr = OP.step(st, q2, k, v, pol, idx=idx)
+        assert not bool(pr["trig"][0, 1]) and math.isinf(float(pr["margin"][0, 1]))
+        expect = hits | {0, nb - 2, nb - 1}
+        assert set(torch.nonzero(pr["read"][0, 1]).flatten().tolist()) == expect
+        assert bool(pr["trig"][0, 0]) == (t % 2 == 0)        # age limit 2 on the ordinary head
+        assert torch.equal(st.keep[0, 1], keep1)               # never refreshed
+        # its output is attention over exactly the index blocks + sink + local
+        ref, _ = O.decode(q2, k, v, 1.0, keep=pr["read"])
+        assert torch.allclose(out[0, 4:8], ref[0, 4:8], atol=1e-12)
+    assert OP.flags_of(pol, 2) == [0, 2]
+
+
+def test_index_union_heads_attend_and_estimate_with_the_index():
+    """An index-union head attends stored set + sink + local + index blocks (src/kvskip_attn.py:359-360)
+    and still refreshes normally. Its estimate leaves the index blocks out of the missed part: right
+    after a refresh with the same query, miss = P_out / (P_out + P_att) by brute force, P_out the
+    softmax mass outside that larger set and P_att the mass of the previous step's attended set
+    (stored + sink + local, the lse_att of src/kvskip_attn.py:392)."""
+    q, k, v = _layer(seed=72)
+    T = k.shape[2]
+    nb = O.nblocks(T)
+    ids = np.random.default_rng(73).integers(0, 30, size=(1, T))
+    idx = torch.from_numpy(OP.index_blocks(ids, T))
+    pol = OP.Policy(index_heads=(1,), index_union=True)
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    stored = st.keep.clone()
+    pr = OP.plan(st, q, k, pol, idx=idx)
+    always = O.always_keep(nb, 2)
+    assert torch.equal(pr["sel"][0, 0], stored[0, 0] | always)
+    assert torch.equal(pr["sel"][0, 1], stored[0, 1] | always | idx[0])
+    assert bool((idx[0] & ~(stored[0, 1] | always)).any())          # the index adds blocks
+    p = torch.softmax(O.scores(q, k, 1.0), -1)
+    p_out = (p * ~O.heads(O.token_mask(pr["sel"], T), 4)).sum(-1)
+    p_att = (p * O.heads(O.token_mask(stored | always, T), 4)).sum(-1)
+    missed = (p_out / (p_out + p_att)).reshape(1, 2, 4).amax(-1)
+    assert torch.allclose(pr["miss"], missed, atol=1e-12)
+    plain = (p * ~O.heads(O.token_mask(stored | always, T), 4)).sum(-1).reshape(1, 2, 4)[0, 1].amax()
+    assert float(missed[0, 1]) < float(plain)                             # the index blocks are not missed
+    pol_dense = OP.Policy(index_heads=(1,), index_union=True, dense_heads=(1,))
+    st, _ = OP.init(q, k, v, 1.0, pol_dense)
+    assert bool(OP.plan(st, q, k, pol_dense, idx=idx)["trig"][0, 1])   # a forced union head refreshes
+    assert OP.flags_of(pol_dense, 2) == [0, 5]
+
+
+def test_auto_index_latch_threshold_and_union():
+    """The latch: after each step's calibration every head with correction > threshold joins the
+    token index for good (src/kvskip_attn.py:318-319), strictly above, sticky, refreshing or not;
+    a latched head's attended set then includes the index blocks (src/kvskip_attn.py:361-362)."""
+    q, k, v = _layer(seed=74)
+    T = k.shape[2]
+    nb = O.nblocks(T)
+    ids = np.random.default_rng(75).integers(0, 30, size=(1, T))
+    idx = torch.from_numpy(OP.index_blocks(ids, T))
+    thr = 0.25
+    # rate 0: c = max(c, resid); delta 0.9 keeps miss + c under it (no refresh)
+    pol = OP.Policy(delta=0.9, calib=0.0, calib_kind="peak", calib_auto_ix=thr)
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    up = math.nextafter(thr, math.inf)
+    st.calib = torch.tensor([[thr, up]], dtype=torch.float64)           # equal: no latch; above: latch
+    _, pr = OP.step(st, q, k, v, pol, idx=idx)
+    assert not pr["trig"].any()                                         # no head refreshed
+    assert st.aix.tolist() == [[False, True]]
+    stored = st.keep.clone()
+    st.calib = torch.zeros_like(st.calib)                               # below the threshold: stays latched
+    pr = OP.plan(st, q, k, pol, idx=idx)
+    assert st.aix.tolist() == [[False, True]]
+    always = O.always_keep(nb, 2)
+    assert torch.equal(pr["sel"][0, 0], stored[0, 0] | always)
+    assert torch.equal(pr["sel"][0, 1], stored[0, 1] | always | idx[0])
+    # a threshold below the initial correction latches every head on the first step
+    pol_neg = OP.Policy(calib=0.05, calib_kind="peak", calib_auto_ix=-1.0)
+    st, _ = OP.init(q, k, v, 1.0, pol_neg)
+    OP.step(st, q, k, v, pol_neg, idx=idx)
+    assert st.aix.all()
+
+
+def test_flags_of():
+    """Bit 0: refreshed on every step; bit 1: token-index head; bit 2: index union; OR-ed per head
+    (src/kvskip_attn.py:413-419)."""
+    assert OP.flags_of(OP.Policy(), 3) == [0, 0, 0]
+    assert OP.flags_of(OP.Policy(dense_heads=(0, 2)), 3) == [1, 0, 1]
+    assert OP.flags_of(OP.Policy(index_heads=(1,)), 3) == [0, 2, 0]
+    assert OP.flags_of(OP.Policy(index_heads=(1, 2), index_union=True), 3) == [0, 4, 4]
+    assert OP.flags_of(OP.Policy(dense_heads=(1,), index_heads=(1,)), 2) == [0, 3]
+    # a head in both lists with index-only: the index rule wins (no refresh), as in refresh_pre
+    q, k, v = _layer(seed=76)
+    ids = np.random.default_rng(77).integers(0, 30, size=(1, k.shape[2]))
+    idx = torch.from_numpy(OP.index_blocks(ids, k.shape[2]))
+    pol = OP.Policy(dense_heads=(1,), index_heads=(1,))
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    assert not bool(OP.plan(st, q, k, pol, idx=idx)["trig"][0, 1])
+
+
+def test_topp_margin_per_head():
+    """update() records each refreshed query head's own top-p margin (inf for the others)."""
+    q, k, v = _layer(seed=78)
+    pol = OP.Policy(dense_heads=(0,))
+    st, _ = OP.init(q, k, v, 1.0, pol)
+    _, pr = OP.step(st, q, k, v, pol)
+    M, S = O.block_stats(q, k, 1.0, keep=pr["read"])
+    _, margin = O.topp_heads(O.block_logw(M, S), pol.level)
+    assert torch.equal(st.topp_heads[0, :4], margin[0, :4]) and torch.isinf(st.topp_heads[0, 4:]).all()
