@@ -2,13 +2,15 @@
 once and replayed for every later step. The step's length lives in device memory (seq_lens, the
 ragged form, here with B 1) and the graph's first node advances it, so no launch argument changes
 between steps; after the policy's warm-up (max age and calibration switch fixed) the replays must
-reproduce the eager step-by-step loop bit for bit."""
+reproduce the eager step-by-step loop bit for bit, and the oracle's refresh_pre loop on the same
+inputs: identical read sets on every layer-step, outputs within 2e-3."""
 
 import pytest
 import torch
 
 from kvskip_amd import workloads as W
 from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+from oracle_side import LayerOracle, oracle_policy, rel_ok, same_decisions
 
 pytestmark = pytest.mark.gpu
 
@@ -38,6 +40,15 @@ def test_one_graph_replayed_every_step(gpu, carried):
             else:
                 outs.append(fp.step(q[l], ks[l], vs[l], run.scale, ids=ids, seq_lens=sl))
         return outs
+
+    # the oracle's loop on the same inputs: read sets and outputs of every layer-step
+    orc = [LayerOracle(oracle_policy(_policy()), run.scale) for _ in range(layers)]
+    ids_c = ids.cpu().numpy()
+    ref_orc = []
+    for t in range(steps):
+        T = T0 + t + 1
+        ref_orc.append([orc[l].step(qs[t][l].cpu(), run.k[l][:, :, :T], run.v[l][:, :, :T], ids_c)
+                        for l in range(layers)])
 
     # eager reference, one step at a time
     ce = UpdateCarrier() if carried else None
@@ -73,6 +84,10 @@ def test_one_graph_replayed_every_step(gpu, carried):
             assert torch.equal(outs[l], ref_out[t][l]), (t, l)
             for k in STATE:
                 assert torch.equal(planners[l].state[k], ref_state[t][l][k]), (t, l, k)
+            o_ref, read, trig, margin = ref_orc[t][l]
+            same_decisions(planners[l].read_mask(read.shape[-1]).cpu(), read, trig,
+                           planners[l].state["trig"].bool().cpu(), margin, (t, l))
+            rel_ok(outs[l], o_ref, (t, l))
     if carried:                  # the last replay's final update (the graph's tail holds it pending)
         ce.flush()
         cg.flush()

@@ -1,9 +1,12 @@
 """GPU: the attention passes over a paged KV cache (kvskip_attn_args.block_table: 64-token pages in a
-pool, a block table per sequence) against the same passes over the contiguous cache. Only the
-addresses differ, so outputs, log-sum-exps and block statistics must be bit-identical. The pools are
-built from the contiguous cache in a random page order, and every byte the pass must not read
-(unused pages, rows past a sequence's last token, pages of other sequences) holds NaN, so a wrong
-page or a read past the sequence shows up in the results."""
+pool, a block table per sequence) against the same passes over the contiguous cache, and against the
+CPU oracle on the rows the block table addresses (gathered from the pools on the CPU). Only the
+addresses differ from the contiguous cache, so outputs, log-sum-exps and block statistics must be
+bit-identical to it; against the oracle, outputs within 2e-3, statistics within 2e-4, and the
+decisions (V-skip votes, top-p sets, the planner's read sets) identical. The pools are built from
+the contiguous cache in a random page order, and every byte the pass must not read (unused pages,
+rows past a sequence's last token, pages of other sequences) holds NaN, so a wrong page or a read
+past the sequence shows up in the results."""
 
 import math
 
@@ -12,6 +15,8 @@ import torch
 
 from kvskip_amd import ext as E
 from kvskip_amd import kvskip as K
+from oracle import attention as O
+from oracle_side import LayerOracle, gather_pages, oracle_policy, rel_ok, same_decisions
 
 pytestmark = pytest.mark.gpu
 
@@ -54,6 +59,22 @@ def _same(a, b, what):
     assert torch.equal(a, b), (what, (a.float() - b.float()).abs().max().item())
 
 
+def _gathered(kp, vp, table, lens):
+    """The oracle's view of the pools: per sequence the rows its table addresses (CPU), concatenated
+    into [B, Hkv, T, D] when the lengths agree."""
+    ks, vs = gather_pages(kp, table, lens), gather_pages(vp, table, lens)
+    if len(set(lens)) == 1:
+        return torch.cat(ks), torch.cat(vs)
+    return ks, vs
+
+
+def _stats_close(got_max, got_sum, M, S, what):
+    fin = torch.isfinite(M)
+    assert torch.equal(torch.isfinite(got_max.cpu()), fin), what
+    assert (got_max.cpu().double()[fin] - M[fin]).abs().max().item() <= 2e-4, what
+    assert (got_sum.cpu().double()[fin] / S[fin] - 1).abs().max().item() <= 2e-4, what
+
+
 @pytest.mark.parametrize("G,D", [(4, 128), (7, 128), (8, 64), (1, 64)])
 @pytest.mark.parametrize("T", [4096, 3001])
 def test_paged_dense_and_stats_match_contiguous(G, D, T):
@@ -69,6 +90,12 @@ def test_paged_dense_and_stats_match_contiguous(G, D, T):
             if stats:
                 _same(got["blk_max"], ref["blk_max"], ("blk_max", S))
                 _same(got["blk_sum"], ref["blk_sum"], ("blk_sum", S))
+    kg, vg = _gathered(kp, vp, table, [T, T])
+    assert torch.equal(kg, k.cpu()) and torch.equal(vg, v.cpu())
+    out, lse = O.decode(q.cpu(), kg, vg, D ** -0.5)
+    rel_ok(got["out"], out, "paged dense vs oracle")
+    assert (got["lse"].cpu().double() - lse).abs().max().item() <= 2e-4
+    _stats_close(got["blk_max"], got["blk_sum"], *O.block_stats(q.cpu(), kg, D ** -0.5), "paged stats vs oracle")
 
 
 @pytest.mark.parametrize("G,D", [(4, 128), (7, 128)])
@@ -88,6 +115,13 @@ def test_paged_masked_stats_match_contiguous(G, D):
         got = K.decode(q, kp, vp, D ** -0.5, plan=plan, stats=True, num_splits=S, block_table=table, T=T)
         for key in ("out", "lse", "blk_max", "blk_sum"):
             _same(got[key], ref[key], (key, S))
+    kg, vg = _gathered(kp, vp, table, [T, T])
+    out, _ = O.decode(q.cpu(), kg, vg, D ** -0.5, keep=keep)
+    live = O.heads(keep.any(-1, keepdim=True), G)[..., 0]                 # the empty list: out 0
+    rel_ok(got["out"][live], out[live], "paged masked vs oracle")
+    assert (got["out"][~live.cuda()] == 0).all()
+    _stats_close(got["blk_max"], got["blk_sum"], *O.block_stats(q.cpu(), kg, D ** -0.5, keep=keep),
+                 "paged masked stats vs oracle")
 
 
 def test_paged_ragged_batch_matches_contiguous():
@@ -106,6 +140,11 @@ def test_paged_ragged_batch_matches_contiguous():
         if stats:
             _same(got["blk_max"], ref["blk_max"], ("blk_max", load_v))
             _same(got["blk_sum"], ref["blk_sum"], ("blk_sum", load_v))
+        if load_v:
+            kg, vg = _gathered(kp, vp, table, lens)
+            for b, n in enumerate(lens):
+                out, _ = O.decode(q[b:b + 1].cpu(), kg[b], vg[b], D ** -0.5)
+                rel_ok(got["out"][b:b + 1], out, ("paged ragged vs oracle", b))
 
 
 def test_paged_invalid_page_reads_as_empty_block():
@@ -166,6 +205,10 @@ def test_paged_vskip_two_pass_matches_contiguous(G, D, T):
         assert torch.equal(got["keep"], ref["keep"]), rule
         assert 0 < ref["kept_frac"] < 1, (rule, ref["kept_frac"])
         _same(got["out"], ref["out"], ("out", rule))
+        kg, vg = _gathered(kp, vp, table, [T, T])
+        o_ref, keep = O.vskip_two_pass(q.cpu(), kg, vg, D ** -0.5, rule, value)
+        assert torch.equal(got["keep"].cpu(), keep), ("paged two-pass selection vs oracle", rule)
+        rel_ok(got["out"], o_ref, ("paged two-pass vs oracle", rule))
 
 
 @pytest.mark.parametrize("G,D", [(4, 128), (8, 64), (1, 64)])
@@ -187,6 +230,16 @@ def test_paged_vskip_one_pass_matches_contiguous(G, D, T):
             for key in ("out", "lse", "v_tiles"):
                 _same(got[key], ref[key], (key, S, lp is None))
             assert ref["v_tiles"].sum().item() < 2 * Hkv * nb, (S, lp is None)      # some V blocks skipped
+    kg, vg = _gathered(kp, vp, table, [T, T])
+    for lp, tau in ((None, 1.2), (lse_prev, 1.2 / nb)):
+        got = K.vskip_one_pass(q, kp, vp, D ** -0.5, tau=tau, num_splits=8, count=True, lse_prev=lp,
+                               block_table=table, T=T)
+        lpd = None if lp is None else lp.cpu().double()
+        o_ref, _, keep, cnt = O.vskip1(q.cpu(), kg, vg, D ** -0.5, tau, 2, lse_prev=lpd)
+        _, z = O.vskip1_keep(q.cpu(), kg, D ** -0.5, tau, 2, lse_prev=lpd)
+        assert float(z.abs().min()) > 1e-5                                  # no vote at float32 noise
+        assert torch.equal(got["v_tiles"].cpu(), cnt), ("paged one-pass votes vs oracle", lp is None)
+        rel_ok(got["out"], o_ref, ("paged one-pass vs oracle", lp is None))
 
 
 def test_paged_rejections():
@@ -232,6 +285,9 @@ def test_paged_planner_loop_matches_contiguous(ragged, G, D):
     dut = [FusedPlanner(pol(), count=False, carrier=cr) for _ in range(layers)]
     keys = ("csum", "keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt", "calib", "est",
             "aix")
+    # the oracle's refresh_pre loop per (layer, sequence) on the rows the block tables address
+    orc = [[LayerOracle(oracle_policy(pol()), run.scale) for _ in range(B)] for _ in range(layers)]
+    ids_c = ids.cpu().numpy()
     for t in range(steps):
         if ragged:
             sl = torch.tensor([n + t + 1 for n in lens0], dtype=torch.int32, device="cuda")
@@ -248,6 +304,17 @@ def test_paged_planner_loop_matches_contiguous(ragged, G, D):
                 a = ref[l].step(qs[t][l], *kv, run.scale, ids=ids, seq_lens=sl)
                 b = dut[l].step(qs[t][l], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
             assert torch.equal(a.clone(), b.clone()), (t, l)
+            lens = [n + t + 1 for n in lens0]
+            kg, vg = gather_pages(kp, table, lens), gather_pages(vp, table, lens)
+            s = dut[l].state
+            for bb in range(B):
+                o_ref, read, trig, margin = orc[l][bb].step(qs[t][l][bb:bb + 1].cpu(), kg[bb], vg[bb], ids_c[bb:bb + 1])
+                nb = read.shape[-1]
+                dev_read = torch.zeros(1, Hkv, nb, dtype=torch.bool)
+                for h in range(Hkv):
+                    dev_read[0, h, s["block_idx"][bb, h, :int(s["block_cnt"][bb, h])].long().cpu()] = True
+                same_decisions(dev_read, read, trig, s["trig"][bb:bb + 1].bool().cpu(), margin, (t, l, bb))
+                rel_ok(b[bb:bb + 1], o_ref, (t, l, bb))
         cr.flush()
         for l in range(layers):
             for key in keys:

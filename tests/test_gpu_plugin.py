@@ -1,9 +1,12 @@
 """GPU: the attention plugin's decode modes (kvskip_amd.attention.kvskip_attention_forward, the
 reference's src/kvskip_attn.py:481-515) driven the way a model drives them: one call per layer per
-step on the growing cache's strided views. Each mode must give what its kernels give when called
-directly (the same launches: bit for bit), the refresh loop with carried updates the same lists as
-without, and a replay of the recorded lists the refresh loop's outputs within the attention
-tolerance."""
+step on the growing cache's strided views. Each mode is checked against the CPU oracle of the
+reference's semantics on the same inputs: dense against exact attention, vskip2 against the oracle's
+two-pass V-skip, vskip1 / vskip1sink against the oracle's keep rule (V blocks read per KV head) and
+output, refresh_fused against the oracle's refresh_pre loop (read sets and refresh decisions
+identical on every head-step, outputs within 2e-3), replay against exact attention over the
+recorded lists. Besides, each mode gives what its kernels give when called directly (the same
+launches: bit for bit), and the refresh loop with carried updates the same lists as without."""
 
 from types import SimpleNamespace
 
@@ -13,6 +16,8 @@ import torch
 from kvskip_amd import attention as A
 from kvskip_amd import kvskip as K
 from kvskip_amd.planner import FusedPlanner
+from oracle import attention as O
+from oracle_side import LayerOracle, oracle_policy, rel_ok, same_decisions
 
 pytestmark = pytest.mark.gpu
 
@@ -62,7 +67,7 @@ def _drive(cfg, ks, vs, qs, ids=None):
     return outs, cache
 
 
-def test_dense_and_vskip_modes_match_direct_calls():
+def test_dense_and_vskip_modes_match_direct_calls_and_oracle():
     ks, vs, qs, _ = _data(31)
     for mode in ("dense", "vskip2", "vskip1", "vskip1sink"):
         outs, cache = _drive(A.KvskipConfig(mode=mode, dense_layers=(), count=False), ks, vs, qs)
@@ -72,15 +77,29 @@ def test_dense_and_vskip_modes_match_direct_calls():
             for l in range(LAYERS):
                 k, v = cache.layers[l]._kbuf[:, :, :n], cache.layers[l]._vbuf[:, :, :n]
                 q = qs[l][t][:, :, 0]
+                qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
                 if mode == "dense":
                     ref = K.decode(q, k, v, SCALE)["out"]
+                    rel_ok(outs[t][l], O.decode(qc, kc, vc, SCALE)[0], (mode, t, l))
                 elif mode == "vskip2":
                     ref = K.vskip_two_pass(q, k, v, SCALE, rule="topp", value=0.99, local=2, sync=False)["out"]
+                    # the oracle's selection on its own statistics: identical sets unless a top-p cut is a
+                    # float32 near tie (checked), then exact attention over the kept set
+                    M, S = O.block_stats(qc, kc, SCALE)
+                    _, margin = O.topp_heads(O.block_logw(M, S), 0.99)
+                    assert float(margin.min()) > 1e-6, (mode, t, l, float(margin.min()))
+                    rel_ok(outs[t][l], O.vskip_two_pass(qc, kc, vc, SCALE, "topp", 0.99, 2)[0], (mode, t, l))
                 else:
-                    r = K.vskip_one_pass(q, k, v, SCALE, tau=1e-4, local=2,
-                                         lse_prev=lse[l] if mode == "vskip1" else None, sync=False)
+                    prev = lse[l] if mode == "vskip1" else None
+                    r = K.vskip_one_pass(q, k, v, SCALE, tau=1e-4, local=2, lse_prev=prev, sync=False, count=True)
                     lse[l] = r["lse"]
                     ref = r["out"]
+                    o_ref, _, keep, cnt = O.vskip1(qc, kc, vc, SCALE, 1e-4, 2,
+                                                   lse_prev=None if prev is None else prev.cpu().double())
+                    _, z = O.vskip1_keep(qc, kc, SCALE, 1e-4, 2, lse_prev=None if prev is None else prev.cpu().double())
+                    assert float(z.abs().min()) > 1e-5, (mode, t, l)        # no vote at float32 noise
+                    assert torch.equal(r["v_tiles"].cpu(), cnt), (mode, t, l)
+                    rel_ok(outs[t][l], o_ref, (mode, t, l))
                 assert torch.equal(outs[t][l], ref), (mode, t, l)
 
 
@@ -96,6 +115,20 @@ def test_refresh_fused_matches_planner_loop(index):
     outs, _ = _drive(cfg, ks, vs, qs, ids if index else None)
     plain_state = {l: cfg.state[l]["planner"].state for l in range(1, LAYERS)}
     masks = cfg.plans
+
+    # the oracle's refresh_pre loop on the same inputs (layer 0 dense): identical decisions
+    orc = {l: LayerOracle(oracle_policy(cfg.policy(l)), SCALE) for l in range(1, LAYERS)}
+    ids_c = ids.cpu().numpy()
+    for t in range(STEPS):
+        n = T0 + t
+        for l in range(LAYERS):
+            qc, kc, vc = qs[l][t][:, :, 0].cpu(), ks[l][:, :, :n].cpu(), vs[l][:, :, :n].cpu()
+            if l == 0:
+                rel_ok(outs[t][l], O.decode(qc, kc, vc, SCALE)[0], (t, l))
+                continue
+            o_ref, read, trig, margin = orc[l].step(qc, kc, vc, ids_c)
+            same_decisions(masks[l][t].cpu(), read, trig, trig, margin, (t, l))   # a refresh reads every block
+            rel_ok(outs[t][l], o_ref, (t, l))
 
     fps = {l: FusedPlanner(cfg.policy(l), count=False) for l in range(1, LAYERS)}
     for t in range(STEPS):
@@ -128,7 +161,8 @@ def test_refresh_fused_matches_planner_loop(index):
 
 def test_replay_of_recorded_lists():
     """replay: the masked + statistics decode over the lists recorded by refresh_fused gives that
-    run's outputs (split count may differ: within 2e-3 relative)."""
+    run's outputs (split count may differ: within 2e-3 relative) and exact attention over those
+    lists (the oracle)."""
     ks, vs, qs, _ = _data(33)
     cfg = A.KvskipConfig(mode="refresh_fused", count=False, record=True)
     outs, _ = _drive(cfg, ks, vs, qs)
@@ -137,9 +171,13 @@ def test_replay_of_recorded_lists():
     cfg_r = A.KvskipConfig(mode="replay", count=False, plans=plans)
     outs_r, _ = _drive(cfg_r, ks, vs, qs)
     for t in range(STEPS):
+        n = T0 + t
         for l in range(LAYERS):
             a, b = outs[t][l].float(), outs_r[t][l].float()
             assert ((a - b).norm() / a.norm()).item() <= 2e-3, (t, l)
+            keep = cfg.plans[l][t].cpu() if l in cfg.plans else None
+            ref, _ = O.decode(qs[l][t][:, :, 0].cpu(), ks[l][:, :, :n].cpu(), vs[l][:, :, :n].cpu(), SCALE, keep=keep)
+            rel_ok(outs_r[t][l], ref, (t, l))
 
 
 def test_counters():
