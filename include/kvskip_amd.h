@@ -279,14 +279,43 @@ int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, i
 int kvskip_token_index(const int32_t* ids, int64_t ids_stride, int32_t B, int32_t T, uint8_t* idx,
                        int32_t NBC, const int32_t* seq_lens, void* stream);
 
+/* GQA-union block selection from per-block statistics, on the device. Replaces the torch steps of
+ * the reference's two-pass V-skip between its passes: select_blocks (kernels/kvskip.py:130-147),
+ * the kept-set normaliser and per-block scales (kernels/kvskip.py:168-172) and make_plan's list
+ * (kernels/kvskip.py:79-85). Per query head the block log-weights x = blk_max + log blk_sum
+ * (-inf where blk_sum is 0); rule 0 ("tau") keeps blocks with softmax weight >= value, rule 1
+ * ("topp") the fewest blocks whose weights reach value (ties at the cut kept); a KV head keeps the
+ * union over its G query heads plus block 0 and the `local` newest. Every output is optional. */
+typedef struct kvskip_select_args {
+  const float* blk_max;        /* [B, Hq, nb] */
+  const float* blk_sum;        /* [B, Hq, nb] */
+  int32_t B, Hq, Hkv, nb;      /* G = Hq / Hkv <= 8, nb <= 4096 */
+  int32_t rule;                /* 0 tau, 1 topp */
+  float value;                 /* tau, or the top-p level */
+  int32_t local;
+  uint8_t* keep;               /* out [B, Hkv, nb]: 1 kept, 0 not */
+  int32_t* block_idx;          /* out [B, Hkv, nb]: kept blocks ascending, then the others ascending */
+  int32_t* block_cnt;          /* out [B, Hkv] (with block_idx) */
+  float* blk_scale;            /* out [B, Hkv, nb, G]: exp(blk_max - lse over the kept blocks), 0 off the set */
+} kvskip_select_args;
+
+int kvskip_select(const kvskip_select_args* s, void* stream);
+
+/* The kept-first block list of a keep mask keep [B, Hkv, nb] (uint8, nonzero = kept): block_idx
+ * [B, Hkv, nb] the kept blocks ascending then the others ascending, block_cnt [B, Hkv]. The device
+ * form of make_plan (kernels/kvskip.py:79-85, a stable argsort of ~keep). */
+int kvskip_block_list(const uint8_t* keep, int32_t B, int32_t Hkv, int32_t nb, int32_t* block_idx,
+                      int32_t* block_cnt, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* kvskip_last_error(void);
 
 /* Library version string. */
 const char* kvskip_version(void);
 
-/* sizeof of the argument blocks (0: kvskip_attn_args, 1: kvskip_plan_args, 2: kvskip_update_args),
- * -1 otherwise: lets a binding check its struct layout. Library utility, no reference counterpart. */
+/* sizeof of the argument blocks (0: kvskip_attn_args, 1: kvskip_plan_args, 2: kvskip_update_args,
+ * 3: kvskip_select_args), -1 otherwise: lets a binding check its struct layout. Library utility, no
+ * reference counterpart. */
 int kvskip_struct_size(int which);
 
 #ifdef __cplusplus

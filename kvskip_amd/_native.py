@@ -65,6 +65,16 @@ class UpdateArgs(ctypes.Structure):
     ]
 
 
+class SelectArgs(ctypes.Structure):
+    """kvskip_select_args."""
+    _fields_ = [
+        ("blk_max", c_void_p), ("blk_sum", c_void_p),
+        ("B", c_int32), ("Hq", c_int32), ("Hkv", c_int32), ("nb", c_int32),
+        ("rule", c_int32), ("value", c_float), ("local", c_int32),
+        ("keep", c_void_p), ("block_idx", c_void_p), ("block_cnt", c_void_p), ("blk_scale", c_void_p),
+    ]
+
+
 # Every entry point of include/kvskip_amd.h with its argument types.
 SIGNATURES = {
     "kvskip_decode": ([POINTER(AttnArgs), c_int, c_int, c_void_p], c_int),
@@ -84,6 +94,8 @@ SIGNATURES = {
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p], c_int),
     "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),
+    "kvskip_select": ([POINTER(SelectArgs), c_void_p], c_int),
+    "kvskip_block_list": ([c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p], c_int),
     "kvskip_last_error": ([], c_char_p),
     "kvskip_version": ([], c_char_p),
     "kvskip_struct_size": ([c_int], c_int),

@@ -127,6 +127,7 @@ int kvskip_struct_size(int which) {
     case 0: return static_cast<int>(sizeof(kvskip_attn_args));
     case 1: return static_cast<int>(sizeof(kvskip_plan_args));
     case 2: return static_cast<int>(sizeof(kvskip_update_args));
+    case 3: return static_cast<int>(sizeof(kvskip_select_args));
     default: return -1;
   }
 }
@@ -411,6 +412,29 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
   if (u != nullptr && (rc = check_update(u)) != KVSKIP_OK) return rc;
   return launched(kvs::launch_planned_split(p, *pl, u, a->D, static_cast<hipStream_t>(stream)),
                   "kvskip_decode_splits_planned");
+}
+
+int kvskip_select(const kvskip_select_args* s, void* stream) {
+  if (s == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
+  if (s->blk_max == nullptr || s->blk_sum == nullptr) return fail(KVSKIP_E_INVALID, "select: blk_max / blk_sum");
+  if (s->B < 1 || s->Hq < 1 || s->Hkv < 1 || s->nb < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
+  if (s->Hq % s->Hkv != 0) return fail(KVSKIP_E_INVALID, "Hq must be a multiple of Hkv");
+  if (s->Hq / s->Hkv > 8) return fail(KVSKIP_E_UNSUPPORTED, "select: G <= 8 (G=%d)", s->Hq / s->Hkv);
+  if (s->nb > kvs::planner_max_blocks(1))
+    return fail(KVSKIP_E_UNSUPPORTED, "select: at most %d blocks (nb=%d)", kvs::planner_max_blocks(1), s->nb);
+  if (s->rule != 0 && s->rule != 1) return fail(KVSKIP_E_INVALID, "rule must be tau or topp");
+  if (!(s->value > 0.f) || s->local < 0) return fail(KVSKIP_E_INVALID, "select: value > 0, local >= 0");
+  if (s->block_idx != nullptr && s->block_cnt == nullptr) return fail(KVSKIP_E_INVALID, "block_cnt is required with block_idx");
+  return launched(kvs::launch_select(*s, static_cast<hipStream_t>(stream)), "kvskip_select");
+}
+
+int kvskip_block_list(const uint8_t* keep, int32_t B, int32_t Hkv, int32_t nb, int32_t* block_idx,
+                      int32_t* block_cnt, void* stream) {
+  if (keep == nullptr || block_idx == nullptr || block_cnt == nullptr)
+    return fail(KVSKIP_E_INVALID, "block_list: null tensor");
+  if (B < 1 || Hkv < 1 || nb < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
+  return launched(kvs::launch_block_list(keep, B, Hkv, nb, block_idx, block_cnt, static_cast<hipStream_t>(stream)),
+                  "kvskip_block_list");
 }
 
 int kvskip_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int32_t B, int32_t Hkv, int32_t T,

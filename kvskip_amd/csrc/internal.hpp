@@ -89,6 +89,11 @@ hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t 
 hipError_t launch_token_index(const int32_t* ids, int64_t ids_stride, int B, int T, uint8_t* idx, int NBC,
                               const int32_t* seq_lens, hipStream_t s);
 
+// Block selection (select.hip): the GQA-union rule, list and scales; the list of a keep mask.
+hipError_t launch_select(const kvskip_select_args& a, hipStream_t s);
+hipError_t launch_block_list(const uint8_t* keep, int B, int Hkv, int nb, int32_t* block_idx, int32_t* block_cnt,
+                             hipStream_t s);
+
 // Largest block count the planner kernels hold in LDS for a group of G query heads.
 int planner_max_blocks(int G);
 int64_t plan_part_floats(int B, int Hq, int Hkv, int NBC);

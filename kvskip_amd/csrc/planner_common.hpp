@@ -200,6 +200,29 @@ __device__ __forceinline__ uint32_t fkey(float y) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Top-p cut of one query head held across a wavefront (lane: blocks lane + 64 r, r < R; slots r >= RU
+// hold no block, RU uniform): the largest key theta of y = x - lse whose upper set {key >= theta}
+// holds >= level of the mass w = exp(y), i.e. the fewest blocks reaching level with ties at the cut
+// kept (kernels/kvskip.py:140-143 keeps the blocks whose heavier blocks hold < level). Exact: one
+// bit of theta per step, 32 steps, the weights computed once. Uniform result.
+template <int R>
+__device__ __forceinline__ uint32_t topp_theta(const uint32_t (&key)[R], const float (&w)[R], int RU, float level) {
+  uint32_t theta = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = theta | (1u << bit);
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; r += 2) {
+      if (r < RU) {
+        acc0 += key[r] >= cand ? w[r] : 0.f;
+        if (r + 1 < R) acc1 += key[r + 1] >= cand ? w[r + 1] : 0.f;
+      }
+    }
+    if (wave_sum(acc0 + acc1) >= level) theta = cand;
+  }
+  return theta;
+}
+
 // Update of (b, KV head h): src/kvskip_attn.py:386-391 (_calib_learn 302-320, _refresh_state
 // 182-199, _attended_lse 282-288) on the device, as kernels/kvskip_planner.cu:229-305.
 // Wavefront w < NWV takes query heads g = w + NWV j of the group (HPW = ceil(G / NWV) per
@@ -294,21 +317,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
         w[r] = r < RU ? __expf(y) : 0.f;
         key[r] = fkey(y);
       }
-      // Largest key theta of y = x - lse whose upper set {key >= theta} holds >= level of the
-      // mass: the fewest blocks reaching level (ties at the cut kept); exact, 32 bit steps.
-      uint32_t theta = 0;
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = theta | (1u << bit);
-        float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; r += 2) {
-          if (r < RU) {
-            acc0 += key[r] >= cand ? w[r] : 0.f;
-            if (r + 1 < R) acc1 += key[r + 1] >= cand ? w[r + 1] : 0.f;
-          }
-        }
-        if (wave_sum(acc0 + acc1) >= p.level) theta = cand;
-      }
+      const uint32_t theta = topp_theta<R>(key, w, RU, p.level);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t m = __ballot(lane + WAVE * r < nb && key[r] >= theta);

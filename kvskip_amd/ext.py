@@ -658,3 +658,54 @@ def token_index(ids, T, NBC, out=None, seq_lens=None):
         _native.check(_native.lib().kvskip_token_index(ids.data_ptr(), ids.stride(0), B, int(T), out.data_ptr(), NBC,
                                                        _seq_lens_ptr(seq_lens, B), _stream(ids.device)))
     return out
+
+
+_RULES = {"tau": 0, "topp": 1}
+
+
+def select(blk_max, blk_sum, Hkv, rule, value, local=2, keep=None, block_idx=None, block_cnt=None, blk_scale=None):
+    """GQA-union block selection on the device (kvskip_select; not in kvskip_ext): from per-block
+    statistics [B, Hq, nb] fp32, rule "tau" (weight >= value) or "topp" (fewest blocks reaching value)
+    per query head, the union over each KV head's group plus block 0 and the `local` newest blocks.
+    Fills whichever outputs are given: keep uint8 [B, Hkv, nb], block_idx / block_cnt int32 ([B, Hkv, nb]
+    kept first ascending, [B, Hkv]) and blk_scale fp32 [B, Hkv, nb, G] (exp(blk_max - lse over the kept
+    blocks), 0 off the set)."""
+    _require(rule in _RULES, "rule must be tau or topp")
+    check_f32(blk_max, "blk_max")
+    check_f32(blk_sum, "blk_sum")
+    _require(blk_max.dim() == 3 and blk_sum.shape == blk_max.shape, "blk_max / blk_sum: [B, Hq, nb]")
+    B, Hq, nb = blk_max.shape
+    _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    G = Hq // Hkv
+    a = _native.SelectArgs()
+    a.blk_max, a.blk_sum = blk_max.data_ptr(), blk_sum.data_ptr()
+    a.B, a.Hq, a.Hkv, a.nb = B, Hq, Hkv, nb
+    a.rule, a.value, a.local = _RULES[rule], float(value), int(local)
+    for t, shape, dtype, name in ((keep, (B, Hkv, nb), torch.uint8, "keep"), (block_idx, (B, Hkv, nb), torch.int32,
+                                  "block_idx"), (block_cnt, (B, Hkv), torch.int32, "block_cnt"),
+                                  (blk_scale, (B, Hkv, nb, G), torch.float32, "blk_scale")):
+        if t is not None:
+            _require(t.is_cuda and t.dtype == dtype and t.is_contiguous() and tuple(t.shape) == shape,
+                     f"{name}: contiguous {dtype} {list(shape)} on the device")
+            setattr(a, name, t.data_ptr())
+    _require(block_idx is None or block_cnt is not None, "block_cnt is required with block_idx")
+    dev = blk_max.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_select(ctypes.byref(a), _stream(dev)))
+
+
+def block_list(keep, block_idx, block_cnt):
+    """The kept-first block list of a keep mask [B, Hkv, nb] (bool or uint8) on the device
+    (kvskip_block_list; not in kvskip_ext): block_idx int32 [B, Hkv, nb] (kept blocks ascending, then
+    the others ascending), block_cnt int32 [B, Hkv]."""
+    _require(keep.is_cuda and keep.dtype in (torch.bool, torch.uint8) and keep.dim() == 3 and keep.is_contiguous(),
+             "keep: contiguous bool / uint8 [B, Hkv, nb] on the device")
+    B, Hkv, nb = keep.shape
+    _require(block_idx.dtype == torch.int32 and block_idx.is_contiguous() and tuple(block_idx.shape) == (B, Hkv, nb),
+             "block_idx: int32 [B, Hkv, nb]")
+    _require(block_cnt.dtype == torch.int32 and block_cnt.is_contiguous() and tuple(block_cnt.shape) == (B, Hkv),
+             "block_cnt: int32 [B, Hkv]")
+    dev = keep.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_block_list(keep.data_ptr(), B, Hkv, nb, block_idx.data_ptr(),
+                                                      block_cnt.data_ptr(), _stream(dev)))

@@ -1,14 +1,18 @@
-"""Python front-end of the kvskip_amd decode kernels: the public API of the reference's
-kernels/kvskip.py (kernels/kvskip.py:28-208) on MI355X.
+"""kvskip_amd's decode front-end: the Python functions a caller of the reference's
+kernels/kvskip.py uses (names, arguments, defaults and result dicts of kernels/kvskip.py:47-208),
+on the kvskip_amd operators. Block lists and block selection are made on the device
+(kvskip_block_list, kvskip_select): vskip_two_pass is the K pass, the selection and the V pass,
+with no host work in between. A host synchronisation happens only where a caller asks for a number
+on the host (sync=True: the longest list sizes the split count, and the kept fraction).
 
-    out = decode(q, k, v, scale)                         # dense
-    out = decode(q, k, v, scale, plan=make_plan(keep))   # skip blocks (neither K nor V read)
-    out = decode(q, k, v, scale, stats=True)             # dense + per-block max / sumexp
-    out = decode(q, k, v, scale, stats=True, load_v=False)  # stats only: reads K, not V
+    r = decode(q, k, v, scale)                              # every block
+    r = decode(q, k, v, scale, plan=make_plan(keep))        # the blocks keep [B, Hkv, nb] marks
+    r = decode(q, k, v, scale, stats=True)                  # + per-block blk_max / blk_sum
+    r = decode(q, k, v, scale, stats=True, load_v=False)    # statistics from K alone
+    out, lse = r["out"], r["lse"]
 
-q [B, Hq, D] or [B, Hq, 1, D]; k, v [B, Hkv, T, D] in any batch/head/token strides with D
-contiguous. Blocks are 64 tokens from position 0. Any G = Hq / Hkv in {1, 2, 4, 7, 8},
-D in {64, 128}.
+q is [B, Hq, D] or [B, Hq, 1, D]; k and v are [B, Hkv, T, D] views (D contiguous, other strides
+free); a block is 64 tokens from position 0; G = Hq / Hkv in {1, 2, 4, 7, 8}; D in {64, 128}.
 """
 
 from __future__ import annotations
@@ -18,17 +22,17 @@ from dataclasses import dataclass
 
 import torch
 
-from . import ext as _ext_mod
+from . import ext as _ops
 
 TILE = 64
 WG_PER_CU = 1          # attention workgroups (4 wavefronts each) per CU in the split heuristic
 
 
 def ext():
-    """The operator module (the reference JIT-builds its extension here; ours is prebuilt)."""
+    """The operator module, with the native library loaded (it raises if the library is missing)."""
     from . import _native
     _native.lib()
-    return _ext_mod
+    return _ops
 
 
 def num_sms() -> int:
@@ -36,23 +40,26 @@ def num_sms() -> int:
     return torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
 
 
+def _split_score(bh: int, splits: int, slots: int) -> float:
+    """How fully bh * splits workgroups use whole waves of `slots`, less 0.002 per split."""
+    waves = bh * splits / slots
+    return waves / math.ceil(waves) - 0.002 * splits
+
+
 def num_splits_for(bh: int, n_tiles: int, sms: int | None = None, max_splits: int = 256,
                    min_tiles: int = 4) -> int:
-    """Split count for B*Hkv work items of n_tiles blocks each (kernels/kvskip.py:51-67).
-
-    Same rule as the reference -- best wave efficiency over the resident workgroup slots, lightly
-    preferring fewer splits, at least `min_tiles` blocks per split (one per wavefront of a
-    workgroup) -- with the slots counted as CUs x WG_PER_CU."""
+    """Split count for bh = B * Hkv work items of n_tiles blocks each. The rule of
+    kernels/kvskip.py:51-67: the best wave efficiency over the resident workgroup slots (here CUs x
+    WG_PER_CU), 0.002 per split against more splits, every split keeping >= min_tiles blocks; the
+    smallest count wins ties."""
     slots = (sms or num_sms()) * WG_PER_CU
-    best, best_score = 1, -1.0
-    for s in range(1, max_splits + 1):
-        if s > 1 and math.ceil(n_tiles / s) < min_tiles:
-            break
-        waves = bh * s / slots
-        eff = waves / math.ceil(waves)
-        score = eff - 0.002 * s
-        if score > best_score + 1e-9:
-            best, best_score = s, score
+    most = 1                                       # ceil(n / s) only falls as s grows
+    while most < max_splits and math.ceil(n_tiles / (most + 1)) >= min_tiles:
+        most += 1
+    best = 1
+    for s in range(2, most + 1):
+        if _split_score(bh, s, slots) > _split_score(bh, best, slots) + 1e-9:
+            best = s
     return best
 
 
@@ -65,147 +72,153 @@ def ragged_splits(B: int, Hkv: int, nb_max: int, sms: int | None = None) -> int:
 
 @dataclass
 class Plan:
-    """Kept-block list for the masked kernel (kernels/kvskip.py:70-76)."""
-    block_idx: torch.Tensor   # int32 [B, Hkv, nb], kept blocks first, ascending
+    """Block lists of the masked pass (the fields of kernels/kvskip.py:70-76)."""
+    block_idx: torch.Tensor   # int32 [B, Hkv, nb]: listed blocks first, ascending
     block_cnt: torch.Tensor   # int32 [B, Hkv]
-    max_cnt: int              # max kept blocks over (b, kv head), sizes the split count
+    max_cnt: int              # longest list (sizes the split count); nb when not read back
     nb: int
 
 
+def _lists(B: int, Hkv: int, nb: int, device):
+    return (torch.empty(B, Hkv, nb, dtype=torch.int32, device=device),
+            torch.empty(B, Hkv, dtype=torch.int32, device=device))
+
+
 def make_plan(keep: torch.Tensor, sync: bool = True) -> Plan:
-    """keep: bool [B, Hkv, nb] -> Plan (kernels/kvskip.py:79-85). With sync=True one host sync
-    sizes the split count by the largest kept list; sync=False sizes it by nb."""
-    cnt = keep.sum(-1, dtype=torch.int32)
-    order = torch.argsort((~keep).to(torch.int8), dim=-1, stable=True).to(torch.int32)
-    return Plan(order.contiguous(), cnt.contiguous(), int(cnt.max()) if sync else keep.shape[-1], keep.shape[-1])
+    """Lists of the blocks keep [B, Hkv, nb] (bool) marks, built on the device. sync=True reads the
+    longest list back (one host synchronisation) so the split count fits it; sync=False sizes the
+    split count by nb (kernels/kvskip.py:79-85)."""
+    B, Hkv, nb = keep.shape
+    idx, cnt = _lists(B, Hkv, nb, keep.device)
+    ext().block_list(keep.contiguous(), idx, cnt)
+    return Plan(idx, cnt, int(cnt.max()) if sync else nb, nb)
+
+
+def _paged(block_table, T) -> dict:
+    return {} if block_table is None else {"block_table": block_table, "T": int(T)}
+
+
+def _as_bhd(q: torch.Tensor) -> torch.Tensor:
+    return q[:, :, 0] if q.dim() == 4 else q
 
 
 def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = False, load_v: bool = True,
            num_splits: int | None = None, stages: int = 2, out_f32: bool = False, write_p: bool = False,
            seq_lens: torch.Tensor | None = None, block_table: torch.Tensor | None = None,
            T: int | None = None) -> dict:
-    """Decode attention for one layer (kernels/kvskip.py:88-113). Returns dict(out [B, Hq, D] bf16,
-    lse [B, Hq] fp32, blk_max / blk_sum [B, Hq, nb] fp32 (stats), out_f32 (if asked), p (write_p:
-    fp16 [B, Hq, nb*64] = exp(s - blk_max))). Not in the reference: seq_lens (int32 [B] on the
-    device): a ragged batch over views of capacity T, with the split budget shared by the batch;
-    block_table (int32 [B, >= ceil(T / 64)]) with T: k, v are page pools [num_pages, Hkv, 64, D]."""
-    if q.dim() == 4:
-        q = q.squeeze(2)
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
-    nb = math.ceil(T / TILE)
-    n_items = nb if plan is None else plan.max_cnt
+    """Decode attention of one layer (kernels/kvskip.py:88-113). Returns a dict with out [B, Hq, D]
+    bf16 (None with load_v=False), lse [B, Hq] fp32, num_splits, and as asked blk_max / blk_sum
+    [B, Hq, nb] fp32, out_f32, p (fp16 [B, Hq, nb*64] = exp(s - blk_max)).
+    Not in the reference: seq_lens (int32 [B] on the device) makes a ragged batch over views of
+    capacity T, the split budget shared by the batch; block_table (int32 [B, >= ceil(T / 64)]) with T
+    makes k, v page pools [num_pages, Hkv, 64, D]."""
+    q = _as_bhd(q)
+    B, Hkv = q.shape[0], k.shape[1]
+    tokens = k.shape[2] if block_table is None else int(T)
+    nb = math.ceil(tokens / TILE)
     if num_splits is None:
-        num_splits = num_splits_for(B * Hkv, n_items) if seq_lens is None else ragged_splits(B, Hkv, n_items)
-    paged = {} if block_table is None else dict(block_table=block_table, T=T)
-    res = ext().decode(q, k, v, float(scale), None if plan is None else plan.block_idx,
-                       None if plan is None else plan.block_cnt, stats, load_v, int(num_splits), int(stages),
-                       out_f32, write_p, seq_lens, **paged)
-    out, lse, bmax, bsum, o32, pbuf = res
-    d = {"out": out if load_v else None, "lse": lse, "num_splits": num_splits}
-    if stats:
-        d["blk_max"], d["blk_sum"] = bmax, bsum
+        items = nb if plan is None else plan.max_cnt
+        num_splits = ragged_splits(B, Hkv, items) if seq_lens is not None else num_splits_for(B * Hkv, items)
+    lists = (None, None) if plan is None else (plan.block_idx, plan.block_cnt)
+    out, lse, bmax, bsum, o32, p = ext().decode(q, k, v, float(scale), *lists, stats, load_v, int(num_splits),
+                                                int(stages), out_f32, write_p, seq_lens, **_paged(block_table, T))
+    res = {"out": out, "lse": lse, "num_splits": num_splits}
+    extra = {"blk_max": bmax, "blk_sum": bsum} if stats else {}
     if out_f32:
-        d["out_f32"] = o32
+        extra["out_f32"] = o32
     if write_p:
-        d["p"] = pbuf
-    return d
+        extra["p"] = p
+    res.update(extra)
+    return res
 
 
 def block_weights(blk_max: torch.Tensor, blk_sum: torch.Tensor) -> torch.Tensor:
-    """Per-block softmax mass [B, Hq, nb] from the stats outputs (kernels/kvskip.py:116-119)."""
-    logw = blk_max + torch.log(blk_sum)
-    return torch.softmax(logw, dim=-1)
+    """Each block's share of its query head's softmax mass [B, Hq, nb], from the statistics
+    (kernels/kvskip.py:116-119)."""
+    return torch.softmax(blk_max + blk_sum.log(), dim=-1)
 
 
 def always_keep(nb: int, local: int, device) -> torch.Tensor:
-    """Blocks every sparse mode reads: the sink block and the `local` newest blocks."""
-    a = torch.zeros(nb, dtype=torch.bool, device=device)
-    a[0] = True
-    if local > 0:
-        a[-local:] = True
-    return a
+    """Blocks every sparse mode reads (kernels/kvskip.py:122-127): block 0 and the `local` newest
+    (none for local = 0)."""
+    pos = torch.arange(nb, device=device)
+    return (pos == 0) | (pos >= nb - local)
 
 
 def select_blocks(logw: torch.Tensor, G: int, rule: str, value: float, local: int = 2) -> torch.Tensor:
-    """GQA-union block selection from per-head block log-weights [B, Hq, nb] (kernels/kvskip.py:130-147).
-
-    rule "tau": keep a block if any head of the group has weight >= value;
-    rule "topp": keep the fewest blocks holding >= value of each head's mass (union over heads).
-    Returns keep [B, Hkv, nb] bool (sink + `local` newest blocks always kept)."""
+    """GQA-union selection from block log-weights [B, Hq, nb] (kernels/kvskip.py:130-147), on the
+    device: "tau" keeps a block if some head of the group gives it weight >= value, "topp" keeps per
+    head the fewest blocks holding >= value of its mass (ties at the cut kept) and unites the group;
+    block 0 and the `local` newest always. Returns keep [B, Hkv, nb] bool."""
     B, Hq, nb = logw.shape
-    W = torch.softmax(logw, dim=-1)
-    if rule == "tau":
-        keep_h = W >= value
-    elif rule == "topp":
-        ws, order = W.sort(-1, descending=True)
-        take = (ws.cumsum(-1) - ws) < value
-        keep_h = torch.zeros_like(take).scatter(-1, order, take)
-    else:
-        raise ValueError(rule)
-    keep = keep_h.view(B, Hq // G, G, nb).any(2)
-    return keep | always_keep(nb, local, logw.device)
+    keep = torch.empty(B, Hq // G, nb, dtype=torch.uint8, device=logw.device)
+    lw = logw.float().contiguous()
+    ext().select(lw, torch.ones_like(lw), Hq // G, rule, value, local, keep=keep)
+    return keep.view(torch.bool)
 
 
 def pv(P, v, blk_scale, plan: Plan, num_splits: int | None = None, out_f32: bool = False,
        block_table: torch.Tensor | None = None, T: int | None = None):
-    """Two-pass V-skip pass 2 (kernels/kvskip.py:150-154); block_table, T: v is a page pool."""
-    B, Hkv = P.shape[0], v.shape[1]
+    """Two-pass V-skip pass 2 over a plan's lists (kernels/kvskip.py:150-154): [out, out_f32 or None].
+    block_table, T (not in the reference): v is a page pool."""
     if num_splits is None:
-        num_splits = num_splits_for(B * Hkv, plan.max_cnt)
-    paged = {} if block_table is None else dict(block_table=block_table, T=T)
-    return ext().pv(P, v, blk_scale, plan.block_idx, plan.block_cnt, int(num_splits), out_f32, **paged)
+        num_splits = num_splits_for(P.shape[0] * v.shape[1], plan.max_cnt)
+    return ext().pv(P, v, blk_scale, plan.block_idx, plan.block_cnt, int(num_splits), out_f32,
+                    **_paged(block_table, T))
 
 
 def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.99, local: int = 2,
                    sync: bool = True, out_f32: bool = False, block_table: torch.Tensor | None = None,
                    T: int | None = None) -> dict:
-    """Two-pass V-skip (kernels/kvskip.py:157-179): pass 1 reads all of K once and writes block stats
-    and P (fp16); the GQA-union selection picks blocks; pass 2 reads P and V of the kept blocks only.
-    block_table, T (not in the reference): k, v are page pools of a paged cache."""
-    if q.dim() == 4:
-        q = q.squeeze(2)
-    B, Hq, D = q.shape
+    """Two-pass V-skip (kernels/kvskip.py:157-179). Pass 1 reads K once, writing the block statistics
+    and P; the device selection (kvskip_select) turns the statistics into the kept set, its lists and
+    the per-block scales exp(blk_max - lse over the kept set); pass 2 reads P and V of the kept blocks.
+    Returns out, keep [B, Hkv, nb] bool and, with sync=True, kept_frac (that read-back also sizes pass
+    2's split count by the longest list). block_table, T (not in the reference): page pools."""
+    q = _as_bhd(q)
+    B, Hq = q.shape[:2]
     Hkv = k.shape[1]
-    G = Hq // Hkv
-    paged = {} if block_table is None else dict(block_table=block_table, T=T)
-    r1 = decode(q, k, v, scale, stats=True, load_v=False, write_p=True, **paged)
-    logw = r1["blk_max"] + torch.log(r1["blk_sum"])                    # [B, Hq, nb]
-    keep = select_blocks(logw, G, rule, value, local)                   # [B, Hkv, nb]
-    keep_h = keep.repeat_interleave(G, dim=1)                           # [B, Hq, nb]
-    lse_kept = logw.masked_fill(~keep_h, float("-inf")).logsumexp(-1, keepdim=True)
-    scale_b = torch.exp(r1["blk_max"] - lse_kept).masked_fill(~keep_h, 0.0)
-    scale_b = scale_b.view(B, Hkv, G, -1).transpose(2, 3).contiguous()  # [B, Hkv, nb, G]
-    plan = make_plan(keep, sync=sync)
-    out, o32 = pv(r1["p"], v, scale_b, plan, out_f32=out_f32, **paged)
-    d = {"out": out, "keep": keep, "kept_frac": keep.float().mean().item() if sync else None}
+    first = decode(q, k, v, scale, stats=True, load_v=False, write_p=True, **_paged(block_table, T))
+    nb = first["blk_max"].shape[-1]
+    dev = q.device
+    keep = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=dev)
+    idx, cnt = _lists(B, Hkv, nb, dev)
+    scales = torch.empty(B, Hkv, nb, Hq // Hkv, dtype=torch.float32, device=dev)
+    ext().select(first["blk_max"], first["blk_sum"], Hkv, rule, value, local, keep=keep, block_idx=idx,
+                 block_cnt=cnt, blk_scale=scales)
+    frac = None
+    longest = nb
+    if sync:
+        longest, kept = torch.stack([cnt.max(), cnt.sum()]).tolist()
+        frac = kept / (B * Hkv * nb)
+    out, o32 = pv(first["p"], v, scales, Plan(idx, cnt, int(longest), nb), out_f32=out_f32,
+                  block_table=block_table, T=T)
+    res = {"out": out, "keep": keep.view(torch.bool), "kept_frac": frac}
     if out_f32:
-        d["out_f32"] = o32
-    return d
+        res["out_f32"] = o32
+    return res
 
 
 def vskip_one_pass(q, k, v, scale: float, tau: float = 1e-4, local: int = 2, num_splits: int | None = None,
                    out_f32: bool = False, count: bool = False, lse_prev: torch.Tensor | None = None,
                    sync: bool = True, block_table: torch.Tensor | None = None, T: int | None = None) -> dict:
-    """Single-pass V-skip (kernels/kvskip.py:182-208): K read once, V of a block read only if some
-    head of the group has estimated weight >= tau there (normaliser: lse_prev, else the sink
-    block's log-sum-exp, a lower bound). With count=True "v_tiles" [B, Hkv] counts V blocks read.
-    block_table, T (not in the reference): k, v are page pools of a paged cache."""
-    if q.dim() == 4:
-        q = q.squeeze(2)
-    B, Hq, D = q.shape
-    Hkv, T = k.shape[1], (k.shape[2] if block_table is None else int(T))
-    paged = {} if block_table is None else dict(block_table=block_table, T=T)
-    nb = math.ceil(T / TILE)
+    """Single-pass V-skip (kernels/kvskip.py:182-208): K read once; a block's V is read only if some
+    head of the group estimates its weight >= tau, against lse_prev (e.g. the previous step's "lse")
+    or else the sink block's log-sum-exp, a lower bound of the normaliser. count=True adds v_tiles
+    [B, Hkv] (V blocks read) and, with sync=True, kept_frac. block_table, T (not in the reference):
+    page pools."""
+    q = _as_bhd(q)
+    B, Hkv = q.shape[0], k.shape[1]
+    nb = math.ceil((k.shape[2] if block_table is None else int(T)) / TILE)
     if num_splits is None:
         num_splits = num_splits_for(B * Hkv, nb)
-    out, lse, o32, cnt = ext().vskip1(q, k, v, float(scale), float(tau), int(local), int(num_splits),
-                                      out_f32, count, lse_prev, **paged)
-    d = {"out": out, "lse": lse, "num_splits": num_splits}
+    out, lse, o32, vt = ext().vskip1(q, k, v, float(scale), float(tau), int(local), int(num_splits), out_f32, count,
+                                     lse_prev, **_paged(block_table, T))
+    res = {"out": out, "lse": lse, "num_splits": num_splits}
     if out_f32:
-        d["out_f32"] = o32
+        res["out_f32"] = o32
     if count:
-        d["v_tiles"] = cnt
+        res["v_tiles"] = vt
         if sync:
-            d["kept_frac"] = (cnt.sum() / (B * Hkv * nb)).item()
-    return d
+            res["kept_frac"] = vt.sum().item() / (B * Hkv * nb)
+    return res

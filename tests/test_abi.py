@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from kvskip_amd import _native, ext
-from kvskip_amd._native import AttnArgs, PlanArgs, UpdateArgs
+from kvskip_amd._native import AttnArgs, PlanArgs, SelectArgs, UpdateArgs
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "kvskip_amd.h"
 
@@ -35,7 +35,8 @@ def test_struct_layouts():
     assert lib.kvskip_struct_size(0) == ctypes.sizeof(AttnArgs)
     assert lib.kvskip_struct_size(1) == ctypes.sizeof(PlanArgs)
     assert lib.kvskip_struct_size(2) == ctypes.sizeof(UpdateArgs)
-    assert lib.kvskip_struct_size(3) == -1
+    assert lib.kvskip_struct_size(3) == ctypes.sizeof(SelectArgs)
+    assert lib.kvskip_struct_size(4) == -1
 
 
 def _args(**kw):
@@ -121,3 +122,22 @@ def test_scratch_decode_validation():
     assert "the scratch holds 16777216" in lib.kvskip_last_error().decode()
     assert lib.kvskip_decode_scratch(ctypes.byref(_args(D=96)), 0, 1, None) == -2
     assert lib.kvskip_decode_scratch(None, 0, 1, None) == -1
+
+
+def test_select_validation():
+    """kvskip_select / kvskip_block_list refuse bad arguments before any device work."""
+    lib = _native.lib()
+    a = SelectArgs()
+    a.blk_max, a.blk_sum = 0x1000, 0x2000
+    a.B, a.Hq, a.Hkv, a.nb, a.rule, a.value, a.local = 1, 32, 8, 512, 1, 0.99, 2
+    for kw, code, msg in ((dict(rule=2), -1, "rule must be tau or topp"), (dict(Hq=30), -1, "multiple of Hkv"),
+                          (dict(Hq=72), -2, "G <= 8"), (dict(nb=5000), -2, "at most 4096 blocks"),
+                          (dict(value=0.0), -1, "value > 0"), (dict(blk_sum=0), -1, "blk_max / blk_sum"),
+                          (dict(block_idx=0x3000), -1, "block_cnt is required")):
+        b = SelectArgs.from_buffer_copy(a)
+        for k_, v_ in kw.items():
+            setattr(b, k_, v_)
+        assert lib.kvskip_select(ctypes.byref(b), None) == code, kw
+        assert msg in lib.kvskip_last_error().decode(), kw
+    assert lib.kvskip_block_list(0, 1, 1, 4, 0x1000, 0x2000, None) == -1
+    assert lib.kvskip_block_list(0x1000, 1, 0, 4, 0x1000, 0x2000, None) == -1
