@@ -310,7 +310,8 @@ def main():
                           "v_block_frac": v_blocks / (Hkv * nb3), "dense_us_per_op_median": us_d3,
                           "time_vs_dense": us_v / us_d3, "num_splits": S3}
     log(f"vskip1 cfg3: {us_v:.1f} us (dense {us_d3:.1f} us), V read {v_blocks / (Hkv * nb3):.3f}")
-    del k3, v3
+    cfg3_cpu = None if args.no_cpu else (L3.q.cpu(), L3.k.cpu(), L3.v.cpu(), L3.scale, lp.cpu())
+    del k3, v3, L3
     torch.cuda.empty_cache()
 
     # ---- config 1 (latency-bound) and the read ceiling
@@ -340,6 +341,11 @@ def main():
                                                     steps=min(args.planner_steps, 64), revert=True,
                                                     tag="cfg4-focused")
         torch.cuda.empty_cache()
+        # the reference's operating point for the planner (README.md:100-105: batch 8 at 32k): config 4's
+        # loop with 8 sequences of T 32768
+        res["planner_b8"] = bench_planner(dev, layers=args.planner_layers, T0=32768, B=8,
+                                          steps=min(args.planner_steps, 64), tag="b8")
+        torch.cuda.empty_cache()
         # config 5: batch 16 of Qwen2.5-7B layers (28 / 4 heads, G 7), contexts log-uniform in
         # [4096, 65536], 28 layers, ragged split-K over the batch
         g5 = torch.Generator().manual_seed(5)
@@ -363,7 +369,8 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(L.q.cpu(), L.k.cpu(), L.v.cpu(), L.scale, bytes_dense)
+        cpu = cpu_baseline((L.q.cpu(), L.k.cpu(), L.v.cpu(), L.scale, keep.cpu()), cfg3_cpu, bytes_dense, bytes_mask,
+                           res["vskip1_cfg3"]["bytes"])
 
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -381,40 +388,45 @@ def main():
 
 
 def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
-    """Two-pass V-skip on one layer (NCOPY KV copies): pass 1 (stats-only + fp16 P) and pass 2 (pv
-    over the kept blocks, top-p 0.99 GQA union) each timed as a graph-replayed region; the whole op
-    (torch selection and its host sync included) by per-call events."""
+    """Two-pass V-skip on one layer (NCOPY KV copies), top-p 0.99 GQA union: pass 1 (stats-only + fp16
+    P), the device selection (kvskip_select: kept set, lists, per-block scales) and pass 2 (pv over the
+    kept blocks) each timed as a graph-replayed region, and the whole op as the front-end runs it
+    without a host read-back (kvskip.vskip_two_pass(sync=False): pass 2 sized by nb), also replayed."""
     import torch
 
     B, Hq, D = q.shape
     Hkv, T = ks[0].shape[1], ks[0].shape[2]
     G, nb = Hq // Hkv, math.ceil(T / 64)
+    dev = q.device
     r1 = E.decode(q, ks[0], vs[0], scale, None, None, True, False, S1, 2, False, True)
-    logw = r1[2] + torch.log(r1[3])
-    keep = K.select_blocks(logw, G, "topp", 0.99, 2)
-    keep_h = keep.repeat_interleave(G, dim=1)
-    lse_kept = logw.masked_fill(~keep_h, float("-inf")).logsumexp(-1, keepdim=True)
-    scale_b = torch.exp(r1[2] - lse_kept).masked_fill(~keep_h, 0.0)
-    scale_b = scale_b.view(B, Hkv, G, -1).transpose(2, 3).contiguous()
-    plan = K.make_plan(keep)
-    S2 = K.num_splits_for(B * Hkv, plan.max_cnt)
+    keep = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=dev)
+    idx = torch.empty(B, Hkv, nb, dtype=torch.int32, device=dev)
+    cnt = torch.empty(B, Hkv, dtype=torch.int32, device=dev)
+    scales = torch.empty(B, Hkv, nb, G, dtype=torch.float32, device=dev)
+
+    def select(i):
+        E.select(r1[2], r1[3], Hkv, "topp", 0.99, 2, keep=keep, block_idx=idx, block_cnt=cnt, blk_scale=scales)
+
+    select(0)
+    kept = int(cnt.sum())
+    S2 = K.num_splits_for(B * Hkv, int(cnt.max()))
     P1 = r1[5]
-    kept = int(plan.block_cnt.sum())
     t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], scale, None, None, True, False, S1, 2, False, True),
                          args.steps // 2, args.warmup)
-    t_p2 = events_region(lambda i: E.pv(P1, vs[i], scale_b, plan.block_idx, plan.block_cnt, S2, False),
-                         args.steps // 2, args.warmup)
-    ev = statistics.median(time_events(lambda i: K.vskip_two_pass(q, ks[i], vs[i], scale), args.events // 2,
-                                       NCOPY, flush))
+    t_sel = events_region(select, args.steps // 2, args.warmup)
+    t_p2 = events_region(lambda i: E.pv(P1, vs[i], scales, idx, cnt, S2, False), args.steps // 2, args.warmup)
+    t_op = events_region(lambda i: K.vskip_two_pass(q, ks[i], vs[i], scale, sync=False), args.steps // 2,
+                         args.warmup)
     bytes_p1 = B * Hkv * T * D * 2 + B * Hq * D * 2 + B * Hq * nb * 64 * 2 + 2 * B * Hq * nb * 4
     bytes_p2 = kept * 64 * D * 2 + kept * G * 64 * 2 + kept * G * 4 + kept * 4
-    out = {"kept_block_frac": kept / (B * Hkv * nb), "pass1_us": t_p1, "pass2_us": t_p2, "pass1_bytes": bytes_p1,
-           "pass2_bytes": bytes_p2, "pass1_GBs": bytes_p1 / t_p1 / 1e3, "pass2_GBs": bytes_p2 / t_p2 / 1e3,
-           "kernels_vs_dense": (t_p1 + t_p2) / us_dense, "num_splits_pass2": S2,
-           "op_us_event_median_incl_host_selection": ev}
-    log(f"{tag}: kept {kept / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), pass 2 "
-        f"{t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s), kernels x{(t_p1 + t_p2) / us_dense:.3f} of dense; whole op "
-        f"with torch selection + host sync {ev:.1f} us")
+    out = {"kept_block_frac": kept / (B * Hkv * nb), "pass1_us": t_p1, "select_us": t_sel, "pass2_us": t_p2,
+           "pass1_bytes": bytes_p1, "pass2_bytes": bytes_p2, "pass1_GBs": bytes_p1 / t_p1 / 1e3,
+           "pass2_GBs": bytes_p2 / t_p2 / 1e3, "kernels_vs_dense": (t_p1 + t_sel + t_p2) / us_dense,
+           "num_splits_pass2": S2, "op_us": t_op, "op_vs_dense": t_op / us_dense,
+           "op_vs_passes": t_op / (t_p1 + t_p2)}
+    log(f"{tag}: kept {kept / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), select "
+        f"{t_sel:.2f} us, pass 2 {t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s); whole op {t_op:.2f} us "
+        f"(x{t_op / us_dense:.3f} of dense, x{t_op / (t_p1 + t_p2):.3f} of the two passes)")
     return out
 
 
@@ -608,7 +620,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
     us_replay, n_replay = replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0) \
-        if ragged is None else (math.nan, 0)
+        if ragged is None and B == 1 else (math.nan, 0)
     out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
            "T0": T0 if ragged is None else list(ragged), "query_noise": noise, "query_revert": revert,
            "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)"
@@ -679,27 +691,75 @@ def replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0):
     return e0.elapsed_time(e1) * 1e3, (steps - w) * layers
 
 
-def cpu_baseline(q, k, v, scale, nbytes, budget_s=12.0):
-    """The reference-semantics PyTorch CPU path (fp32 einsum -> softmax -> einsum, oracle/attention.py
-    in fp32) on config 2's layer, all host threads, median over a bounded sample."""
+def _median_time(fn, reps, budget_s):
+    """Median seconds of fn() over up to `reps` calls after one warm-up call, within budget_s."""
+    fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < reps and (len(ts) < 5 or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), len(ts)
+
+
+def cpu_baseline(cfg2, cfg3, bytes_dense, bytes_mask, bytes_v1, budget_s=6.0):
+    """The reference-semantics PyTorch CPU path (the oracle's restatement in float32, all host
+    threads) on a bounded sample of each path, median of >= 5 calls after one warm-up: config 2's
+    dense layer-step, its masked + block-statistics step over the 35% list, config 3's single-pass
+    V-skip (the keep rule, then attention over the kept V), and one refresh_pre layer-step of the
+    planner (config 4's shape: plan, masked + statistics attention, update)."""
     import torch
 
+    from kvskip_amd import workloads as W
     from oracle import attention as O
+    from oracle import planner as OP
 
     n_threads = os.cpu_count() or 1
     torch.set_num_threads(n_threads)
-    O.decode(q, k, v, scale, dtype=torch.float32)            # warm-up
-    ts = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(ts) < 20:
-        t0 = time.perf_counter()
-        O.decode(q, k, v, scale, dtype=torch.float32)
-        ts.append(time.perf_counter() - t0)
-    med = statistics.median(ts)
-    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": n_threads, "kind": "port",
-            "us_per_layer_step": round(med * 1e6, 1),
-            "sample": f"{len(ts)} dense fp32 decode steps of config 2 (one layer, T 32768), median",
-            "cpu": _cpu_model()}
+    f32 = torch.float32
+    q, k, v, scale, keep = cfg2
+    paths = {}
+
+    def record(name, fn, nbytes, what):
+        med, n = _median_time(fn, 9, budget_s)
+        paths[name] = {"us_per_layer_step": round(med * 1e6, 1), "samples": n, "what": what}
+        if nbytes:
+            paths[name]["GBs"] = round(nbytes / med / 1e9, 2)
+        log(f"cpu {name}: {med * 1e3:.1f} ms per layer-step")
+
+    record("dense_cfg2", lambda: O.decode(q, k, v, scale, dtype=f32), bytes_dense,
+           "config 2 dense decode, fp32 einsum -> softmax -> einsum")
+    record("masked_stats_cfg2", lambda: (O.decode(q, k, v, scale, keep=keep, dtype=f32),
+                                         O.block_stats(q, k, scale, keep=keep, dtype=f32)), bytes_mask,
+           "config 2 masked decode over the 35% list + per-block statistics, fp32")
+    q3, k3, v3, scale3, lp3 = cfg3
+    record("vskip1_cfg3", lambda: O.vskip1(q3, k3, v3, scale3, 1e-4, 2, lse_prev=lp3.double(), dtype=f32), bytes_v1,
+           "config 3 single-pass V-skip (T 65536): block statistics, the keep rule, attention over the kept V, fp32")
+    del q3, k3, v3
+    run = W.planner_run(layers=1, T0=32768, steps=16, seed=4)
+    qp = W.QueryProcess(run, 0)
+    pol = OP.Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    box = {"T": 32769}
+    st, _ = OP.init(qp.next(), run.k[0][:, :, :32769], run.v[0][:, :, :32769], run.scale, pol)
+    ids = run.ids.numpy()
+
+    def planner_step():
+        box["T"] += 1
+        T = box["T"]
+        OP.step(st, qp.next(), run.k[0][:, :, :T], run.v[0][:, :, :T], pol,
+                idx=torch.from_numpy(OP.index_blocks(ids, T)), dtype=f32)
+
+    record("refresh_pre_step_cfg4", planner_step, None,
+           "one refresh_pre layer-step of config 4's shape after a dense first step: plan (centroid drift "
+           "estimate, decision, list; float64), masked + statistics attention (float32), update (top-p, references, "
+           "calibration; float64)")
+    d = paths["dense_cfg2"]
+    return {"value": d["GBs"], "unit": "GB/s", "cores": n_threads, "kind": "port",
+            "us_per_layer_step": d["us_per_layer_step"],
+            "sample": "config 2 dense decode steps (one layer, T 32768), median of >= 5 after one warm-up; "
+                      "the other paths in `paths`",
+            "cpu": _cpu_model(), "paths": paths}
 
 
 def _cpu_model():

@@ -24,6 +24,7 @@ run inside the next layer's split pass (planner.UpdateCarrier; flush() before re
 
 from __future__ import annotations
 
+import collections
 import math
 from dataclasses import dataclass, field
 
@@ -98,20 +99,21 @@ class KvskipConfig:
 KVSKIP = KvskipConfig()
 
 
-def _count(layer, key, value):
-    if not KVSKIP.count:
-        return
-    d = KVSKIP.log.setdefault(layer, {})
-    d[key] = d.get(key, 0.0) + value
+def _tally(layer, **amounts):
+    """Add device (or host) amounts to a layer's counters; nothing when counting is off."""
+    if KVSKIP.count:
+        counters = KVSKIP.log.setdefault(layer, {})
+        for name, amount in amounts.items():
+            counters[name] = counters.get(name, 0.0) + amount
 
 
 def log_totals() -> dict:
-    """Counters summed over layers, as floats (one host synchronisation per counter)."""
-    out = {}
-    for d in KVSKIP.log.values():
-        for key, val in d.items():
-            out[key] = out.get(key, 0.0) + float(val)
-    return out
+    """Every counter summed over the layers, as floats (src/kvskip_attn.py:155-163; reading a device
+    counter synchronises once)."""
+    acc = collections.Counter()
+    for counters in KVSKIP.log.values():
+        acc.update({name: float(amount) for name, amount in counters.items()})
+    return dict(acc)
 
 
 def _prefill(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
@@ -144,41 +146,66 @@ def _refresh(layer, q, k, v, scale):
     return out
 
 
+def _dense(layer, q, k, v, scale):
+    return K.decode(q, k, v, scale)["out"]
+
+
+def _two_pass(layer, q, k, v, scale):
+    return K.vskip_two_pass(q, k, v, scale, rule="topp", value=KVSKIP.level, local=KVSKIP.local, sync=False)["out"]
+
+
+def _one_pass(layer, q, k, v, scale, *, sink_bound=False):
+    """Single-pass V-skip; the layer's normaliser estimate is its previous step's log-sum-exp, or with
+    sink_bound the sink block's own bound (mode vskip1sink)."""
+    mem = KVSKIP.state.setdefault(layer, {})
+    res = K.vskip_one_pass(q, k, v, scale, tau=KVSKIP.tau, local=KVSKIP.local,
+                           lse_prev=None if sink_bound else mem.get("lse"), count=KVSKIP.count, sync=False)
+    mem["lse"] = res["lse"]
+    if KVSKIP.count:
+        vt = res["v_tiles"]
+        _tally(layer, v_tiles=vt.sum(), blocks_total=vt.numel() * math.ceil(k.shape[2] / BLOCK))
+    return res["out"]
+
+
+def _replay(layer, q, k, v, scale):
+    """Masked + statistics decode over the lists recorded for this layer, one per step in order."""
+    mem = KVSKIP.state.setdefault(layer, {"t": 0})
+    plan = KVSKIP.plans[layer][mem["t"]]
+    mem["t"] += 1
+    return K.decode(q, k, v, scale, plan=plan, stats=True)["out"]
+
+
+def _no_host_planner(layer, q, k, v, scale):
+    raise ValueError("mode 'refresh' (the host-side torch planner) is not provided; use 'refresh_fused'")
+
+
+# Decode-step handlers by KVSKIP.mode (src/kvskip_attn.py:487-513).
+MODES = {
+    "dense": _dense,
+    "vskip2": _two_pass,
+    "vskip1": _one_pass,
+    "vskip1sink": lambda layer, q, k, v, scale: _one_pass(layer, q, k, v, scale, sink_bound=True),
+    "refresh_fused": _refresh,
+    "refresh_pre": _refresh,
+    "replay": _replay,
+    "refresh": _no_host_planner,
+}
+
+
 def kvskip_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
     """AttentionInterface forward (src/kvskip_attn.py:481-515): query [B, Hq, Sq, D], key / value
-    [B, Hkv, T, D] (the cache's views); returns ([B, Sq, Hq, D], None)."""
+    [B, Hkv, T, D] (the cache's views); returns ([B, Sq, Hq, D], None). Prefill goes to SDPA; a
+    decode step to the handler of KVSKIP.mode, or dense for a layer in dense_layers."""
     if query.shape[2] != 1:
         return _prefill(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
     layer = module.layer_idx
-    if scaling is None:
-        scaling = query.shape[-1] ** -0.5
-    q = query[:, :, 0]
     mode = "dense" if layer in KVSKIP.dense_layers else KVSKIP.mode
-    if mode == "dense":
-        out = K.decode(q, key, value, scaling)["out"]
-    elif mode == "vskip2":
-        out = K.vskip_two_pass(q, key, value, scaling, rule="topp", value=KVSKIP.level, local=KVSKIP.local,
-                               sync=False)["out"]
-    elif mode in ("vskip1", "vskip1sink"):
-        st = KVSKIP.state.setdefault(layer, {})
-        r = K.vskip_one_pass(q, key, value, scaling, tau=KVSKIP.tau, local=KVSKIP.local,
-                             lse_prev=st.get("lse") if mode == "vskip1" else None, count=KVSKIP.count, sync=False)
-        st["lse"] = r["lse"]
-        out = r["out"]
-        if KVSKIP.count:
-            _count(layer, "v_tiles", r["v_tiles"].sum())
-            _count(layer, "blocks_total", r["v_tiles"].numel() * math.ceil(key.shape[2] / BLOCK))
-    elif mode in ("refresh_fused", "refresh_pre"):
-        out = _refresh(layer, q, key, value, scaling)
-    elif mode == "replay":
-        st = KVSKIP.state.setdefault(layer, {"t": 0})
-        out = K.decode(q, key, value, scaling, plan=KVSKIP.plans[layer][st["t"]], stats=True)["out"]
-        st["t"] += 1
-    elif mode == "refresh":
-        raise ValueError("mode 'refresh' (the host-side torch planner) is not provided; use 'refresh_fused'")
-    else:
+    handler = MODES.get(mode)
+    if handler is None:
         raise ValueError(f"unknown kvskip mode {mode!r}")
-    return out[:, None], None
+    scale = query.shape[-1] ** -0.5 if scaling is None else scaling
+    out = handler(layer, query[:, :, 0], key, value, scale)
+    return out.unsqueeze(1), None
 
 
 def register():

@@ -13,8 +13,12 @@
 // per-block statistics fall out of its own registers. The 4 states are merged once, in LDS,
 // at the end. With num_splits > 1 each workgroup writes its partial state and a second,
 // short kernel merges the splits (8 split classes x 32 dims per workgroup). A merge inside the
-// same kernel (last-arriving workgroup) needs device-scope fences, which on gfx950 write back
-// and invalidate the whole XCD L2 per workgroup: measured 2x slower at 2 workgroups per CU.
+// same kernel (last-arriving workgroup) costs more than that launch on gfx950: with device-scope
+// fences (an L2 write-back and invalidate per workgroup) 2x slower at 2 workgroups per CU; with
+// the partials stored and read at agent scope (no write-back) and a self-resetting ticket, +3.8 us
+// per op at config 2 (dense and masked alike, graph-replayed or eager): the pass's tail gains
+// three dependent memory round trips (store completion, ticket, partials), more than the
+// dispatch gap of the merge kernel.
 //
 // Pipeline per wavefront: K(j) and V(j) are in flight when block j starts; after QK(j) the K
 // loads of block j+1 are issued, after PV(j) its V loads. The last block is peeled off the

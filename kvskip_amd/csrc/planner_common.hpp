@@ -203,22 +203,82 @@ __device__ __forceinline__ uint32_t fkey(float y) {
 // Top-p cut of one query head held across a wavefront (lane: blocks lane + 64 r, r < R; slots r >= RU
 // hold no block, RU uniform): the largest key theta of y = x - lse whose upper set {key >= theta}
 // holds >= level of the mass w = exp(y), i.e. the fewest blocks reaching level with ties at the cut
-// kept (kernels/kvskip.py:140-143 keeps the blocks whose heavier blocks hold < level). Exact: one
-// bit of theta per step, 32 steps, the weights computed once. Uniform result.
+// kept (kernels/kvskip.py:140-143 keeps the blocks whose heavier blocks hold < level); theta = 0
+// (every block) when the whole mass falls short of level. Uniform result.
+//
+// Radix select over the key, 8 bits per pass: a pass sums the mass of the blocks still in play
+// (key above the bits decided so far equal to them) into 256 bins of the next 8 bits, and takes the
+// highest bin whose mass from the top reaches what is still needed. The mass is summed exactly in
+// 2^-60 fixed point (64-bit integer adds in LDS), so the passes agree with each other and the
+// result does not depend on the order of the adds. hist: this wavefront's 256 LDS bins, used by it
+// alone.
+__device__ __forceinline__ uint64_t fixmass(float w) {  // floor(w 2^60), w in [0, 16)
+  const float s = w * 0x1p28f;                        // exact
+  const uint32_t hi = static_cast<uint32_t>(s);
+  const float f = s - static_cast<float>(hi);         // exact fraction of s
+  return (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(f * 0x1p32f);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {  // 0 where the source lane is out of the row
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, 0xF, 0xF, true);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+__device__ __forceinline__ uint64_t lane64(uint64_t v, int src) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), src);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), src);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Inclusive scan over the lanes (lane 0 first) of a 64-bit sum: DPP shifts inside each 16-lane
+// row, then the totals of the rows before.
+__device__ __forceinline__ uint64_t wave_scan64(uint64_t v, int lane) {
+  v += dpp64<0x111>(v);  // row_shr:1
+  v += dpp64<0x112>(v);  // row_shr:2
+  v += dpp64<0x114>(v);  // row_shr:4
+  v += dpp64<0x118>(v);  // row_shr:8
+  const uint64_t t0 = lane64(v, 15), t1 = lane64(v, 31), t2 = lane64(v, 47);
+  const int row = lane >> 4;
+  return v + (row == 0 ? 0 : row == 1 ? t0 : row == 2 ? t0 + t1 : t0 + t1 + t2);
+}
+
 template <int R>
-__device__ __forceinline__ uint32_t topp_theta(const uint32_t (&key)[R], const float (&w)[R], int RU, float level) {
+__device__ __forceinline__ uint32_t topp_theta(const uint32_t (&key)[R], const float (&w)[R], int RU, float level,
+                                               uint64_t* hist) {
+  const int lane = threadIdx.x % WAVE;
+  uint64_t need = fixmass(level);  // mass still needed from the blocks in play
   uint32_t theta = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = theta | (1u << bit);
-    float acc0 = 0.f, acc1 = 0.f;
+  uint64_t* mine = hist + 4 * (WAVE - 1 - lane);  // lane L holds bins 4 (63 - L) .. + 3: lane 0 the top
 #pragma unroll
-    for (int r = 0; r < R; r += 2) {
-      if (r < RU) {
-        acc0 += key[r] >= cand ? w[r] : 0.f;
-        if (r + 1 < R) acc1 += key[r + 1] >= cand ? w[r + 1] : 0.f;
-      }
-    }
-    if (wave_sum(acc0 + acc1) >= level) theta = cand;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int sh = 24 - 8 * pass;
+    const uint32_t hm = pass == 0 ? 0u : ~0u << (sh + 8);  // bits decided so far
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mine[k] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r < RU && w[r] > 0.f && (key[r] & hm) == theta)
+        __hip_atomic_fetch_add(hist + ((key[r] >> sh) & 255u), fixmass(w[r]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WAVEFRONT);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    uint64_t h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h[k] = mine[k];
+    const uint64_t s3 = h[3], s2 = h[2] + s3, s1 = h[1] + s2, s0 = h[0] + s1;  // from bin k up, in the lane
+    const uint64_t incl = wave_scan64(s0, lane);  // mass of the bins >= 4 (63 - lane)
+    const uint64_t excl = incl - s0;
+    const uint64_t reach = __ballot(incl >= need);
+    if (reach == 0) return 0;                      // only in the first pass: the whole mass < level
+    const int L = __builtin_ctzll(reach);          // the lane of the highest bin that reaches need
+    const int k = excl + s3 >= need ? 3 : excl + s2 >= need ? 2 : excl + s1 >= need ? 1 : 0;
+    const uint64_t hk = k == 3 ? s3 : k == 2 ? s2 - s3 : k == 1 ? s1 - s2 : s0 - s1;
+    const uint64_t above = excl + (k == 3 ? s3 : k == 2 ? s2 : k == 1 ? s1 : s0) - hk;  // bins over the chosen
+    const int kL = __builtin_amdgcn_readlane(k, L);
+    need -= lane64(above, L);
+    theta |= static_cast<uint32_t>(4 * (WAVE - 1 - L) + kL) << sh;
   }
   return theta;
 }
@@ -243,6 +303,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
   const int64_t hrow0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;  // head g: hrow0 + g
   __shared__ uint64_t sKm[G][R];  // each query head's top-p blocks (lane bits of r)
   __shared__ float sReal[G];
+  __shared__ uint64_t sHist[NWV][256];  // each wavefront's top-p histogram
   uint8_t* keep = p.keep + bh * p.NBC;
   const uint8_t* ixp = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
   const bool tr = p.trig[bh] != 0;
@@ -317,7 +378,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
         w[r] = r < RU ? __expf(y) : 0.f;
         key[r] = fkey(y);
       }
-      const uint32_t theta = topp_theta<R>(key, w, RU, p.level);
+      const uint32_t theta = topp_theta<R>(key, w, RU, p.level, sHist[wave]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t m = __ballot(lane + WAVE * r < nb && key[r] >= theta);

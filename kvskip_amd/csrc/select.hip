@@ -10,11 +10,21 @@ namespace {
 constexpr int SW = 4;       // wavefronts per selection workgroup
 constexpr int SEL_MAX_G = 8;
 
-// Block i's log-weight blk_max + log blk_sum (-inf where the block holds nothing).
-__device__ __forceinline__ float log_weight(const float* bm, const float* bs, int i) {
-  const float s = bs[i];
-  return s > 0.f ? bm[i] + __logf(s) : NEG_INF;
+// A head's statistics of the blocks lane + 64 r (r < RU, clamped into [0, nb)): every load issued
+// before any is used, so the wavefront waits for one memory round trip, not one per slot.
+template <int R>
+__device__ __forceinline__ void load_stats(const float* bm, const float* bs, int nb, int RU, int lane, float (&m)[R],
+                                           float (&s)[R]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int ic = min(lane + WAVE * r, nb - 1);
+    m[r] = r < RU ? bm[ic] : NEG_INF;
+    s[r] = r < RU ? bs[ic] : 0.f;
+  }
 }
+
+// Block log-weight blk_max + log blk_sum (-inf where the block holds nothing or is past nb).
+__device__ __forceinline__ float log_weight(float m, float s, bool in) { return in && s > 0.f ? m + __logf(s) : NEG_INF; }
 
 // Workgroup (KV head h, sequence b): each wavefront takes query heads g = wave + 4 j; lane holds
 // blocks i = lane + 64 r (r < R, nb <= 64 R). A head keeps its blocks by the rule, the group keeps
@@ -22,6 +32,7 @@ __device__ __forceinline__ float log_weight(const float* bm, const float* bs, in
 // the others ascending, as a stable sort of ~keep) and each head's scale exp(blk_max - lse_kept).
 template <int R>
 __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_args a) {
+  constexpr int HPW = (SEL_MAX_G + SW - 1) / SW;  // query heads per wavefront at most
   const int h = blockIdx.x, b = blockIdx.y;
   const int G = a.Hq / a.Hkv;
   const int nb = a.nb;
@@ -31,17 +42,30 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
   const int64_t hrow0 = static_cast<int64_t>(b) * a.Hq + static_cast<int64_t>(h) * G;
   __shared__ uint64_t sKm[SEL_MAX_G][R];  // per query head: the blocks its rule keeps
   __shared__ uint64_t sKeep[R];           // the group's union with sink and local blocks
+  __shared__ uint64_t sHist[SW][256];     // each wavefront's top-p histogram
   // slots past the last block's group of 4 hold nothing (uniform)
   const int RU = R <= 4 ? R : min(R, 4 * ((nb + 4 * WAVE - 1) / (4 * WAVE)));
+  // a head's statistics stay in registers for its scales when they fit (else they are loaded again)
+  constexpr bool KEEP_REGS = R <= 16;
+  float bmk[KEEP_REGS ? HPW : 1][KEEP_REGS ? R : 1], xk[KEEP_REGS ? HPW : 1][KEEP_REGS ? R : 1];
 
-  for (int g = wave; g < G; g += SW) {
-    const float* bm = a.blk_max + (hrow0 + g) * nb;
-    const float* bs = a.blk_sum + (hrow0 + g) * nb;
-    float x[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = lane + WAVE * r;
-      x[r] = (r < RU && i < nb) ? log_weight(bm, bs, i) : NEG_INF;
+  for (int j = 0; j < HPW; ++j) {
+    const int g = wave + SW * j;
+    if (g >= G) break;
+    float x[R], bmv[R];
+    {
+      float bsv[R];
+      load_stats<R>(a.blk_max + (hrow0 + g) * nb, a.blk_sum + (hrow0 + g) * nb, nb, RU, lane, bmv, bsv);
+#pragma unroll
+      for (int r = 0; r < R; ++r) x[r] = log_weight(bmv[r], bsv[r], r < RU && lane + WAVE * r < nb);
+    }
+    if constexpr (KEEP_REGS) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        bmk[j][r] = bmv[r];
+        xk[j][r] = x[r];
+      }
     }
     float mx = NEG_INF;
 #pragma unroll
@@ -69,7 +93,7 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
         if (lane == 0) sKm[g][r] = m;
       }
     } else {            // topp: the fewest blocks reaching value
-      const uint32_t theta = any ? topp_theta<R>(key, w, RU, a.value) : 0xffffffffu;
+      const uint32_t theta = any ? topp_theta<R>(key, w, RU, a.value, sHist[wave]) : 0xffffffffu;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t m = __ballot(any && lane + WAVE * r < nb && x[r] != NEG_INF && key[r] >= theta);
@@ -78,16 +102,17 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
     }
   }
   __syncthreads();
-  if (wave == 0) {
+  if (tid < R) {  // thread r: slot r's union over the group, the sink and the local blocks
+    uint64_t u = 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      uint64_t u = 0;
-      for (int g = 0; g < G; ++g) u |= sKm[g][r];
-      const int i = lane + WAVE * r;
-      const bool k = i < nb && (((u >> lane) & 1) || always_block(i, nb, a.local));
-      const uint64_t m = __ballot(k);
-      if (lane == 0) sKeep[r] = m;
-    }
+    for (int g = 0; g < SEL_MAX_G; ++g)
+      if (g < G) u |= sKm[g][tid];
+    const int i0 = WAVE * tid;  // blocks i0 .. i0 + 63 of this slot
+    const int n_in = min(max(nb - i0, 0), WAVE);
+    const uint64_t valid = n_in == WAVE ? ~0ull : ((1ull << n_in) - 1);
+    const int a0 = max(nb - a.local, 0) - i0;  // slot bits >= a0 are local blocks
+    const uint64_t local = a0 <= 0 ? ~0ull : (a0 >= WAVE ? 0ull : ~((1ull << a0) - 1));
+    sKeep[tid] = (u | local | (tid == 0 ? 1ull : 0ull)) & valid;
   }
   __syncthreads();
   const uint64_t* kn = sKeep;
@@ -119,22 +144,41 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
   }
 
   if (a.blk_scale != nullptr) {
-    for (int g = wave; g < G; g += SW) {
-      const float* bm = a.blk_max + (hrow0 + g) * nb;
-      const float* bs = a.blk_sum + (hrow0 + g) * nb;
-      float m = NEG_INF, s = 0.f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int i = lane + WAVE * r;
-        if (r < RU && i < nb && ((kn[r] >> lane) & 1)) lse_push(m, s, log_weight(bm, bs, i));
+    for (int j = 0; j < HPW; ++j) {
+      const int g = wave + SW * j;
+      if (g >= G) break;
+      float bmv[R], x[R];
+      if constexpr (KEEP_REGS) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          bmv[r] = bmk[j][r];
+          x[r] = xk[j][r];
+        }
+      } else {
+        float bsv[R];
+        load_stats<R>(a.blk_max + (hrow0 + g) * nb, a.blk_sum + (hrow0 + g) * nb, nb, RU, lane, bmv, bsv);
+#pragma unroll
+        for (int r = 0; r < R; ++r) x[r] = log_weight(bmv[r], bsv[r], r < RU && lane + WAVE * r < nb);
       }
-      lse_wave(m, s);
-      const float lk = s > 0.f ? m + __logf(s) : 0.f;
+      // log-sum-exp over the kept blocks: the max first, then the scaled sum (independent terms)
+      float m = NEG_INF;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if ((kn[r] >> lane) & 1) m = fmaxf(m, x[r]);
+      m = wave_max(m);
+      float sum = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (((kn[r] >> lane) & 1) && x[r] != NEG_INF) sum += __expf(x[r] - m);
+      sum = wave_sum(sum);
+      const float lk = sum > 0.f ? m + __logf(sum) : 0.f;
       float* sc = a.blk_scale + bh * nb * G + g;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int i = lane + WAVE * r;
-        if (i < nb) sc[static_cast<int64_t>(i) * G] = (s > 0.f && ((kn[r] >> lane) & 1)) ? __expf(bm[i] - lk) : 0.f;
+        const bool kept = (kn[r] >> lane) & 1;
+        if (i < nb) sc[static_cast<int64_t>(i) * G] = (sum > 0.f && kept) ? __expf(bmv[r] - lk) : 0.f;
       }
     }
   }

@@ -137,7 +137,7 @@ def select_blocks(logw, G, rule, value, local=2):
     return keep | always_keep(nb, local)
 
 
-def vskip1_keep(q, k, scale, tau, local, lse_prev=None):
+def vskip1_keep(q, k, scale, tau, local, lse_prev=None, dtype=torch.float64):
     """Blocks whose V the single-pass V-skip reads, and the signed decision margin.
 
     kernels/kvskip_kernel.cu:562-578,630-640 (and bench/test_decode.py:134-150): a block is read
@@ -148,18 +148,19 @@ def vskip1_keep(q, k, scale, tau, local, lse_prev=None):
     Hkv, T = k.shape[1], k.shape[2]
     G = Hq // Hkv
     nb = nblocks(T)
-    M, S = block_stats(q, k, scale)
+    M, S = block_stats(q, k, scale, dtype=dtype)
     lse_b = block_logw(M, S)                                           # [B, Hq, nb]
-    lse0 = lse_b[..., :1] if lse_prev is None else lse_prev.to(torch.float64)[..., None]
+    lse0 = lse_b[..., :1] if lse_prev is None else lse_prev.to(dtype)[..., None]
     z = (lse_b - lse0 - math.log(tau)).reshape(B, Hkv, G, nb).amax(2)
     keep = (z >= 0) | always_keep(nb, local)
     return keep, z
 
 
-def vskip1(q, k, v, scale, tau, local=2, lse_prev=None):
-    """Single-pass V-skip result: (out, lse, keep, vcount [B, Hkv])."""
-    keep, _ = vskip1_keep(q, k, scale, tau, local, lse_prev)
-    out, lse = decode(q, k, v, scale, keep=keep)
+def vskip1(q, k, v, scale, tau, local=2, lse_prev=None, dtype=torch.float64):
+    """Single-pass V-skip result: (out, lse, keep, vcount [B, Hkv]). dtype: float32 for the timed CPU
+    baseline (the checks use float64)."""
+    keep, _ = vskip1_keep(q, k, scale, tau, local, lse_prev, dtype)
+    out, lse = decode(q, k, v, scale, keep=keep, dtype=dtype)
     return out, lse, keep, keep.sum(-1).to(torch.int32)
 
 

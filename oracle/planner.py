@@ -243,12 +243,14 @@ def update(st: State, pr: dict, logw, policy: Policy):
     st.lse_att = attended_lse(logw, st.keep | A.always_keep(nb, policy.local), G)
 
 
-def step(st: State, q, k, v, policy: Policy, idx=None):
-    """One decode step after the first (src/kvskip_attn.py:356-396). Returns (out, plan dict)."""
+def step(st: State, q, k, v, policy: Policy, idx=None, dtype=torch.float64):
+    """One decode step after the first (src/kvskip_attn.py:356-396). Returns (out, plan dict).
+    dtype: the attention pass's arithmetic (float32 for the timed CPU baseline; the checks use
+    float64); the planner's own arithmetic stays float64."""
     pr = plan(st, q, k, policy, idx)
-    out, _ = A.decode(q, k, v, st.scale, keep=pr["read"])
-    M, S = A.block_stats(q, k, st.scale, keep=pr["read"])
-    update(st, pr, A.block_logw(M, S), policy)
+    out, _ = A.decode(q, k, v, st.scale, keep=pr["read"], dtype=dtype)
+    M, S = A.block_stats(q, k, st.scale, keep=pr["read"], dtype=dtype)
+    update(st, pr, A.block_logw(M.double(), S.double()), policy)
     return out, pr
 
 
