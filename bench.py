@@ -389,7 +389,7 @@ def main():
 
 def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
     """Two-pass V-skip on one layer (NCOPY KV copies), top-p 0.99 GQA union: pass 1 (stats-only + fp16
-    P), the device selection (kvskip_select: kept set, lists, per-block scales) and pass 2 (pv over the
+    P; its split pass alone, as the op runs it), the device selection (kvskip_select: kept set, lists, per-block scales) and pass 2 (pv over the
     kept blocks) each timed as a graph-replayed region, and the whole op as the front-end runs it
     without a host read-back (kvskip.vskip_two_pass(sync=False): pass 2 sized by nb), also replayed."""
     import torch
@@ -398,7 +398,7 @@ def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
     Hkv, T = ks[0].shape[1], ks[0].shape[2]
     G, nb = Hq // Hkv, math.ceil(T / 64)
     dev = q.device
-    r1 = E.decode(q, ks[0], vs[0], scale, None, None, True, False, S1, 2, False, True)
+    r1 = E.decode(q, ks[0], vs[0], scale, None, None, True, False, S1, 2, False, True, merge=False)
     keep = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=dev)
     idx = torch.empty(B, Hkv, nb, dtype=torch.int32, device=dev)
     cnt = torch.empty(B, Hkv, dtype=torch.int32, device=dev)
@@ -411,8 +411,8 @@ def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
     kept = int(cnt.sum())
     S2 = K.num_splits_for(B * Hkv, int(cnt.max()))
     P1 = r1[5]
-    t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], scale, None, None, True, False, S1, 2, False, True),
-                         args.steps // 2, args.warmup)
+    t_p1 = events_region(lambda i: E.decode(q, ks[i], vs[i], scale, None, None, True, False, S1, 2, False, True,
+                                            merge=False), args.steps // 2, args.warmup)
     t_sel = events_region(select, args.steps // 2, args.warmup)
     t_p2 = events_region(lambda i: E.pv(P1, vs[i], scales, idx, cnt, S2, False), args.steps // 2, args.warmup)
     t_op = events_region(lambda i: K.vskip_two_pass(q, ks[i], vs[i], scale, sync=False), args.steps // 2,

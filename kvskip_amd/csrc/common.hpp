@@ -112,6 +112,22 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return __builtin_amdgcn_readlane(wave_incl_scan(v), WAVE - 1);
 }
 
+// Unsigned integer minimum over the wavefront (uniform result).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppu(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int src) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), src));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, dppu<DPP_XOR1>(v));
+  v = min(v, dppu<DPP_XOR2>(v));
+  v = min(v, dppu<DPP_HALF_MIRROR>(v));
+  v = min(v, dppu<DPP_MIRROR>(v));
+  return min(min(lane_u32(v, 0), lane_u32(v, 16)), min(lane_u32(v, 32), lane_u32(v, 48)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_XOR1>(v));
   v = fmaxf(v, dpp<DPP_XOR2>(v));

@@ -204,16 +204,23 @@ __device__ __forceinline__ uint32_t fkey(float y) {
 // hold no block, RU uniform): the largest key theta of y = x - lse whose upper set {key >= theta}
 // holds >= level of the mass w = exp(y), i.e. the fewest blocks reaching level with ties at the cut
 // kept (kernels/kvskip.py:140-143 keeps the blocks whose heavier blocks hold < level); theta = 0
-// (every block) when the whole mass falls short of level. Uniform result.
+// (every block) when the whole mass falls short of level. Uniform result. w > 0 exactly where a
+// block holds mass; ymax = max y, with w of that block = __expf(ymax).
 //
-// Radix select over the key, 8 bits per pass: a pass sums the mass of the blocks still in play
-// (key above the bits decided so far equal to them) into 256 bins of the next 8 bits, and takes the
-// highest bin whose mass from the top reaches what is still needed. The mass is summed exactly in
-// 2^-60 fixed point (64-bit integer adds in LDS), so the passes agree with each other and the
-// result does not depend on the order of the adds. hist: this wavefront's 256 LDS bins, used by it
-// alone.
-__device__ __forceinline__ uint64_t fixmass(float w) {  // floor(w 2^60), w in [0, 16)
-  const float s = w * 0x1p28f;                        // exact
+// Radix select over the key less the smallest key of a block with mass (kmin), 8 bits per pass from
+// the top bit of the span up to the largest key (that of ymax, the largest y). A pass sums the
+// blocks still in play (offset key above the bits decided so far equal to them) into 256 bins of the
+// next 8 bits and takes the highest bin whose mass from the top reaches what is still needed; a bin
+// holding one block ends the search at that block's key. Bins over the span spread the blocks (few
+// LDS atomics to one address). Each bin packs the count of its blocks (bits 51..63) over their mass
+// in 2^-48 fixed point (a head's mass, about 1, stays under 2^49, so the fields never carry into each
+// other): the sums are exact, the passes agree with each other and the result does not depend on the
+// order of the adds. hist: this wavefront's 256 LDS bins, used by it alone.
+constexpr int BIN_CNT_SHIFT = 51;
+constexpr uint64_t BIN_MASS = (1ull << BIN_CNT_SHIFT) - 1;
+
+__device__ __forceinline__ uint64_t fixmass(float w) {  // floor(w 2^48), w in [0, 8)
+  const float s = w * 0x1p16f;                        // exact
   const uint32_t hi = static_cast<uint32_t>(s);
   const float f = s - static_cast<float>(hi);         // exact fraction of s
   return (static_cast<uint64_t>(hi) << 32) | static_cast<uint32_t>(f * 0x1p32f);
@@ -246,41 +253,77 @@ __device__ __forceinline__ uint64_t wave_scan64(uint64_t v, int lane) {
 
 template <int R>
 __device__ __forceinline__ uint32_t topp_theta(const uint32_t (&key)[R], const float (&w)[R], int RU, float level,
-                                               uint64_t* hist) {
+                                               float ymax, uint64_t* hist) {
   const int lane = threadIdx.x % WAVE;
   uint64_t need = fixmass(level);  // mass still needed from the blocks in play
-  uint32_t theta = 0;
+  if (fixmass(__expf(ymax)) >= need) return fkey(ymax);  // the heaviest block alone reaches level
+  // Blocks lighter than wcut are out of play: together they hold < (1 - level) / 8, so the blocks
+  // above them hold >= level and the cut lies among those (with room for the rounding of w; none
+  // are left out for level within 1e-5 of 1).
+  const float wcut = level < 0.99999f ? (1.f - level) / (8.f * WAVE * RU) : 0.f;
+  uint64_t inc = 0;  // bit r: slot r in play
+  uint32_t kmin = ~0u;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r < RU && w[r] > wcut) {
+      inc |= 1ull << r;
+      kmin = min(kmin, key[r]);
+    }
+  kmin = wave_min_u32(kmin);
+  const uint32_t kmax = fkey(ymax);
+  if (kmax < kmin) return 0;  // no block holds mass
+  const uint32_t span = kmax - kmin;
+  int sh = span == 0 ? 0 : max(24 - static_cast<int>(__builtin_clz(span)), 0);  // top 8 bits of the span
+  int prev = 32;              // offset bits >= prev are decided (none yet)
+  uint32_t dec = 0;           // the decided offset bits
   uint64_t* mine = hist + 4 * (WAVE - 1 - lane);  // lane L holds bins 4 (63 - L) .. + 3: lane 0 the top
 #pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int sh = 24 - 8 * pass;
-    const uint32_t hm = pass == 0 ? 0u : ~0u << (sh + 8);  // bits decided so far
+  for (int pass = 0; pass < 4; ++pass) {  // the span has <= 32 bits: <= 4 passes
 #pragma unroll
     for (int k = 0; k < 4; ++k) mine[k] = 0;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r < RU && w[r] > 0.f && (key[r] & hm) == theta)
-        __hip_atomic_fetch_add(hist + ((key[r] >> sh) & 255u), fixmass(w[r]), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WAVEFRONT);
+    for (int r = 0; r < R; ++r) {
+      const uint32_t off = key[r] - kmin;
+      if (((inc >> r) & 1) && (pass == 0 || (off >> prev) == (dec >> prev)))
+        __hip_atomic_fetch_add(hist + ((off >> sh) & 255u), (1ull << BIN_CNT_SHIFT) | fixmass(w[r]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     uint64_t h[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) h[k] = mine[k];
     const uint64_t s3 = h[3], s2 = h[2] + s3, s1 = h[1] + s2, s0 = h[0] + s1;  // from bin k up, in the lane
-    const uint64_t incl = wave_scan64(s0, lane);  // mass of the bins >= 4 (63 - lane)
+    const uint64_t incl = wave_scan64(s0, lane);  // bins >= 4 (63 - lane)
     const uint64_t excl = incl - s0;
-    const uint64_t reach = __ballot(incl >= need);
+    const uint64_t reach = __ballot((incl & BIN_MASS) >= need);
     if (reach == 0) return 0;                      // only in the first pass: the whole mass < level
     const int L = __builtin_ctzll(reach);          // the lane of the highest bin that reaches need
-    const int k = excl + s3 >= need ? 3 : excl + s2 >= need ? 2 : excl + s1 >= need ? 1 : 0;
+    const int k = ((excl + s3) & BIN_MASS) >= need ? 3 : ((excl + s2) & BIN_MASS) >= need ? 2
+                : ((excl + s1) & BIN_MASS) >= need ? 1 : 0;
     const uint64_t hk = k == 3 ? s3 : k == 2 ? s2 - s3 : k == 1 ? s1 - s2 : s0 - s1;
     const uint64_t above = excl + (k == 3 ? s3 : k == 2 ? s2 : k == 1 ? s1 : s0) - hk;  // bins over the chosen
-    const int kL = __builtin_amdgcn_readlane(k, L);
-    need -= lane64(above, L);
-    theta |= static_cast<uint32_t>(4 * (WAVE - 1 - L) + kL) << sh;
+    const uint32_t bin = 4 * (WAVE - 1 - L) + __builtin_amdgcn_readlane(k, L);
+    const uint64_t hb = lane64(hk, L);
+    need -= lane64(above, L) & BIN_MASS;
+    dec |= bin << sh;
+    if (sh == 0) break;
+    if ((hb >> BIN_CNT_SHIFT) == 1) {  // one block in the bin: the cut is its key
+      uint32_t mk = 0;
+      bool has = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t off = key[r] - kmin;
+        const bool c = ((inc >> r) & 1) && (pass == 0 || (off >> prev) == (dec >> prev)) && ((off >> sh) & 255u) == bin;
+        mk = c ? key[r] : mk;
+        has = has || c;
+      }
+      return __builtin_amdgcn_readlane(mk, __builtin_ctzll(__ballot(has)));
+    }
+    prev = sh;
+    sh = max(sh - 8, 0);
   }
-  return theta;
+  return kmin + dec;
 }
 
 // Update of (b, KV head h): src/kvskip_attn.py:386-391 (_calib_learn 302-320, _refresh_state
@@ -378,7 +421,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
         w[r] = r < RU ? __expf(y) : 0.f;
         key[r] = fkey(y);
       }
-      const uint32_t theta = topp_theta<R>(key, w, RU, p.level, sHist[wave]);
+      const uint32_t theta = topp_theta<R>(key, w, RU, p.level, mx - lse, sHist[wave]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t m = __ballot(lane + WAVE * r < nb && key[r] >= theta);

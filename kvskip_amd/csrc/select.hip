@@ -93,7 +93,7 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
         if (lane == 0) sKm[g][r] = m;
       }
     } else {            // topp: the fewest blocks reaching value
-      const uint32_t theta = any ? topp_theta<R>(key, w, RU, a.value, sHist[wave]) : 0xffffffffu;
+      const uint32_t theta = any ? topp_theta<R>(key, w, RU, a.value, mx - lse, sHist[wave]) : 0xffffffffu;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint64_t m = __ballot(any && lane + WAVE * r < nb && x[r] != NEG_INF && key[r] >= theta);
@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
   if (a.keep != nullptr)
     for (int i = tid; i < nb; i += SW * WAVE) a.keep[bh * nb + i] = (kn[i / WAVE] >> (i % WAVE)) & 1;
 
-  if (a.block_idx != nullptr && wave == 0) {
+  if (a.block_idx != nullptr) {  // wavefront w writes slots r = w + SW t; positions from the slots before
     int total = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) total += __popcll(kn[r]);
@@ -129,18 +129,17 @@ __global__ void __launch_bounds__(SW * WAVE) select_kernel(const kvskip_select_a
     int32_t* bi = a.block_idx + bh * nb;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int i = lane + WAVE * r;
       const int n_valid = min(max(nb - WAVE * r, 0), WAVE);
       const uint64_t valid = n_valid == WAVE ? ~0ull : ((1ull << n_valid) - 1);
-      const bool k = (kn[r] >> lane) & 1;
-      if (i < nb) {
-        const int pos = k ? base_k + __popcll(kn[r] & below) : base_u + __popcll(valid & ~kn[r] & below);
-        bi[pos] = i;
+      if (r % SW == wave) {
+        const int i = lane + WAVE * r;
+        const bool k = (kn[r] >> lane) & 1;
+        if (i < nb) bi[k ? base_k + __popcll(kn[r] & below) : base_u + __popcll(valid & ~kn[r] & below)] = i;
       }
       base_k += __popcll(kn[r]);
       base_u += __popcll(valid & ~kn[r]);
     }
-    if (lane == 0) a.block_cnt[bh] = total;
+    if (tid == 0) a.block_cnt[bh] = total;
   }
 
   if (a.blk_scale != nullptr) {

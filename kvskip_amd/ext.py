@@ -112,7 +112,7 @@ def _set_pages(a, block_table, pool):
 
 
 def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
-           want_f32=False, write_p=False, seq_lens=None, block_table=None, T=None):
+           want_f32=False, write_p=False, seq_lens=None, block_table=None, T=None, merge=True):
     """Split-K decode attention (kernels/kvskip_ext.cpp:25-101).
 
     Returns [out bf16 [B,Hq,D], lse fp32 [B,Hq], blk_max, blk_sum ([B,Hq,nb] or None), out_f32 (or None),
@@ -121,7 +121,9 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     seq_lens (not in the reference): int32 [B] on the device, a ragged batch; sequence b attends
     tokens [0, clamp(seq_lens[b], 1, T)) of its view; num_splits is then the per-KV-head split
     budget over the whole batch (>= 2).
-    block_table, T (not in the reference): a paged cache, see _kv_dims (the pass with V, MFMA engine)."""
+    block_table, T (not in the reference): a paged cache, see _kv_dims (the pass with V, MFMA engine).
+    merge=False (not in the reference; load_v=False): the split pass alone, no merge launch; the block
+    statistics and P are whole, lse is not computed (returned as None)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -133,6 +135,7 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     _require(1 <= num_splits <= 256, "num_splits in 1..256")
     _require(load_v or stats, "load_v=false only makes sense with stats=true")
     _require(not write_p or stats, "write_p needs stats=true")
+    _require(merge or not load_v, "merge=False needs load_v=False")
     _require(stages in (2, 3), "kvskip: unsupported head dim / stages")
     nb = (T + TILE - 1) // TILE
     dev = q.device
@@ -149,9 +152,10 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
     if num_splits > 1:
         part_acc = torch.empty(B, Hq, num_splits, D, **f32) if load_v else None
         part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
+    split_only = not merge and num_splits > 1
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens, block_table=block_table, T=T)
-    return [out, lse, bmax, bsum, out32, pbuf]
+                   pbuf, part_acc, part_ml, seq_lens, phase=1 if split_only else 3, block_table=block_table, T=T)
+    return [out, None if split_only else lse, bmax, bsum, out32, pbuf]
 
 
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,

@@ -105,13 +105,14 @@ def _as_bhd(q: torch.Tensor) -> torch.Tensor:
 def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = False, load_v: bool = True,
            num_splits: int | None = None, stages: int = 2, out_f32: bool = False, write_p: bool = False,
            seq_lens: torch.Tensor | None = None, block_table: torch.Tensor | None = None,
-           T: int | None = None) -> dict:
+           T: int | None = None, merge: bool = True) -> dict:
     """Decode attention of one layer (kernels/kvskip.py:88-113). Returns a dict with out [B, Hq, D]
     bf16 (None with load_v=False), lse [B, Hq] fp32, num_splits, and as asked blk_max / blk_sum
     [B, Hq, nb] fp32, out_f32, p (fp16 [B, Hq, nb*64] = exp(s - blk_max)).
     Not in the reference: seq_lens (int32 [B] on the device) makes a ragged batch over views of
     capacity T, the split budget shared by the batch; block_table (int32 [B, >= ceil(T / 64)]) with T
-    makes k, v page pools [num_pages, Hkv, 64, D]."""
+    makes k, v page pools [num_pages, Hkv, 64, D]; merge=False (with load_v=False) skips the split
+    merge, leaving lse None."""
     q = _as_bhd(q)
     B, Hkv = q.shape[0], k.shape[1]
     tokens = k.shape[2] if block_table is None else int(T)
@@ -121,7 +122,8 @@ def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = Fal
         num_splits = ragged_splits(B, Hkv, items) if seq_lens is not None else num_splits_for(B * Hkv, items)
     lists = (None, None) if plan is None else (plan.block_idx, plan.block_cnt)
     out, lse, bmax, bsum, o32, p = ext().decode(q, k, v, float(scale), *lists, stats, load_v, int(num_splits),
-                                                int(stages), out_f32, write_p, seq_lens, **_paged(block_table, T))
+                                                int(stages), out_f32, write_p, seq_lens, **_paged(block_table, T),
+                                                merge=merge)
     res = {"out": out, "lse": lse, "num_splits": num_splits}
     extra = {"blk_max": bmax, "blk_sum": bsum} if stats else {}
     if out_f32:
@@ -171,14 +173,15 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
                    sync: bool = True, out_f32: bool = False, block_table: torch.Tensor | None = None,
                    T: int | None = None) -> dict:
     """Two-pass V-skip (kernels/kvskip.py:157-179). Pass 1 reads K once, writing the block statistics
-    and P; the device selection (kvskip_select) turns the statistics into the kept set, its lists and
-    the per-block scales exp(blk_max - lse over the kept set); pass 2 reads P and V of the kept blocks.
+    and P (its split pass alone: the log-sum-exp merge is not needed); the device selection
+    (kvskip_select) turns the statistics into the kept set, its lists and the per-block scales
+    exp(blk_max - lse over the kept set); pass 2 reads P and V of the kept blocks.
     Returns out, keep [B, Hkv, nb] bool and, with sync=True, kept_frac (that read-back also sizes pass
     2's split count by the longest list). block_table, T (not in the reference): page pools."""
     q = _as_bhd(q)
     B, Hq = q.shape[:2]
     Hkv = k.shape[1]
-    first = decode(q, k, v, scale, stats=True, load_v=False, write_p=True, **_paged(block_table, T))
+    first = decode(q, k, v, scale, stats=True, load_v=False, write_p=True, merge=False, **_paged(block_table, T))
     nb = first["blk_max"].shape[-1]
     dev = q.device
     keep = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=dev)
