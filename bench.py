@@ -130,6 +130,9 @@ def main():
                     help="only the dominant kernel's timed region (the rocprofv3 --stats target), then exit")
     ap.add_argument("--pmc-target", action="store_true",
                     help="profiling target only: 20 dense config-2 decodes + copy kernels of known size, then exit")
+    ap.add_argument("--pmc-paths", action="store_true",
+                    help="profiling target only: config 2 masked + stats, the peaked two-pass V-skip op, a short "
+                         "config-4 planner loop, + copy kernels of known size, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -167,6 +170,9 @@ def main():
 
     if args.pmc_target:
         pmc_target(dense, dev)
+        return
+    if args.pmc_paths:
+        pmc_paths(q, ks, vs, L.scale, bi, bc, dev)
         return
 
     def masked(i):
@@ -504,6 +510,56 @@ def pmc_target(dense, dev):
         E.read_bw(a, o, 1024)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_target": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2}), flush=True)
+
+
+def pmc_paths(q, ks, vs, scale, bi, bc, dev):
+    """Profiling target for rocprofv3 --pmc beyond the dense pass: 20 config-2 masked + statistics
+    ops (the bench's list), 20 two-pass V-skip ops on the peaked layer (pass 1, select, pass 2),
+    a config-4 planner loop of 4 layers x 12 steps (updates carried), then the known-size copy and
+    read of pmc_target."""
+    import torch
+
+    from kvskip_amd import ext as E
+    from kvskip_amd import kvskip as K
+    from kvskip_amd import workloads as W
+    from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+
+    Hkv, T = ks[0].shape[1], ks[0].shape[2]
+    S_mask = K.num_splits_for(Hkv, int(bc.max()))
+    for i in range(20):
+        E.decode(q, ks[i % NCOPY], vs[i % NCOPY], scale, bi, bc, True, True, S_mask, 2, False, False)
+    run = W.planner_run(layers=1, T0=T, steps=1, seed=44, device=dev)
+    q_p = run.q0[0].to(torch.bfloat16).contiguous()
+    for i in range(20):
+        K.vskip_two_pass(q_p, run.k[0][:, :, :T], run.v[0][:, :, :T], run.scale, sync=False)
+    del run
+    layers, steps = 4, 12
+    run = W.planner_run(layers=layers, T0=T, steps=steps, seed=4, device=dev)
+    qps = [W.QueryProcess(run, l, noise=0.25) for l in range(layers)]
+    ids = run.ids.to(dev)
+    pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    carrier = UpdateCarrier()
+    pls = [FusedPlanner(pol, count=False, carrier=carrier) for _ in range(layers)]
+    for t in range(steps):
+        for l in range(layers):
+            k, v = run.k[l][:, :, :T + t + 1], run.v[l][:, :, :T + t + 1]
+            ql = qps[l].next().to(dev)
+            if t == 0:
+                pls[l].first(ql, k, v, run.scale)
+            else:
+                pls[l].step(ql, k, v, run.scale, ids=ids)
+    carrier.flush()
+    torch.cuda.synchronize()
+    del run, pls
+    a = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    o = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(5):
+        b.copy_(a)
+    for _ in range(5):
+        E.read_bw(a, o, 1024)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_paths": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2}), flush=True)
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
