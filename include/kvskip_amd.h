@@ -192,6 +192,14 @@ typedef struct kvskip_plan_args {
   const int32_t* block_table;
   int64_t bt_stride;
   int32_t num_pages;
+  /* Optional, read by kvskip_decode_splits_planned only (not in the reference): 0, or the pass's
+   * workgroup budget over all B * Hkv (<= 16) lists together. Every workgroup then decides all the
+   * lists and cuts them into chunks of one length over all of them (a refreshing head gets more
+   * workgroups than a light one); the pass's num_splits is the count of split-partial slots per
+   * head (each list gets at most that many chunks), and the slots a list leaves unused are written
+   * empty, so the split merge takes num_splits as usual. The grid is pass_budget + B * Hkv
+   * workgroups. */
+  int32_t pass_budget;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);

@@ -48,7 +48,7 @@ class PlanArgs(ctypes.Structure):
         ("scale", c_float), ("delta", c_float),
         ("part", c_void_p), ("seq_lens", c_void_p), ("seq_lens_out", c_void_p),
         ("ids", c_void_p), ("ids_sb", c_int64), ("idx_out", c_void_p),
-        ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32),
+        ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32), ("pass_budget", c_int32),
     ]
 
 

@@ -518,7 +518,7 @@ __device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq
   float A = 0.f, L = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (cls + NC * u < Sv) {
+    if (cls + NC * u < Sv && (plain || ls[u] > 0.f)) {  // an empty partial (l = 0) adds nothing
       const float w = plain ? 1.f : fexp2(ms[u] - mu);
       L += ls[u] * w;
       if constexpr (WITH_V) A += as[u] * w;

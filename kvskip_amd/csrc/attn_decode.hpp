@@ -63,13 +63,122 @@ __device__ void write_gap_stats(const AttnP& p, const List& list, int n_items, i
   }
 }
 
+// A planned pass over all B * Hkv (<= BAL_MAX_LISTS) lists together (kvskip_plan_args.pass_budget
+// > 0): wavefront w decides lists w + NWAVE j together (decide_heads: one load round trip;
+// workgroup 0 stores trig and est), the
+// lists are cut into chunks of one length C over all of them (pass_budget workgroups' worth, at
+// most p.num_splits chunks per list, at least one) numbered list by list, and this workgroup takes
+// chunk number bid: its list (b, h), chunk (the partial slot `split`), positions
+// [i0, i0 + n) of n_items, refresh flag and, for a stored-set list, its slice of the positions in
+// sPl (positions i0 - 1 .. i0 + n - 1). The workgroup of a list's chunk 0 empties the list's unused
+// partial slots; on the one of its last chunk, `writer` is set on the wavefront that decided the
+// list, whose masks go to omk: it writes the list and its count after its blocks. Returns false for
+// a workgroup past the last chunk (nothing to do). Uniform results.
+constexpr int BAL_MAX_LISTS = 16;
+
+template <int G, int NH>
+__device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, int bid, int wave, int lane, int nbb,
+                                    int* sPl, uint32_t* sMk, int* sPre, int& split, int& h, int& b, int& n_items,
+                                    int& i0, int& n, bool& dense, bool& writer, uint32_t (&omk)[DCL]) {
+  __shared__ int sCnt[BAL_MAX_LISTS];
+  __shared__ int sTr[BAL_MAX_LISTS];
+  const int P = p.B * p.Hkv;
+  int lists[NH];  // this wavefront's lists wave + NWAVE k (clamped: a repeat is decided, not stored)
+#pragma unroll
+  for (int k = 0; k < NH; ++k) lists[k] = min(wave + NWAVE * k, P - 1);
+  uint32_t mk[NH][DCL];
+  bool tr[NH];
+  decide_heads<G, NH>(pa, lists, lane, mk, tr, bid == 0, false);
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    int c = 0;
+#pragma unroll
+    for (int d = 0; d < DCL; ++d) c += __popc(mk[k][d]);
+    c = static_cast<int>(wave_sum(static_cast<float>(c)));  // exact: counts <= MAX_NB
+    if (lane == 0 && wave + NWAVE * k < P) {
+      sCnt[wave + NWAVE * k] = tr[k] ? nbb : c;
+      sTr[wave + NWAVE * k] = tr[k] ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  // the partition, lane q holding list q (every wavefront computes the same)
+  const int cq = lane < P ? sCnt[lane] : 0;
+  const int total = static_cast<int>(wave_sum(static_cast<float>(cq)));  // exact: <= 16 * MAX_NB
+  const int most = static_cast<int>(wave_max(static_cast<float>(cq)));
+  const int slots = p.num_splits, budget = pa.pass_budget;
+  const int C = max(1, max((total + budget - 1) / budget, (most + slots - 1) / slots));
+  const int ch = lane < P ? max(1, (cq + C - 1) / C) : 0;
+  const int incl = wave_incl_scan(ch);
+  const int it = bid;  // consecutive chunks on different XCDs: a grid's unused tail idles no XCD
+  const uint64_t hit = __ballot(lane < P && it >= incl - ch && it < incl);
+  if (hit == 0) return false;
+  const int q_sel = __builtin_ctzll(hit);
+  const int ch_sel = __builtin_amdgcn_readlane(ch, q_sel);
+  split = it - (__builtin_amdgcn_readlane(incl, q_sel) - ch_sel);
+  b = q_sel / p.Hkv;
+  h = q_sel % p.Hkv;
+  n_items = __builtin_amdgcn_readlane(cq, q_sel);
+  dense = sTr[q_sel] != 0;
+  i0 = min(n_items, split * C);
+  n = min(n_items, i0 + C) - i0;
+  writer = false;  // the list's last chunk writes the list at its end (it has the fewest items)
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    if (wave + NWAVE * k == q_sel) {  // the wavefront that decided this list holds its masks
+      if (!dense) {
+        int pre[DCL];
+        mask_prefix(mk[k], lane, plan_chunks(pa.T), pre);
+#pragma unroll
+        for (int d = 0; d < DCL; ++d) {
+          sMk[lane + WAVE * d] = mk[k][d];
+          sPre[lane + WAVE * d] = pre[d];
+        }
+      }
+      writer = split == ch_sel - 1;
+#pragma unroll
+      for (int d = 0; d < DCL; ++d) omk[d] = mk[k][d];
+    }
+  }
+  if (split == 0) {  // the slots [ch_sel, slots) of the list's query heads: empty partials
+    const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+    for (int t = threadIdx.x; t < G * (slots - ch_sel); t += NT) {
+      float* ml = p.part_ml + ((hq0 + t % G) * slots + ch_sel + t / G) * 2;
+      ml[0] = NEG_INF;
+      ml[1] = 0.f;
+    }
+  }
+  __syncthreads();
+  if (!dense) {  // this workgroup's slice, positions i0 - 1 .. i0 + n - 1, by every thread
+    slice_from_masks(sMk, sPre, plan_chunks(pa.T), i0, i0 + n, sPl, threadIdx.x, NT);
+    if (threadIdx.x == 0 && i0 == 0) sPl[0] = -1;
+    __syncthreads();
+  }
+  return true;
+}
+
+template <int G>
+__device__ bool planned_balanced(const AttnP& p, const kvskip_plan_args& pa, int bid, int wave, int lane, int nbb,
+                                 int* sPl, uint32_t* sMk, int* sPre, int& split, int& h, int& b, int& n_items,
+                                 int& i0, int& n, bool& dense, bool& writer, uint32_t (&omk)[DCL]) {
+  const int P = p.B * p.Hkv;
+  if (P <= NWAVE)
+    return planned_balanced_nh<G, 1>(p, pa, bid, wave, lane, nbb, sPl, sMk, sPre, split, h, b, n_items, i0, n, dense,
+                                     writer, omk);
+  if (P <= 2 * NWAVE)
+    return planned_balanced_nh<G, 2>(p, pa, bid, wave, lane, nbb, sPl, sMk, sPre, split, h, b, n_items, i0, n, dense,
+                                     writer, omk);
+  return planned_balanced_nh<G, BAL_MAX_LISTS / NWAVE>(p, pa, bid, wave, lane, nbb, sPl, sMk, sPre, split, h, b,
+                                                        n_items, i0, n, dense, writer, omk);
+}
+
 // The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads. PLANNED (masked,
 // unragged partition): the list is the plan's decision for (b, h), made in this workgroup's
 // prologue from the scores pass's partials (pa): wavefront 0 decides (as plan_decide; every
-// workgroup of the head reaches the same result from the same partials) and puts the list
-// positions of this split into LDS; split 0 also stores trig, est and, at its end, the head's block
+// workgroup of the head reaches the same result from the same partials) and puts the chunk masks
+// and their prefixes into LDS, from which all threads place this split's list positions; split 0 also stores trig, est and, at its end, the head's block
 // list and count (the age is advanced by the update). With seq_lens (one sequence) its length
-// comes from device memory; the grid is still num_splits x Hkv x B.
+// comes from device memory; the grid is still num_splits x Hkv x B. With pa->pass_budget > 0 the
+// prologue is planned_balanced's instead (grid pass_budget + B Hkv, num_splits partial slots).
 template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false,
           bool PAGED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
@@ -88,35 +197,55 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   int Tb = p.T, nbb = p.nb;
   __shared__ int sPl[PLANNED ? MAX_NB + 1 : 1];  // planned: list positions i0 - 1 .. i0 + n - 1
   __shared__ int sPi[2];                          // planned: refresh, list length
+  __shared__ uint32_t sMk[PLANNED ? MAX_NB / WCB : 1];  // planned: the list's chunk masks
+  __shared__ int sPre[PLANNED ? MAX_NB / WCB : 1];      // planned: their exclusive prefixes
   uint32_t pmk[DCL];                              // planned, wavefront 0: the chunk masks
   bool dense = false;                             // planned: a refresh (every block, in order)
+  const bool balanced = PLANNED && pa->pass_budget > 0;  // every list cut by one chunk length
+  bool list_writer = false;                               // balanced: this wavefront writes the list
   if constexpr (PLANNED) {
-    work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
-    if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
-      Tb = seq_len(p, b);
-      nbb = (Tb + BLK - 1) / BLK;
-    }
-    if (wave == 0) {
-      int pre[DCL];
-      const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0, false);
-      const int cnt = t ? nbb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
-      if (!t) {
-        const int per = (cnt + p.num_splits - 1) / p.num_splits;
-        const int a0 = min(cnt, split * per), a1 = min(cnt, a0 + per);
-        slice_positions<DCL>(pmk, pre, lane, a0, a1, sPl);
-        if (lane == 0 && a0 == 0) sPl[0] = -1;
+    if (balanced) {
+      if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
+        Tb = seq_len(p, 0);
+        nbb = (Tb + BLK - 1) / BLK;
       }
-      if (lane == 0) {
-        sPi[0] = t ? 1 : 0;
-        sPi[1] = cnt;
+      if (!planned_balanced<G>(p, *pa, bid, wave, lane, nbb, sPl, sMk, sPre, split, h, b, n_items, i0, n, dense,
+                               list_writer, pmk))
+        return;
+    } else {
+      work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
+      if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
+        Tb = seq_len(p, b);
+        nbb = (Tb + BLK - 1) / BLK;
+      }
+      if (wave == 0) {
+        int pre[DCL];
+        const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0, false);
+        const int cnt = t ? nbb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
+        if (!t) {
+#pragma unroll
+          for (int d = 0; d < DCL; ++d) {
+            sMk[lane + WAVE * d] = pmk[d];
+            sPre[lane + WAVE * d] = pre[d];
+          }
+        }
+        if (lane == 0) {
+          sPi[0] = t ? 1 : 0;
+          sPi[1] = cnt;
+        }
+      }
+      __syncthreads();
+      dense = sPi[0] != 0;
+      n_items = sPi[1];
+      const int per = (n_items + p.num_splits - 1) / p.num_splits;
+      i0 = min(n_items, split * per);
+      n = min(n_items, i0 + per) - i0;
+      if (!dense) {  // this split's slice, positions i0 - 1 .. i0 + n - 1, by every thread
+        slice_from_masks(sMk, sPre, plan_chunks(pa->T), i0, i0 + n, sPl, tid, NT);
+        if (tid == 0 && i0 == 0) sPl[0] = -1;
+        __syncthreads();
       }
     }
-    __syncthreads();
-    dense = sPi[0] != 0;
-    n_items = sPi[1];
-    const int per = (n_items + p.num_splits - 1) / p.num_splits;
-    i0 = min(n_items, split * per);
-    n = min(n_items, i0 + per) - i0;
   } else if constexpr (!RAG) {
     work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
     n_items = MASKED ? min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks) : p.nb;
@@ -474,7 +603,8 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
   if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
   if constexpr (PLANNED) {
-    if (split == 0 && wave == 0) write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, nbb, dense, pmk, lane);
+    if (balanced ? list_writer : (split == 0 && wave == 0))
+      write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, nbb, dense, pmk, lane);
   }
   if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)
     if (nbb < p.nb && i0 + n == n_items) {

@@ -403,6 +403,10 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
                                       "separately for a ragged batch)");
   if (a->B != pl->B || a->Hq != pl->Hq || a->Hkv != pl->Hkv || a->T != pl->T || a->D != pl->D)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
+  if (pl->pass_budget < 0 || pl->pass_budget > 65536)
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: pass_budget in 0..65536");
+  if (pl->pass_budget > 0 && a->B * a->Hkv > 16)
+    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: pass_budget needs B * Hkv <= 16 (got %d)", a->B * a->Hkv);
   kvskip_attn_args am = *a;  // the pass's list is the plan's
   am.block_idx = pl->block_idx;
   am.block_cnt = pl->block_cnt;

@@ -98,15 +98,22 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<DPP_MIRROR>(v);
   return rows4_sum(v);
 }
-// Integer wavefront scan (inclusive, over lanes) and sum; uniform sum.
+// Integer wavefront scan (inclusive, over lanes) and sum; uniform sum. DPP shifts inside each
+// 16-lane row (0 from outside the row), then the totals of the rows before.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i0(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
 __device__ __forceinline__ int wave_incl_scan(int v) {
   const int lane = threadIdx.x % WAVE;
-#pragma unroll
-  for (int o = 1; o < WAVE; o <<= 1) {
-    const int t = __shfl_up(v, o, WAVE);
-    if (lane >= o) v += t;
-  }
-  return v;
+  v += dpp_i0<0x111>(v);  // row_shr:1
+  v += dpp_i0<0x112>(v);  // row_shr:2
+  v += dpp_i0<0x114>(v);  // row_shr:4
+  v += dpp_i0<0x118>(v);  // row_shr:8
+  const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31),
+            t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row == 0 ? 0 : row == 1 ? t0 : row == 2 ? t0 + t1 : t0 + t1 + t2);
 }
 __device__ __forceinline__ int wave_sum_int(int v) {
   return __builtin_amdgcn_readlane(wave_incl_scan(v), WAVE - 1);

@@ -25,12 +25,13 @@ __global__ void __launch_bounds__(NT, 2) planned_split_kernel(const AttnP a, con
   decode_body<D, G, true, true, true, true, false, true, PAGED>(a, i - n_update, &pa);
 }
 
-// The pass's grid is num_splits x Hkv x B workgroups whether or not seq_lens is given (B is 1 then):
+// The pass's grid is num_splits x Hkv x B workgroups whether or not seq_lens is given (B is 1 then),
+// or pass_budget + Hkv x B for the balanced partition:
 // the list of a (b, KV head) is cut into num_splits slices as in the unragged pass.
 template <int D, int G, bool PAGED>
 hipError_t launch_planned_p(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, hipStream_t s) {
   const dim3 blk(NT);
-  const int n_pass = a.num_splits * a.Hkv * a.B;
+  const int n_pass = pa.pass_budget > 0 ? pa.pass_budget + a.Hkv * a.B : a.num_splits * a.Hkv * a.B;
   if (u == nullptr) {
     hipLaunchKernelGGL((planned_split_kernel<D, G, 0, PAGED>), dim3(n_pass), blk, 0, s, a, pa, kvskip_update_args{});
     return hipGetLastError();

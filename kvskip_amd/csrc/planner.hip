@@ -402,82 +402,17 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   }
 }
 
-// One wavefront per (b, KV head): merge the C = ceil(nb / 32) partials (lane l: chunks l, l + 64,
-// ...), decide, and compact the list from the chunk masks (prefix over lanes, ascending).
+// One wavefront per (b, KV head): the decision from the C = ceil(nb / 32) partials (decide_head,
+// the arithmetic the planned pass's prologue repeats) and the list compacted from the chunk masks.
 template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
-  constexpr int SP = part_stride(G);
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int Tb = seq_T(p.seq_lens, b, p.T);
-  const int nb = (Tb + BLK - 1) / BLK;                            // the sequence's blocks
+  const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
   if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
-  const int C = ((p.T + BLK - 1) / BLK + WCB - 1) / WCB;          // chunks of the scores pass (capacity)
-  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
-  const int fl = p.flags[h];
-  const float* pb = p.part + bh * C * SP;
-  int* bi = p.block_idx + bh * p.NBC;
-  const int age0 = p.age[bh];
-  const float cal0 = (p.calib != nullptr && p.calib_on) ? p.calib[bh] : 0.f;
-  const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + min(lane, G - 1)];
-  constexpr int CL = MAX_NB / WCB / WAVE;  // chunks per lane at capacity
-  float pm[CL][G], ps[CL][G];
-  uint32_t mk[CL];
-#pragma unroll
-  for (int j = 0; j < CL; ++j) {  // every partial first
-    const int cc = min(lane + WAVE * j, C - 1);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      pm[j][g] = pb[cc * SP + g];
-      ps[j][g] = pb[cc * SP + G + g];
-    }
-    mk[j] = __float_as_uint(pb[cc * SP + 2 * G]);
-  }
-  bool tr = false;
-  if (!(fl & 2)) {
-    float miss = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float m = NEG_INF, sv = 0.f;
-#pragma unroll
-      for (int j = 0; j < CL; ++j)
-        if (lane + WAVE * j < C) lse_merge(m, sv, pm[j][g], ps[j][g]);
-      lse_wave(m, sv);
-      if (sv > 0.f) miss = fmaxf(miss, 1.f / (1.f + __expf(lane_value(la, g) - (m + __logf(sv)))));
-    }
-    float dec = miss;
-    if (p.calib != nullptr && p.calib_on)
-      dec = p.calib_kind ? miss + cal0 : 1.f / (1.f + __expf(-(clamped_logit(miss) + cal0)));
-    const int a = age0 + 1;
-    tr = dec > p.delta || a >= p.max_age || (fl & 1);
-    if (lane == 0) {
-      if (p.est != nullptr) p.est[bh] = miss;
-      p.age[bh] = tr ? 0 : a;
-    }
-  }
-  if (lane == 0) p.trig[bh] = tr ? 1 : 0;
-  if (tr) {  // refresh: every block
-    for (int i = lane; i < nb; i += WAVE) bi[i] = i;
-    if (lane == 0) p.block_cnt[bh] = nb;
-    return;
-  }
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < CL; ++j) {
-    if (WAVE * j >= C) break;
-    const int cc = lane + WAVE * j;
-    const uint32_t m0 = cc < C ? mk[j] : 0u;
-    const int n = __popc(m0);
-    int incl = n;  // inclusive prefix over lanes
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int t = __shfl_up(incl, o, WAVE);
-      if (lane >= o) incl += t;
-    }
-    int off = base + incl - n;
-    for (uint32_t m = m0; m != 0; m &= m - 1) bi[off++] = cc * WCB + __ffs(m) - 1;
-    base += __shfl(incl, WAVE - 1, WAVE);
-  }
-  if (lane == 0) p.block_cnt[bh] = base;
+  uint32_t mk[DCL];
+  const bool tr = decide_head<G>(p, b, h, lane, mk, true, true);
+  write_block_list(p, static_cast<int64_t>(b) * p.Hkv + h, nb, tr, mk, lane);
 }
 
 template <int G, int R>

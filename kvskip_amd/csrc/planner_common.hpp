@@ -29,20 +29,15 @@ __device__ __forceinline__ float clamped_logit(float x) {
   return __logf(x) - __logf(1.f - x);
 }
 
-// Merge (m, s) log-sum-exp pairs: (m1, s1) <- (m1, s1) + (m2, s2).
+// Merge (m, s) log-sum-exp pairs: (m1, s1) <- (m1, s1) + (m2, s2); a pair with s <= 0 is empty.
+// Branch-free (selects), so merges of independent pairs interleave.
 __device__ __forceinline__ void lse_merge(float& m1, float& s1, float m2, float s2) {
-  if (s2 <= 0.f) return;
-  if (s1 <= 0.f) {
-    m1 = m2;
-    s1 = s2;
-    return;
-  }
-  if (m2 > m1) {
-    s1 = s1 * __expf(m1 - m2) + s2;
-    m1 = m2;
-  } else {
-    s1 += s2 * __expf(m2 - m1);
-  }
+  const bool h1 = s1 > 0.f, h2 = s2 > 0.f;
+  const float m = h1 ? (h2 ? fmaxf(m1, m2) : m1) : m2;
+  const float a = h1 ? s1 * __expf(m1 - m) : 0.f;
+  const float b = h2 ? s2 * __expf(m2 - m) : 0.f;
+  s1 = (h1 || h2) ? a + b : s1;
+  m1 = (h1 || h2) ? m : m1;
 }
 
 // Whole-wavefront log-sum-exp of per-lane (m, s) pairs: max, then rescaled sums (uniform result).
@@ -73,99 +68,157 @@ __host__ __device__ constexpr int part_stride(int G) { return 2 * G + 1; }  // m
 // Chunks of the scores pass over the capacity T (tokens).
 __device__ __forceinline__ int plan_chunks(int T) { return ((T + BLK - 1) / BLK + WCB - 1) / WCB; }
 
-// The plan's decision for (b, KV head h) from the scores pass's partials: one wavefront, uniform
-// result (src/kvskip_attn.py:366-383, kernels/kvskip_planner.cu:179-201): per query head the
-// log-sum-exp of the estimates over chunks, the missed mass, its calibration, age and flags.
-// mk[j] receives the attended-block mask of chunk lane + 64 j (0 past the chunks). With `write`
-// lane 0 stores est and trig, and the advanced age if `write_age` (a decision repeated by every
-// workgroup of a pass leaves the age to the update: the others still read the old one).
+// The plan's decision for NH lists (b, KV head h) = bh[k] = b * Hkv + h from the scores pass's
+// partials: one wavefront, uniform results (src/kvskip_attn.py:366-383,
+// kernels/kvskip_planner.cu:179-201): per query head the log-sum-exp of the estimates over chunks,
+// the missed mass, its calibration, age and flags. Each (list, query head) pair is reduced by a
+// team of DLP = 8 lanes: lane t of the team merges chunks t, t + 8, ... in order, then the team
+// merges across its lanes (DPP), so the reductions of up to 64 / (8 G) lists run side by side and
+// the arithmetic does not depend on how many lists one call takes. mk[k][j] receives the
+// attended-block mask of chunk lane + 64 j of list k (0 past the chunks). Every load is issued
+// before any is used. With `write` lane 0 stores est and trig, and the advanced age if
+// `write_age` (a decision repeated by every workgroup of a pass leaves the age to the update: the
+// others still read the old one).
+constexpr int DLP = 8;
+
+template <int CTRL>
+__device__ __forceinline__ void lse_dpp(float& m, float& s) {
+  lse_merge(m, s, dpp<CTRL>(m), dpp<CTRL>(s));
+}
+
+template <int G, int NH>
+__device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const int (&bh)[NH], int lane,
+                                             uint32_t (&mk)[NH][DCL], bool (&tr)[NH], bool write,
+                                             bool write_age = true) {
+  constexpr int SP = part_stride(G);
+  constexpr int KW = G * DLP <= WAVE ? WAVE / (G * DLP) : 1;  // lists side by side
+  constexpr int CPL = MAX_NB / WCB / DLP;                      // chunks per team lane at capacity
+  const int C = plan_chunks(p.T);
+  const int pair = lane / DLP, t = lane % DLP;
+  const int kr = pair / G, g = pair % G;  // this lane's list (within a round) and query head
+  int fl[NH], age0[NH];
+  float cal0[NH];
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    const float* pb = p.part + static_cast<int64_t>(bh[k]) * C * SP;
+#pragma unroll
+    for (int j = 0; j < DCL; ++j) mk[k][j] = __float_as_uint(pb[min(lane + WAVE * j, C - 1) * SP + 2 * G]);
+  }
+  // The per-list values are the same on every lane; read through an index the compiler takes for a
+  // per-lane one, they stay in vector registers, where a uniform value would be moved to a scalar
+  // register (a wait for its load) before the next loads were issued.
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    int v = bh[k];
+    asm volatile("" : "+v"(v));
+    age0[k] = p.age[v];
+    cal0[k] = (p.calib != nullptr && p.calib_on) ? p.calib[v] : 0.f;
+    fl[k] = p.flags[v % p.Hkv];
+  }
+  float miss[NH];
+#pragma unroll
+  for (int r = 0; r < NH; r += KW) {
+    const int k = min(r + kr, NH - 1);
+    int v = bh[k];
+    asm volatile("" : "+v"(v));
+    const int b = v / p.Hkv, h = v - b * p.Hkv;
+    const float* pb = p.part + static_cast<int64_t>(v) * C * SP;
+    const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + g];
+    const int NI = (C + DLP - 1) / DLP;  // chunk rounds of the team (uniform)
+    float pm[CPL], ps[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {  // clamped into the list's chunks; the ones past C are empty
+      pm[i] = NEG_INF;
+      ps[i] = 0.f;
+      if (i < NI) {
+        const int c = t + DLP * i, cc = min(c, C - 1);
+        const float mv = pb[cc * SP + g], sv = pb[cc * SP + G + g];
+        pm[i] = c < C ? mv : NEG_INF;
+        ps[i] = c < C ? sv : 0.f;
+      }
+    }
+    float m = NEG_INF, sv = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      if (i < NI) lse_merge(m, sv, pm[i], ps[i]);
+    lse_dpp<DPP_XOR1>(m, sv);
+    lse_dpp<DPP_XOR2>(m, sv);
+    lse_dpp<DPP_HALF_MIRROR>(m, sv);
+    const float e = sv > 0.f ? 1.f / (1.f + __expf(la - (m + __logf(sv)))) : 0.f;
+#pragma unroll
+    for (int q = 0; q < KW; ++q) {
+      if (r + q < NH) {
+        float mx = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) mx = fmaxf(mx, lane_value(e, DLP * (q * G + gg)));
+        miss[r + q] = mx;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+#pragma unroll
+    for (int j = 0; j < DCL; ++j)
+      if (lane + WAVE * j >= C) mk[k][j] = 0u;
+    float dec = miss[k];
+    if (p.calib != nullptr && p.calib_on)
+      dec = p.calib_kind ? miss[k] + cal0[k] : 1.f / (1.f + __expf(-(clamped_logit(miss[k]) + cal0[k])));
+    const int a = age0[k] + 1;
+    const bool ix = (fl[k] & 2) != 0;  // a token-index list never refreshes
+    tr[k] = !ix && (dec > p.delta || a >= p.max_age || (fl[k] & 1));
+    if (write && lane == 0) {
+      if (!ix && p.est != nullptr) p.est[bh[k]] = miss[k];
+      if (!ix && write_age) p.age[bh[k]] = tr[k] ? 0 : a;
+      p.trig[bh[k]] = tr[k] ? 1 : 0;
+    }
+  }
+}
+
 template <int G>
 __device__ __forceinline__ bool decide_head(const kvskip_plan_args& p, int b, int h, int lane, uint32_t (&mk)[DCL],
                                             bool write, bool write_age = true) {
-  constexpr int SP = part_stride(G);
-  const int C = plan_chunks(p.T);
-  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
-  const int fl = p.flags[h];
-  const float* pb = p.part + bh * C * SP;
-  const int age0 = p.age[bh];
-  const float cal0 = (p.calib != nullptr && p.calib_on) ? p.calib[bh] : 0.f;
-  const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + min(lane, G - 1)];
-  float pm[DCL][G], ps[DCL][G];
+  const int bh[1] = {b * p.Hkv + h};
+  uint32_t m[1][DCL];
+  bool tr[1];
+  decide_heads<G, 1>(p, bh, lane, m, tr, write, write_age);
 #pragma unroll
-  for (int j = 0; j < DCL; ++j) {  // every partial first
-    const int cc = min(lane + WAVE * j, C - 1);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      pm[j][g] = pb[cc * SP + g];
-      ps[j][g] = pb[cc * SP + G + g];
-    }
-    mk[j] = __float_as_uint(pb[cc * SP + 2 * G]);
-  }
-#pragma unroll
-  for (int j = 0; j < DCL; ++j)
-    if (lane + WAVE * j >= C) mk[j] = 0u;
-  bool tr = false;
-  if (!(fl & 2)) {
-    float miss = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float m = NEG_INF, sv = 0.f;
-#pragma unroll
-      for (int j = 0; j < DCL; ++j)
-        if (lane + WAVE * j < C) lse_merge(m, sv, pm[j][g], ps[j][g]);
-      lse_wave(m, sv);
-      if (sv > 0.f) miss = fmaxf(miss, 1.f / (1.f + __expf(lane_value(la, g) - (m + __logf(sv)))));
-    }
-    float dec = miss;
-    if (p.calib != nullptr && p.calib_on)
-      dec = p.calib_kind ? miss + cal0 : 1.f / (1.f + __expf(-(clamped_logit(miss) + cal0)));
-    const int a = age0 + 1;
-    tr = dec > p.delta || a >= p.max_age || (fl & 1);
-    if (write && lane == 0) {
-      if (p.est != nullptr) p.est[bh] = miss;
-      if (write_age) p.age[bh] = tr ? 0 : a;
-    }
-  }
-  if (write && lane == 0) p.trig[bh] = tr ? 1 : 0;
-  return tr;
+  for (int j = 0; j < DCL; ++j) mk[j] = m[0][j];
+  return tr[0];
 }
 
 // Exclusive prefix over the wavefront of the attended blocks in the chunks a lane holds (pre[j]
-// for chunk lane + 64 j, ascending block order); returns the total (uniform).
+// for chunk lane + 64 j, ascending block order; masks past the C chunks are 0, as the decision
+// leaves them); returns the total (uniform). Both chunks' counts go through one scan, packed in the
+// two 16-bit halves (a prefix is at most 64 * 32).
 __device__ __forceinline__ int mask_prefix(const uint32_t (&mk)[DCL], int lane, int C, int (&pre)[DCL]) {
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < DCL; ++j) {
-    pre[j] = base;
-    if (WAVE * j >= C) continue;
-    const int n = __popc(mk[j]);
-    int incl = n;  // inclusive prefix over lanes
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int t = __shfl_up(incl, o, WAVE);
-      if (lane >= o) incl += t;
-    }
-    pre[j] = base + incl - n;
-    base += __shfl(incl, WAVE - 1, WAVE);
-  }
-  return base;
+  static_assert(DCL == 2, "two chunks per lane");
+  (void)lane;
+  (void)C;
+  const int n0 = __popc(mk[0]), n1 = __popc(mk[1]);
+  const int incl = wave_incl_scan(n0 | (n1 << 16));
+  const int tot = __builtin_amdgcn_readlane(incl, WAVE - 1);
+  const int tot0 = tot & 0xFFFF;
+  pre[0] = (incl & 0xFFFF) - n0;
+  pre[1] = tot0 + (incl >> 16) - n1;
+  return tot0 + (tot >> 16);
 }
 
-// List positions [a0 - 1, a1) of the ascending attended blocks whose chunk masks this lane holds
-// (chunk lane + 64 j: mask mk[j], exclusive prefix pre[j] from mask_prefix) into
-// out[pos - a0 + 1]; position -1 (before the list) is the caller's. Signed arithmetic throughout:
-// with an unsigned popcount in the range test, a0 = 0 made a0 - 1 the largest unsigned value and
-// split 0 skipped every chunk, leaving its slice unwritten.
-template <int NCL>
-__host__ __device__ __forceinline__ void slice_positions(const uint32_t (&mk)[NCL], const int (&pre)[NCL], int lane,
-                                                         int a0, int a1, int* out) {
-#pragma unroll
-  for (int j = 0; j < NCL; ++j) {
-    int pos = pre[j];
-    const int n = static_cast<int>(__builtin_popcount(mk[j]));
-    if (pos + n <= a0 - 1 || pos >= a1) continue;
-    for (uint32_t m = mk[j]; m != 0; m &= m - 1, ++pos)
-      if (pos >= a0 - 1 && pos < a1) out[pos - a0 + 1] = (lane + WAVE * j) * WCB + __builtin_ctz(m);
+// List positions [a0 - 1, a1) of the ascending attended blocks, into out[pos - a0 + 1], from the
+// chunk masks and their exclusive prefixes in shared memory (mk[c], pre[c] for the C chunks, as
+// mask_prefix gives them; chunk c holds blocks 32 c + bit), by a team of `stride` threads (this
+// one t): each thread takes blocks t, t + stride, ... and places a marked block at its list
+// position if that falls in the range. Position -1 (before the list) is the caller's. No thread
+// loops over set bits, so a slice costs about C * 32 / stride steps of a few instructions. Signed
+// arithmetic throughout (with an unsigned rank, a0 = 0 would make a0 - 1 the largest value).
+__host__ __device__ __forceinline__ void slice_from_masks(const uint32_t* mk, const int* pre, int C, int a0, int a1,
+                                                          int* out, int t, int stride) {
+  for (int i = t; i < C * WCB; i += stride) {
+    const uint32_t m = mk[i / WCB];
+    const int bit = i % WCB;
+    if ((m >> bit) & 1u) {
+      const int r = pre[i / WCB] + static_cast<int>(__builtin_popcount(m & ((1u << bit) - 1u)));
+      if (r >= a0 - 1 && r < a1) out[r - a0 + 1] = i;
+    }
   }
 }
 

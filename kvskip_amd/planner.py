@@ -28,6 +28,7 @@ from . import kvskip as K
 
 TILE = 64
 MARGIN = 64                      # spare block capacity of the state (src/kvskip_attn.py:399)
+BALANCE_MAX_LISTS = 16           # (b, KV head) lists a balanced planned pass decides in every workgroup
 KINDS = {"logit": 0, "add": 1, "peak": 2}
 
 
@@ -117,12 +118,16 @@ class FusedPlanner:
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
-                 decide_in_pass: bool = True):
+                 decide_in_pass: bool = True, balance: bool = True):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
         # plan's decision inside the masked pass (batches without seq_lens): one launch fewer per
         # step, the same decisions and lists as plan's own decision launch
         self.decide_in_pass = decide_in_pass
+        # with the decision in the pass and B * Hkv <= 16: the lists of all heads cut by one chunk
+        # length (kvskip_plan_args.pass_budget), so a refreshing head gets more workgroups than a
+        # light one; the partials get twice the split count's slots
+        self.balance = balance
         self._pargs = None
         self._pg = {}               # this step's paged cache (block_table, T), if any
         self.state = None
@@ -182,6 +187,9 @@ class FusedPlanner:
         B, Hq, D = q.shape
         Hkv = k.shape[1]
         S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb)
+        budget = 0
+        if self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
+            budget, S = S * B * Hkv, min(2 * S, 256)          # S: partial slots per head
         n_st, n_part = B * Hq * self.NBC, B * Hq * S * D
         b = self.bufs
         if b is None or b["blk_max"].numel() < n_st or b["part_acc"].numel() < n_part or b["out"].shape != q.shape:
@@ -195,6 +203,7 @@ class FusedPlanner:
         self._S = S
         carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         if self._pargs is not None:
+            self._pargs.pass_budget = budget
             E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens, **pg)
         elif carried is not None:
             E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens, **pg)

@@ -1,7 +1,8 @@
 // Host check of the planner's list arithmetic shared with the attention kernels (compiled and run
-// on the CPU by tests/test_list_slice.py): slice_positions, which builds a split's slice of the
-// block list from the chunk masks in the planned pass's prologue, against the list built directly,
-// for every split of random masks; gap_range, which bounds the statistics writes between list
+// on the CPU by tests/test_list_slice.py): slice_from_masks, which builds a split's slice of the
+// block list from the chunk masks in the planned pass's prologue (every thread of the workgroup a
+// share of the blocks), against the list built directly, for every split of random masks and
+// teams of several sizes; gap_range, which bounds the statistics writes between list
 // entries, against the blocks strictly between two entries, and on entries of any value.
 #include <climits>
 #include <cstdio>
@@ -53,15 +54,8 @@ int main() {
       const int per = (cnt + S - 1) / S;
       const int a0 = std::min(cnt, split * per), a1 = std::min(cnt, a0 + per);
       std::vector<int> out(MAX_NB + 2, SENT);
-      for (int lane = 0; lane < WAVE; ++lane) {
-        uint32_t mk[DCL];
-        int pr[DCL];
-        for (int j = 0; j < DCL; ++j) {
-          mk[j] = mask[lane + WAVE * j];
-          pr[j] = pre[lane + WAVE * j];
-        }
-        slice_positions<DCL>(mk, pr, lane, a0, a1, out.data());
-      }
+      const int C = (nb + WCB - 1) / WCB, stride = it % 3 == 0 ? 256 : 1 + static_cast<int>(rnd() % 300);
+      for (int t = 0; t < stride; ++t) slice_from_masks(mask.data(), pre.data(), C, a0, a1, out.data(), t, stride);
       if (a0 == 0) out[0] = -1;
       for (int pos = a0 - 1; pos < a1; ++pos)
         CHECK(out[pos - a0 + 1] == (pos < 0 ? -1 : list[pos]), "slice nb %d S %d split %d pos %d: %d", nb, S, split,

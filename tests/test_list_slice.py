@@ -1,6 +1,6 @@
 """CPU: the list arithmetic shared by the attention kernels, compiled for the host and run
 (tests/list_slice_check.hip): the planned pass's per-split slice of the block list built from the
-chunk masks (every split of random masks, split 0 included) and the bounds of the statistics
+chunk masks by a team of threads (every split of random masks, split 0 included) and the bounds of the statistics
 writes between list entries (exact for valid entries, inside the head for any entry value)."""
 
 import os
