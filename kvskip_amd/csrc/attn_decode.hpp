@@ -147,8 +147,8 @@ __device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, 
       ml[1] = 0.f;
     }
   }
-  __syncthreads();
   if (!dense) {  // this workgroup's slice, positions i0 - 1 .. i0 + n - 1, by every thread
+    __syncthreads();  // the masks and prefixes in LDS
     slice_from_masks(sMk, sPre, plan_chunks(pa.T), i0, i0 + n, sPl, threadIdx.x, NT);
     if (threadIdx.x == 0 && i0 == 0) sPl[0] = -1;
     __syncthreads();

@@ -189,7 +189,11 @@ class FusedPlanner:
         S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb)
         budget = 0
         if self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
-            budget, S = S * B * Hkv, min(2 * S, 256)          # S: partial slots per head
+            # workgroups: S per head less the partition's B*Hkv spare chunks and room for a carried
+            # update of this shape, so that the pass fits the CUs the per-head split fills (a CU
+            # given a second full chunk would double the critical path); the same with and without
+            # a carried update, so both cut the lists alike. S becomes the partial slots per head.
+            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 256)
         n_st, n_part = B * Hq * self.NBC, B * Hq * S * D
         b = self.bufs
         if b is None or b["blk_max"].numel() < n_st or b["part_acc"].numel() < n_part or b["out"].shape != q.shape:
