@@ -563,7 +563,7 @@ def pmc_paths(q, ks, vs, scale, bi, bc, dev):
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
-                  Hkv=8, ragged=None, dense_layer0=True, seed=4):
+                  Hkv=8, ragged=None, dense_layer0=True, seed=4, p_jump=0.03):
     """The device-side planner loop over `layers` attention layers for `steps` decode steps (one
     token appended per step and sequence), query drift + jumps, stage-4 policy (delta 0.05, max
     age 32, calibration 0.05 peak, warm-up (32, 8), token-index latch at 0.1;
@@ -582,7 +582,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     t_gen = time.perf_counter()
     run = W.planner_run(layers=layers, B=B, Hq=Hq, Hkv=Hkv, T0=T0, steps=steps, seed=seed, ragged=ragged, device=dev)
     _, _, Tcap, D = run.k[0].shape
-    qps = [W.QueryProcess(run, l, noise=noise, revert=revert) for l in range(layers)]
+    qps = [W.QueryProcess(run, l, p_jump=p_jump, noise=noise, revert=revert) for l in range(layers)]
     qs = torch.stack([torch.stack([qps[l].next() for l in range(layers)]) for _ in range(steps)]).to(dev)
     ids = run.ids.to(dev)
     if ragged is None:
@@ -679,6 +679,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
         if ragged is None and B == 1 else (math.nan, 0)
     out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
            "T0": T0 if ragged is None else list(ragged), "query_noise": noise, "query_revert": revert,
+           "query_jump_prob": p_jump,
            "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)"
                      + (", layer 0 dense" if dense_layer0 else ""),
            "blocks_read_frac": read / total,

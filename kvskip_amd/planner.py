@@ -118,7 +118,7 @@ class FusedPlanner:
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
-                 decide_in_pass: bool = True, balance: bool = True):
+                 decide_in_pass: bool = True, balance: bool = True, batch_balance: bool = True):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
         # plan's decision inside the masked pass (batches without seq_lens): one launch fewer per
@@ -128,6 +128,11 @@ class FusedPlanner:
         # length (kvskip_plan_args.pass_budget), so a refreshing head gets more workgroups than a
         # light one; the partials get twice the split count's slots
         self.balance = balance
+        # a batch of B > 1 with more than BALANCE_MAX_LISTS lists: the lists are cut over the batch
+        # (the ragged partition, each KV head's lists of all sequences together) by passing the
+        # lengths, all T, as seq_lens; a refreshing head of one sequence then no longer sets the
+        # pass's time alone
+        self.batch_balance = batch_balance
         self._pargs = None
         self._pg = {}               # this step's paged cache (block_table, T), if any
         self.state = None
@@ -161,6 +166,7 @@ class FusedPlanner:
             aix=torch.zeros(B, Hkv, dtype=torch.uint8, device=dev),
             idx=torch.zeros(B, NBC, dtype=torch.uint8, device=dev),
             tlen=torch.zeros(B, dtype=torch.int32, device=dev),       # this step's lengths (ragged)
+            lens=torch.zeros(B, dtype=torch.int32, device=dev),       # all T, for batch_balance
             part=torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), **f32),     # multi-workgroup plan
         )
 
@@ -250,6 +256,15 @@ class FusedPlanner:
     def _age(self):
         return dict(age=self.state["age"]) if self._pargs is not None else {}
 
+    def _batch_lens(self, B, Hkv, T, seq_lens, block_table):
+        """seq_lens, or (batch_balance, B > 1, more than BALANCE_MAX_LISTS lists, contiguous cache)
+        the state's length buffer filled with T, so the passes cut the lists over the batch."""
+        if (seq_lens is not None or block_table is not None or not self.batch_balance or B < 2
+                or B * Hkv <= BALANCE_MAX_LISTS):
+            return seq_lens
+        self.state["lens"].fill_(T)
+        return self.state["lens"]
+
     def _tlen(self, seq_lens):
         """The update's lengths: the plan's copy of seq_lens in the planner's state (rewritten only
         by this layer's next plan), so a carried update reads this step's lengths even after the
@@ -295,6 +310,7 @@ class FusedPlanner:
         self.flush()
         self._alloc(q, k, nb + MARGIN)
         s = self.state
+        seq_lens = self._batch_lens(B, Hkv, T, seq_lens, block_table)
         E.block_sums(k, self.NBC, out=s["csum"], seq_lens=seq_lens, **self._pg)
         every = torch.ones(Hkv, dtype=torch.int32, device=q.device)      # refresh all, no index heads
         pol = self.policy
@@ -308,7 +324,7 @@ class FusedPlanner:
                       float(pol.level), int(pol.local), every),
                      dict(list_stats=True, seq_lens=self._tlen(seq_lens), **self._age()))
         self.t, self.T = 0, T
-        self.ragged = seq_lens is not None
+        self.ragged = seq_lens is not None and seq_lens is not s["lens"]
         if self.count:
             total = B * Hkv * nb if seq_lens is None else ((seq_lens + TILE - 1) // TILE).sum() * Hkv
             self._count("dense_heads", B * Hkv)
@@ -343,6 +359,7 @@ class FusedPlanner:
                 E.block_sums(k, self.NBC, out=s["csum"], **self._pg)  # several tokens appended: resum
         self.t += 1
         self.T = T
+        seq_lens = self._batch_lens(B, Hkv, T, seq_lens, block_table)
         fuse_ix = pol.needs_index and ids is not None and idx is None     # the plan finds the index itself
         if fuse_ix:
             _require_ids(ids, T)

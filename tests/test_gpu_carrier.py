@@ -102,6 +102,37 @@ def test_decode_splits_update_rejects_group_mismatch(gpu):
         E.decode_splits_update(q2, k, k, 0.125, bufs, bi, bc, 2, u)
 
 
+@pytest.mark.parametrize("carry", [False, True])
+def test_batch_balanced_partition(gpu, carry):
+    """B 3 x 8 KV heads (24 lists, over the balanced pass's 16): the planner passes the lengths (all
+    T) as seq_lens, so the ragged partition cuts each KV head's lists over the batch. Against the
+    per-(sequence, head) split (batch_balance=False): identical state on every step, outputs to
+    float rounding."""
+    layers, B, Hkv, G, D, T0, steps = 2, 3, 8, 4, 64, 1900, 6
+    run = W.planner_run(layers=layers, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=T0, steps=steps, seed=77)
+    ks = [k.cuda() for k in run.k]
+    vs = [v.cuda() for v in run.v]
+    ids = run.ids.to(torch.int32).cuda()
+    qps = [W.QueryProcess(run, l, p_jump=0.1, revert=True) for l in range(layers)]
+    qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
+    pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
+    cr = [UpdateCarrier(), UpdateCarrier()] if carry else [None, None]
+    ref = [FusedPlanner(pol(), count=False, carrier=cr[0], batch_balance=False) for _ in range(layers)]
+    dut = [FusedPlanner(pol(), count=False, carrier=cr[1]) for _ in range(layers)]
+    for t in range(steps):
+        T = T0 + t + 1
+        for l in range(layers):
+            kv = (ks[l][:, :, :T], vs[l][:, :, :T])
+            outs = [(fp.first(qs[t][l], *kv, run.scale) if t == 0 else fp.step(qs[t][l], *kv, run.scale, ids=ids)).clone()
+                    for fp in (ref[l], dut[l])]
+            a, b = outs[0].float(), outs[1].float()
+            assert float((a - b).norm() / b.norm()) <= 1e-3, (t, l)
+        for c in cr:
+            if c is not None:
+                c.flush()
+        _same_state(ref, dut, t)
+
+
 @pytest.mark.parametrize("B,Hkv,G", [(2, 8, 2), (1, 12, 8), (4, 4, 4), (1, 1, 7)])
 def test_balanced_pass_many_lists(gpu, B, Hkv, G):
     """The balanced planned pass (every workgroup decides all B * Hkv lists: 16, 12, 16 and 1 here,
