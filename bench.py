@@ -352,6 +352,18 @@ def main():
         res["planner_b8"] = bench_planner(dev, layers=args.planner_layers, T0=32768, B=8,
                                           steps=min(args.planner_steps, 64), tag="b8")
         torch.cuda.empty_cache()
+        # the same batch with queries that stay on their planted blocks and re-aim rarely (0.3% per
+        # query head and step): the regime where the reference reports its planner's gain
+        # (README.md:100-105, attention time -33% at batch 8 / 32k)
+        res["planner_b8_stable"] = bench_planner(dev, layers=args.planner_layers, T0=32768, B=8,
+                                                 steps=min(args.planner_steps, 64), revert=True, p_jump=0.003,
+                                                 tag="b8-stable")
+        torch.cuda.empty_cache()
+        # the reference's largest point (batch 32 at 64k, README.md:100-105), 4 layers (8.6 GB of K / V
+        # each) x 32 steps, stable queries
+        res["planner_b32_64k_stable"] = bench_planner(dev, layers=4, T0=65536, B=32, steps=min(args.planner_steps, 32),
+                                                      revert=True, p_jump=0.003, chunk=8, tag="b32-64k-stable")
+        torch.cuda.empty_cache()
         # config 5: batch 16 of Qwen2.5-7B layers (28 / 4 heads, G 7), contexts log-uniform in
         # [4096, 65536], 28 layers, ragged split-K over the batch
         g5 = torch.Generator().manual_seed(5)
@@ -687,6 +699,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
            "us_per_layer_step_policy_update_own_launch": us_plan_own / n,
            "us_per_layer_step_policy_one_graph_replayed": us_replay / n_replay if n_replay else None,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
+           "dense_GBs": (B * Hkv * (T0 + steps // 2) * D * 4 / (us_dense / n) / 1e3) if ragged is None else None,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
     log(f"{tag}: policy {us_plan / n:.2f} us/layer-step (updates carried; {us_plan_own / n:.2f} with their own "
