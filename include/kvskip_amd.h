@@ -208,6 +208,28 @@ int kvskip_plan(const kvskip_plan_args* p, void* stream);
  * reference: with kvskip_decode_splits_planned after it, the decision runs inside the masked pass. */
 int kvskip_plan_scores(const kvskip_plan_args* p, void* stream);
 
+/* A decision launch after kvskip_plan_scores(p) (same arguments, needs part), by mode:
+ *   KVSKIP_DECIDE_PLAN  plan's second launch: the decision (trig, est, age) and the list to read,
+ *                       every block of a refreshing head or the attended set (kvskip_plan with part
+ *                       is kvskip_plan_scores followed by this).
+ *   KVSKIP_DECIDE_LISTS block_idx / block_cnt = the attended set of every head (stored set + block 0
+ *                       + the `local` newest, + the index blocks of an index-union head): the list
+ *                       of the refresh mode's masked pass. trig, est and age are not written.
+ *   KVSKIP_DECIDE_POST  the decision with lse_att = the log-sum-exp of THIS step's pass over the
+ *                       attended set (the lse output of that kvskip_decode): est, trig and the
+ *                       advanced age as kvskip_plan writes them; block_idx / block_cnt = every block
+ *                       of a refreshing head and none (count 0) of the others: the list of the
+ *                       refresh pass. The stored set and the partials are only read, so LISTS, the
+ *                       masked pass and POST may follow one scores pass.
+ * LISTS and POST replace the torch steps of the reference's "refresh" mode around its two decode
+ * calls: make_plan of the stored set (src/kvskip_attn.py:233-238), the estimate and trigger after
+ * the pass (src/kvskip_attn.py:241-254) and make_plan of the refreshing heads
+ * (src/kvskip_attn.py:259-263). Not in the reference's C++ interface. */
+#define KVSKIP_DECIDE_PLAN 0
+#define KVSKIP_DECIDE_LISTS 1
+#define KVSKIP_DECIDE_POST 2
+int kvskip_plan_decide(const kvskip_plan_args* p, int32_t mode, void* stream);
+
 /* Floats of kvskip_plan_args.part for a state of capacity NBC blocks (-1 for invalid sizes).
  * Not in the reference: sizes the optional multi-workgroup plan workspace. */
 int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC);

@@ -13,9 +13,12 @@ on KVSKIP.mode (layers in dense_layers always run dense):
                    statistics pass -> update, no host synchronisation); "refresh_pre" is accepted
                    as the same loop: the fused loop reproduces that mode's decisions
                    (src/kvskip_attn.py:399-478), here on the device from the first step on
+  "refresh"        the trigger decided after a masked pass over the stored sets, against that
+                   pass's log-sum-exp, with a dense + statistics pass for the refreshing heads
+                   (src/kvskip_attn.py:215-270; planner.PostPlanner, on the device, no host
+                   synchronisation where the reference syncs once per step to skip an empty
+                   second pass)
   "replay"         masked + statistics decode over KVSKIP.plans[layer][t] (one kvskip.Plan per step)
-The reference's "refresh" mode (a host-side torch planner, src/kvskip_attn.py:215-270) is not on
-this path and raises.
 
 Not in the reference: KVSKIP.ids (token ids [B, >= T] int32 on the device) lets the planner find the
 token index itself instead of reading idx_blocks, and KVSKIP.carry lets each layer's planner update
@@ -32,7 +35,7 @@ import torch
 import torch.nn.functional as F
 
 from . import kvskip as K
-from .planner import FusedPlanner, Policy, UpdateCarrier
+from .planner import FusedPlanner, Policy, PostPlanner, UpdateCarrier
 
 BLOCK = 64
 
@@ -175,8 +178,17 @@ def _replay(layer, q, k, v, scale):
     return K.decode(q, k, v, scale, plan=plan, stats=True)["out"]
 
 
-def _no_host_planner(layer, q, k, v, scale):
-    raise ValueError("mode 'refresh' (the host-side torch planner) is not provided; use 'refresh_fused'")
+def _refresh_post(layer, q, k, v, scale):
+    """Mode "refresh" (src/kvskip_attn.py:215-270): the layer's PostPlanner; its device counters are
+    the layer's."""
+    st = KVSKIP.state.setdefault(layer, {})
+    pp = st.get("post")
+    if pp is None:
+        pp = st["post"] = PostPlanner(KVSKIP.policy(layer), count=KVSKIP.count)
+        if KVSKIP.count:
+            KVSKIP.log[layer] = pp.counters
+        return pp.first(q, k, v, scale)
+    return pp.step(q, k, v, scale)
 
 
 # Decode-step handlers by KVSKIP.mode (src/kvskip_attn.py:487-513).
@@ -188,7 +200,7 @@ MODES = {
     "refresh_fused": _refresh,
     "refresh_pre": _refresh,
     "replay": _replay,
-    "refresh": _no_host_planner,
+    "refresh": _refresh_post,
 }
 
 

@@ -405,3 +405,91 @@ class FusedPlanner:
         m = torch.zeros(B, H, n + 1, dtype=torch.bool, device=bi.device)
         m.scatter_(-1, torch.where(valid, bi.long(), n), True)
         return m[..., :nb]
+
+
+class PostPlanner(FusedPlanner):
+    """The reference's "refresh" mode (src/kvskip_attn.py:215-270) on the device: the trigger is
+    decided AFTER a masked pass over the stored sets, against that pass's own log-sum-exp, and the
+    refreshing heads then get a dense + statistics pass whose output replaces their masked one.
+    Per later step, all on the current stream with no host synchronisation: plan's scores pass
+    (estimate partials, the appended key's sum) -> the attended sets' lists -> masked split pass
+    (no statistics; writes the lse the decision reads) -> the decision and the refresh pass's lists
+    (every block of a refreshing head, none of the others) -> dense + statistics split pass -> the
+    two outputs joined per head -> update of the refreshing heads. The first step is
+    FusedPlanner.first (dense + statistics and the state initialisation, src/kvskip_attn.py:223-231).
+    The mode has no calibration, token index or warm-up age, and takes contiguous caches without
+    seq_lens (as the reference's, which reads k.shape[2] as every sequence's length)."""
+
+    def __init__(self, policy: Policy, count: bool = True):
+        if (policy.calib is not None or policy.index_heads or policy.calib_warm
+                or policy.calib_auto_ix is not None):
+            raise ValueError("the refresh mode has no calibration, token index or warm-up age")
+        super().__init__(policy, count, carrier=None, decide_in_pass=False, balance=False, batch_balance=False)
+        self.post = None
+
+    def _post_bufs(self, q, S, nb):
+        """The two passes' buffers: out / lse of the masked pass, out2 / lse2 + statistics of the
+        refresh pass, shared split partials (the passes run one after the other)."""
+        B, Hq, D = q.shape
+        p = self.post
+        n_st = B * Hq * self.NBC
+        if p is None or p["blk_max"].numel() < n_st or p["part_acc"].numel() < B * Hq * S * D or p["out"].shape != q.shape:
+            dev = q.device
+            f32 = dict(dtype=torch.float32, device=dev)
+            p = self.post = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
+                                 lse=torch.empty(B, Hq, **f32),
+                                 out2=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
+                                 lse2=torch.empty(B, Hq, **f32),
+                                 blk_max=torch.empty(n_st, **f32), blk_sum=torch.empty(n_st, **f32),
+                                 part_acc=torch.empty(B * Hq * S * D, **f32), part_ml=torch.empty(B * Hq * S * 2, **f32))
+        first = dict(out=p["out"], lse=p["lse"], part_acc=p["part_acc"], part_ml=p["part_ml"])
+        second = dict(out=p["out2"], lse=p["lse2"], blk_max=p["blk_max"], blk_sum=p["blk_sum"],
+                      part_acc=p["part_acc"], part_ml=p["part_ml"])
+        return first, second
+
+    def step(self, q, k, v, scale, seq_lens=None, block_table=None, T=None):
+        """One decode step (k, v grown by one token, or several: the key sums are then rebuilt)."""
+        if seq_lens is not None or block_table is not None:
+            raise ValueError("the refresh mode takes a contiguous cache without seq_lens")
+        if self.state is None:
+            return self.first(q, k, v, scale)
+        if q.dim() == 4:
+            q = q.squeeze(2)
+        B, Hq, D = q.shape
+        Hkv, T = k.shape[1], k.shape[2]
+        G = Hq // Hkv
+        nb = math.ceil(T / TILE)
+        dev = q.device
+        if nb > self.NBC:
+            self._grow(nb + MARGIN)
+        s = self.state
+        pol = self.policy
+        add_token = T == self.T + 1
+        if not add_token and T != self.T:
+            E.block_sums(k, self.NBC, out=s["csum"])
+        self.t += 1
+        self.T = T
+        S = K.num_splits_for(B * Hkv, nb)
+        first, second = self._post_bufs(q, S, nb)
+        pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], first["lse"], s["age"],
+                              s["flags"], s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale),
+                              float(pol.delta), int(pol.max_age), int(pol.local), add_token, est=s["est"],
+                              part=s["part"])
+        E.plan_scores(pargs, dev)
+        E.plan_decide(pargs, E.DECIDE_LISTS, dev)
+        if self.count:
+            self._count("blocks_read", s["block_cnt"].sum())
+        E.decode_into(q, k, v, scale, first, s["block_idx"], s["block_cnt"], stats=False, num_splits=S)
+        E.plan_decide(pargs, E.DECIDE_POST, dev)
+        E.decode_into(q, k, v, scale, second, s["block_idx"], s["block_cnt"], stats=True, num_splits=S)
+        out = torch.where(s["trig"].bool().repeat_interleave(G, 1)[..., None], second["out"], first["out"])
+        n = B * Hq * nb
+        E.update(second["blk_max"][:n].view(B, Hq, nb), second["blk_sum"][:n].view(B, Hq, nb), s["trig"],
+                 s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T, float(pol.level),
+                 int(pol.local), s["flags"], list_stats=True)
+        if self.count:
+            self._count("blocks_read", s["block_cnt"].sum())
+            self._count("blocks_total", B * Hkv * nb)
+            self._count("masked_heads", B * Hkv)
+            self._count("dense_heads", s["trig"].sum())
+        return out

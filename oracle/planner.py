@@ -254,6 +254,36 @@ def step(st: State, q, k, v, policy: Policy, idx=None, dtype=torch.float64):
     return out, pr
 
 
+def post_step(st: State, q, k, v, policy: Policy, dtype=torch.float64):
+    """One decode step after the first of the reference's "refresh" mode (src/kvskip_attn.py:233-270):
+    attend the stored set + sink + local blocks, then decide with THIS step's attended
+    log-sum-exp (not the previous step's, as refresh_pre_step does) and give each refreshing head
+    a dense + statistics pass whose output replaces its masked one; the refreshing heads' sets and
+    references are rebuilt from that pass (src/kvskip_attn.py:182-198). The mode knows no
+    calibration, token index or warm-up age (src/kvskip_attn.py:251-254): policy must have none.
+    Reuses plan() with st.lse_att set to the pass's log-sum-exp (the estimate, age and trigger
+    arithmetic of src/kvskip_attn.py:241-254 is the same as :366-376) and update() for the rebuild
+    (its attended log-sum-exp is not read by this mode). Returns (out, plan dict + "lse" of the
+    masked pass)."""
+    assert policy.calib is None and not policy.index_heads and not policy.calib_warm \
+        and policy.calib_auto_ix is None, "the refresh mode has no calibration, index or warm-up"
+    update_csum(st, k)
+    nb = A.nblocks(st.T)
+    sel = pad_blocks(st.keep, nb, False) | A.always_keep(nb, policy.local)
+    out, lse = A.decode(q, k, v, st.scale, keep=sel, dtype=dtype)
+    st.lse_att = lse.to(torch.float64)
+    pr = plan(st, q, k, policy)
+    trig = pr["trig"]
+    full = trig[..., None].expand(*trig.shape, nb)
+    out2, _ = A.decode(q, k, v, st.scale, keep=full, dtype=dtype)
+    out = torch.where(A.heads(trig, st.G)[..., None], out2, out)
+    M, S = A.block_stats(q, k, st.scale, keep=full, dtype=dtype)
+    update(st, pr, A.block_logw(M.double(), S.double()), policy)
+    pr["read"] = sel | trig[..., None]
+    pr["lse"] = lse
+    return out, pr
+
+
 # ---------------------------------------------------------------- token index
 
 def index_blocks(ids: np.ndarray, T: int) -> np.ndarray:

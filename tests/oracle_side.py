@@ -32,10 +32,11 @@ def gather_pages(pool: torch.Tensor, table: torch.Tensor, lens) -> list[torch.Te
 
 
 class LayerOracle:
-    """The oracle's refresh_pre loop (OP.init, then OP.step) for one layer of one sequence."""
+    """The oracle's refresh_pre loop (OP.init, then OP.step) for one layer of one sequence; with
+    post, the refresh mode's loop (OP.init, then OP.post_step)."""
 
-    def __init__(self, policy: OP.Policy, scale: float):
-        self.pol, self.scale, self.st = policy, scale, None
+    def __init__(self, policy: OP.Policy, scale: float, post: bool = False):
+        self.pol, self.scale, self.st, self.post = policy, scale, None, post
 
     def step(self, q, k, v, ids=None):
         """q [1, Hq, D], k / v [1, Hkv, T, D] (CPU), ids [1, >= T] token ids (index heads / auto index).
@@ -46,6 +47,9 @@ class LayerOracle:
             Hkv = k.shape[1]
             return (out, torch.ones(1, Hkv, O.nblocks(T), dtype=torch.bool), torch.ones(1, Hkv, dtype=torch.bool),
                     torch.full((1, Hkv), math.inf, dtype=torch.float64))
+        if self.post:
+            out, pr = OP.post_step(self.st, q, k, v, self.pol)
+            return out, pr["read"], pr["trig"], pr["margin"]
         idx = None if ids is None else torch.from_numpy(OP.index_blocks(np.asarray(ids)[:, :T], T))
         out, pr = OP.step(self.st, q, k, v, self.pol, idx=idx)
         return out, pr["read"], pr["trig"], pr["margin"]

@@ -19,7 +19,7 @@ import torch
 from kvskip_amd import ext as E
 from kvskip_amd import kvskip as K
 from kvskip_amd import workloads as W
-from kvskip_amd.planner import FusedPlanner, Policy as DPolicy
+from kvskip_amd.planner import FusedPlanner, Policy as DPolicy, PostPlanner
 from oracle import attention as O
 from oracle import planner as OP
 
@@ -234,6 +234,49 @@ def test_planner_loop(gpu, name):
 def test_planner_loop_gqa7_batch(gpu):
     """Config 5 shape (28 / 4 heads, G 7) at batch 3 with the stage-4 policy."""
     _run_loop(POLICIES["stage4"], G=7, Hkv=4, B=3, T0=2500, steps=30, seed=5, p_jump=0.05)
+
+
+@pytest.mark.parametrize("pol", [OP.Policy(), OP.Policy(delta=0.02, max_age=8, dense_heads=(3,))],
+                         ids=["default", "age8_forced"])
+@pytest.mark.parametrize("B,G,Hkv", [(1, 4, 8), (2, 7, 4)])
+def test_post_planner_loop(gpu, pol, B, G, Hkv):
+    """The refresh mode's device loop (PostPlanner: scores, attended lists, masked pass, decision
+    against that pass's lse, refresh pass, update) against the oracle's post_step, free-running for
+    30 steps with query drift and jumps: refresh decisions identical on every head-step (failures
+    name the oracle's margin), the refresh pass's lists every block of a refreshing head and none of
+    the others, stored sets identical after every step, estimates within 1e-4, outputs within 2e-3."""
+    T0, steps = 4096, 30
+    run = W.planner_run(layers=1, B=B, Hq=G * Hkv, Hkv=Hkv, D=128, T0=T0, steps=steps, seed=6)
+    qp = W.QueryProcess(run, 0, p_jump=0.05)
+    k_cpu, v_cpu = run.k[0], run.v[0]
+    k, v = k_cpu.cuda(), v_cpu.cuda()
+    pp = PostPlanner(dpolicy(pol))
+    st = None
+    n_trig = n_kept = 0
+    margin_min = math.inf
+    max_err = 0.0
+    for t in range(steps):
+        T = T0 + t + 1
+        q = qp.next()
+        nb = O.nblocks(T)
+        if t == 0:
+            out_d = pp.first(q.cuda(), k[:, :, :T], v[:, :, :T], run.scale)
+            st, out_r = OP.init(q, k_cpu[:, :, :T], v_cpu[:, :, :T], run.scale, pol)
+        else:
+            out_d = pp.step(q.cuda(), k[:, :, :T], v[:, :, :T], run.scale)
+            out_r, pr = OP.post_step(st, q, k_cpu[:, :, :T], v_cpu[:, :, :T], pol)
+            s = pp.state
+            margin_min = min(margin_min, _agree(s["trig"].bool().cpu(), pr["trig"], pr["margin"], f"trigger at step {t}"))
+            assert torch.equal(s["block_cnt"].cpu(), torch.where(pr["trig"], nb, 0).to(torch.int32)), t
+            assert (s["est"].double().cpu() - pr["miss"]).abs().max().item() <= 1e-4, t
+            n_trig += int(pr["trig"].sum())
+            n_kept += int((~pr["trig"]).sum())
+        _agree(pp.state["keep"][:, :, :nb].bool().cpu(), st.keep, _kv_margin(st.topp_heads, G), f"stored set at step {t}")
+        max_err = max(max_err, O.rel_err(out_d.float().cpu(), out_r))
+    print(f"post loop {pol}, B {B} G {G}: refreshes {n_trig}, kept {n_kept}, smallest trigger margin "
+          f"{margin_min:.1e}, max rel. output err {max_err:.2e}", flush=True)
+    assert n_trig > 0 and n_kept > 0
+    assert max_err <= 2e-3
 
 
 def test_merge_update_matches_separate_launches(gpu):

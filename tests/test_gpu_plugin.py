@@ -44,8 +44,9 @@ def _data(seed):
     return ks, vs, qs, ids
 
 
-def _drive(cfg, ks, vs, qs, ids=None):
-    """Run the plugin over every layer and step (cache appends included); outputs [step][layer]."""
+def _drive(cfg, ks, vs, qs, ids=None, after=None):
+    """Run the plugin over every layer and step (cache appends included); outputs [step][layer].
+    after(t, l, out): called after each layer's call with its output [B, Hq, D]."""
     A.KVSKIP = cfg
     cache = A.GrowingCache(capacity=T0 + 64)
     mods = [SimpleNamespace(layer_idx=l) for l in range(LAYERS)]
@@ -62,6 +63,8 @@ def _drive(cfg, ks, vs, qs, ids=None):
             o, _ = A.kvskip_attention_forward(mods[l], qs[l][t], kk, vv, None, scaling=SCALE)
             assert o.shape == (B, 1, HQ, D)
             row.append(o[:, 0].clone())
+            if after is not None:
+                after(t, l, row[-1])
         outs.append(row)
     cfg.flush()
     return outs, cache
@@ -157,6 +160,48 @@ def test_refresh_fused_matches_planner_loop(index):
     for l in range(1, LAYERS):
         for key in ("block_idx", "block_cnt", "trig", "age", "keep", "lse_att", "calib", "aix"):
             assert torch.equal(plain_state[l][key], cfg2.state[l]["planner"].state[key]), (l, key)
+
+
+def test_refresh_mode_matches_oracle():
+    """Mode "refresh" (the trigger after the masked pass, src/kvskip_attn.py:215-270) against the
+    oracle's loop of that mode on the same inputs (layer 0 dense): refresh decisions and read sets
+    (the attended set from the device's previous stored set, plus every block of a refreshing head)
+    identical on every head-step, the refresh pass's lists every block of a refreshing head and none
+    of the others, stored sets identical after each step, outputs within 2e-3; the device counters
+    add up the blocks of both passes (src/kvskip_attn.py:256,269)."""
+    ks, vs, qs, _ = _data(35)
+    cfg = A.KvskipConfig(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),))
+    orc = {l: LayerOracle(oracle_policy(cfg.policy(l)), SCALE, post=True) for l in range(1, LAYERS)}
+    prev_keep = {}
+    seen = dict(refresh=0, kept=0, read=0)
+
+    def check(t, l, out):
+        n = T0 + t
+        qc, kc, vc = qs[l][t][:, :, 0].cpu(), ks[l][:, :, :n].cpu(), vs[l][:, :, :n].cpu()
+        if l == 0:
+            rel_ok(out, O.decode(qc, kc, vc, SCALE)[0], (t, l))
+            return
+        o_ref, read, trig, margin = orc[l].step(qc, kc, vc)
+        rel_ok(out, o_ref, (t, l))
+        st = cfg.state[l]["post"].state
+        nb = O.nblocks(n)
+        if t > 0:
+            dev_trig = st["trig"].bool().cpu()
+            sel = torch.nn.functional.pad(prev_keep[l], (0, nb - prev_keep[l].shape[-1])) | O.always_keep(nb, cfg.local)
+            same_decisions(sel | dev_trig[..., None], read, trig, dev_trig, margin, (t, l))
+            assert torch.equal(st["block_cnt"].cpu(), torch.where(trig, nb, 0).to(torch.int32)), (t, l)
+            seen["refresh"] += int(trig.sum())
+            seen["kept"] += int((~trig).sum())
+            # as the reference counts them: the masked pass's blocks, then the refresh pass's
+            seen["read"] += int(sel.sum()) + int(trig.sum()) * nb
+        else:
+            seen["read"] += int(read.sum())
+        prev_keep[l] = st["keep"][:, :, :nb].bool().cpu()
+        assert torch.equal(prev_keep[l], orc[l].st.keep), (t, l)
+
+    _drive(cfg, ks, vs, qs, after=check)
+    assert seen["refresh"] > 0 and seen["kept"] > 0, seen
+    assert int(A.log_totals()["blocks_read"]) == seen["read"], (A.log_totals(), seen)
 
 
 def test_replay_of_recorded_lists():

@@ -444,3 +444,148 @@ def test_topp_margin_per_head():
     M, S = O.block_stats(q, k, 1.0, keep=pr["read"])
     _, margin = O.topp_heads(O.block_logw(M, S), pol.level)
     assert torch.equal(st.topp_heads[0, :4], margin[0, :4]) and torch.isinf(st.topp_heads[0, 4:]).all()
+
+
+# ---------------------------------------------------------------- the "refresh" mode (post trigger)
+
+def _brute_block_lse(q, k, scale, T):
+    """Per query head and block: log-sum-exp of the block's scores, block by block with explicit dot
+    products: [B, Hq, nb]."""
+    B, Hq, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    nb = O.nblocks(T)
+    out = torch.empty(B, Hq, nb, dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hq):
+            for blk in range(nb):
+                rows = k[b, h // G, blk * 64:min(T, blk * 64 + 64)]
+                out[b, h, blk] = torch.logsumexp(scale * (rows @ q[b, h]), 0)
+    return out
+
+
+def _brute_centroid_scores(q, k, scale, T):
+    B, Hq, D = q.shape
+    G = Hq // k.shape[1]
+    nb = O.nblocks(T)
+    out = torch.empty(B, Hq, nb, dtype=torch.float64)
+    for b in range(B):
+        for h in range(Hq):
+            for blk in range(nb):
+                c = k[b, h // G, blk * 64:min(T, blk * 64 + 64)].mean(0)
+                out[b, h, blk] = scale * float(q[b, h] @ c)
+    return out
+
+
+def _post_case(seed):
+    """A layer of 700 tokens (init at fewer, then appended ones) and a drifted query."""
+    q, k, v = _layer(T=700, D=8, seed=seed)
+    q2 = q + 0.6 * rnd(*q.shape, seed=seed + 7)
+    return q, q2, k, v
+
+
+def _post_reference(q, q2, k, v, scale, keep0, local):
+    """Brute-force decision inputs of the step after the refresh at T0 = T - 1: the attended set,
+    its log-sum-exp under THIS step's query, and per KV head the missed-mass estimate
+    sigma(lse(est over the unattended blocks) - lse_sel) maxed over the group, with
+    est_b = lse_ref_b + cs_b(q2, T) - cs_ref_b (references from q at T0)."""
+    T = k.shape[2]
+    G = q.shape[1] // k.shape[1]
+    nb = O.nblocks(T)
+    sel = OP.pad_blocks(keep0, nb, False) | O.always_keep(nb, local)
+    lse_ref = _brute_block_lse(q, k[:, :, :T - 1], scale, T - 1)
+    cs_ref = _brute_centroid_scores(q, k[:, :, :T - 1], scale, T - 1)
+    cs_now = _brute_centroid_scores(q2, k, scale, T)
+    _, lse_sel = brute_decode(q2, k, v, scale, keep=sel)
+    _, lse_old = brute_decode(q, k[:, :, :T - 1], v[:, :, :T - 1], scale, keep=sel)   # the previous step's
+    B, Hq = lse_sel.shape
+    miss = torch.zeros(B, Hq // G, dtype=torch.float64)
+    miss_old = torch.zeros_like(miss)
+    for b in range(B):
+        for h in range(Hq):
+            est = [float(lse_ref[b, h, i] + cs_now[b, h, i] - cs_ref[b, h, i])
+                   for i in range(nb) if not bool(sel[b, h // G, i])]
+            if not est:
+                continue
+            e = torch.logsumexp(torch.tensor(est, dtype=torch.float64), 0)
+            miss[b, h // G] = max(float(miss[b, h // G]), float(torch.sigmoid(e - lse_sel[b, h])))
+            miss_old[b, h // G] = max(float(miss_old[b, h // G]), float(torch.sigmoid(e - lse_old[b, h])))
+    return sel, miss, miss_old, cs_now
+
+
+def test_post_step_decides_on_this_steps_lse():
+    """The refresh mode's estimate (src/kvskip_attn.py:241-251) against brute force, with the
+    log-sum-exp of this step's masked pass; the previous step's (refresh_pre's) gives a clearly
+    different number here, so the test tells them apart. delta set between the two KV heads'
+    estimates: one refreshes (dense output, new set from its full statistics, age 0), the other keeps
+    its masked output (brute-force masked attention), set and age + 1."""
+    scale = 3.0
+    q, q2, k, v = _post_case(80)
+    T = k.shape[2]
+    pol = OP.Policy(delta=0.05, max_age=32)
+    st0, _ = OP.init(q, k[:, :, :T - 1], v[:, :, :T - 1], scale, pol)
+    sel, miss, miss_old, cs_now = _post_reference(q, q2, k, v, scale, st0.keep, pol.local)
+    assert (miss > 0).all() and (miss - miss_old).abs().min() > 1e-3
+    lo, hi = sorted(miss[0].tolist())
+    assert hi - lo > 1e-3
+    pol = OP.Policy(delta=(lo + hi) / 2, max_age=32)
+    st, _ = OP.init(q, k[:, :, :T - 1], v[:, :, :T - 1], scale, pol)
+    keep0 = st.keep.clone()
+    out, pr = OP.post_step(st, q2, k, v, pol)
+    assert torch.allclose(pr["miss"], miss, atol=1e-10)
+    assert torch.equal(pr["sel"], sel)
+    trig = miss > pol.delta
+    assert torch.equal(pr["trig"], trig) and int(trig.sum()) == 1
+    dense = F.scaled_dot_product_attention(q2[:, :, None], k, v, scale=scale, enable_gqa=True)[:, :, 0]
+    masked, _ = brute_decode(q2, k, v, scale, keep=sel)
+    G = 4
+    for h in range(2):
+        ref = dense if bool(trig[0, h]) else masked
+        assert torch.allclose(out[:, h * G:(h + 1) * G], ref[:, h * G:(h + 1) * G], atol=1e-10)
+    # state: the refreshing head's set from its full statistics under q2 (top-p 0.99 union, brute
+    # force), references = this step's block log-sum-exps and centroid scores; the other unchanged
+    h_t, h_k = (0, 1) if bool(trig[0, 0]) else (1, 0)
+    lse_now = _brute_block_lse(q2, k, scale, T)
+    nb = O.nblocks(T)
+    kept = set()
+    for g in range(G):
+        w = torch.softmax(lse_now[0, h_t * G + g], -1).tolist()
+        kept |= brute_topp(w, pol.level)
+    kept |= {0} | set(range(nb - pol.local, nb))
+    assert set(torch.nonzero(st.keep[0, h_t]).flatten().tolist()) == kept
+    assert torch.equal(st.keep[0, h_k], OP.pad_blocks(keep0, nb, False)[0, h_k])
+    rows = slice(h_t * G, (h_t + 1) * G)
+    assert torch.allclose(st.lse_ref[0, rows], lse_now[0, rows], atol=1e-10)
+    assert torch.allclose(st.cs_ref[0, rows], cs_now[0, rows], atol=1e-10)
+    assert int(st.age[0, h_t]) == 0 and int(st.age[0, h_k]) == 1
+
+
+def test_post_step_age_and_forced_heads():
+    """max_age 1: every head refreshes on every step and the output is dense attention (SDPA);
+    delta 1 with a forced head: only that head refreshes, the other keeps its set and its masked
+    output (brute force) over the steps, its age counting up."""
+    scale = 3.0
+    q, q2, k, v = _post_case(80)
+    T = k.shape[2]
+    pol = OP.Policy(max_age=1)
+    st, _ = OP.init(q, k[:, :, :T - 4], v[:, :, :T - 4], scale, pol)
+    for t in range(T - 3, T + 1):
+        out, pr = OP.post_step(st, q2, k[:, :, :t], v[:, :, :t], pol)
+        ref = F.scaled_dot_product_attention(q2[:, :, None], k[:, :, :t], v[:, :, :t], scale=scale,
+                                             enable_gqa=True)[:, :, 0]
+        assert pr["trig"].all() and torch.allclose(out, ref, atol=1e-10)
+    pol = OP.Policy(delta=1.0, max_age=1000, dense_heads=(1,))
+    st, _ = OP.init(q, k[:, :, :T - 4], v[:, :, :T - 4], scale, pol)
+    keep0 = st.keep[0, 0].clone()
+    assert not keep0.all()
+    for i, t in enumerate(range(T - 3, T + 1)):
+        out, pr = OP.post_step(st, q2, k[:, :, :t], v[:, :, :t], pol)
+        assert pr["trig"].tolist() == [[False, True]]
+        nb = O.nblocks(t)
+        sel = OP.pad_blocks(keep0[None, None], nb, False)[0, 0] | O.always_keep(nb, 2)
+        assert torch.equal(pr["sel"][0, 0], sel) and int(st.age[0, 0]) == i + 1 and int(st.age[0, 1]) == 0
+        masked, _ = brute_decode(q2[:, :4], k[:, :1, :t], v[:, :1, :t], scale, keep=sel[None, None])
+        assert torch.allclose(out[:, :4], masked, atol=1e-10)
+        ref = F.scaled_dot_product_attention(q2[:, 4:, None], k[:, 1:, :t], v[:, 1:, :t], scale=scale,
+                                             enable_gqa=True)[:, :, 0]
+        assert torch.allclose(out[:, 4:], ref, atol=1e-10)

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from kvskip_amd import attention as A
+from kvskip_amd.planner import Policy, PostPlanner
 
 
 def test_config_defaults_follow_the_reference():
@@ -60,21 +61,26 @@ def test_prefill_goes_to_sdpa():
 
 def test_decode_route_errors():
     """A decode step never falls back to the CPU: host tensors are refused by the extension's checks;
-    the host planner mode and unknown modes raise."""
+    unknown modes raise; the refresh mode refuses policies it has no rule for."""
     q = torch.randn(1, 8, 1, 64).to(torch.bfloat16)
     k = torch.randn(1, 2, 128, 64).to(torch.bfloat16)
     mod = SimpleNamespace(layer_idx=1)
     saved = A.KVSKIP.mode
     try:
-        for mode in ("refresh", "nonsense"):
-            A.KVSKIP.mode = mode
-            with pytest.raises(ValueError):
-                A.kvskip_attention_forward(mod, q, k, k, None, scaling=0.125)
-        A.KVSKIP.mode = "dense"
-        with pytest.raises(Exception):
+        A.KVSKIP.mode = "nonsense"
+        with pytest.raises(ValueError):
             A.kvskip_attention_forward(mod, q, k, k, None, scaling=0.125)
+        for mode in ("dense", "refresh", "refresh_fused"):
+            A.KVSKIP.reset()
+            A.KVSKIP.mode = mode
+            with pytest.raises(Exception):
+                A.kvskip_attention_forward(mod, q, k, k, None, scaling=0.125)
     finally:
         A.KVSKIP.mode = saved
+        A.KVSKIP.reset()
+    for bad in (dict(calib=0.1), dict(index_heads=(0,)), dict(calib_warm=(4, 2)), dict(calib_auto_ix=0.1)):
+        with pytest.raises(ValueError):
+            PostPlanner(Policy(**bad))
 
 
 def test_register():
