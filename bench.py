@@ -346,6 +346,11 @@ def main():
         res["planner_cfg4_focused"] = bench_planner(dev, layers=args.planner_layers, T0=32768,
                                                     steps=min(args.planner_steps, 64), revert=True,
                                                     tag="cfg4-focused")
+        # the reference's "refresh" mode (trigger after the masked pass, then a dense + statistics
+        # pass for the refreshing heads) on config 4's loop
+        res["planner_cfg4_refresh_mode"] = bench_planner(dev, layers=args.planner_layers, T0=32768,
+                                                         steps=min(args.planner_steps, 64), post=True,
+                                                         tag="cfg4-refresh-mode")
         torch.cuda.empty_cache()
         # the reference's operating point for the planner (README.md:100-105: batch 8 at 32k): config 4's
         # loop with 8 sequences of T 32768
@@ -575,7 +580,7 @@ def pmc_paths(q, ks, vs, scale, bi, bc, dev):
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
-                  Hkv=8, ragged=None, dense_layer0=True, seed=4, p_jump=0.03):
+                  Hkv=8, ragged=None, dense_layer0=True, seed=4, p_jump=0.03, post=False):
     """The device-side planner loop over `layers` attention layers for `steps` decode steps (one
     token appended per step and sequence), query drift + jumps, stage-4 policy (delta 0.05, max
     age 32, calibration 0.05 peak, warm-up (32, 8), token-index latch at 0.1;
@@ -583,13 +588,14 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     Config 5: `ragged` per-sequence prefix lengths (views of a common capacity, seq_lens). One
     eager pass with counters gives the read fraction and refresh rate; the timed passes replay HIP
     graphs of `chunk` steps x all layers (decisions still made on the device) for the planner loop
-    and for dense decode of every layer."""
+    and for dense decode of every layer. post: the reference's "refresh" mode instead (PostPlanner,
+    the trigger after the masked pass; its default policy: delta 0.05, max age 32, no calibration)."""
     import torch
 
     from kvskip_amd import ext as E
     from kvskip_amd import kvskip as K
     from kvskip_amd import workloads as W
-    from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+    from kvskip_amd.planner import FusedPlanner, Policy, PostPlanner, UpdateCarrier
 
     t_gen = time.perf_counter()
     run = W.planner_run(layers=layers, B=B, Hq=Hq, Hkv=Hkv, T0=T0, steps=steps, seed=seed, ragged=ragged, device=dev)
@@ -607,7 +613,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     idx_all = torch.zeros(steps, B, NBC, dtype=torch.uint8, device=dev)
     for t in range(steps):
         E.token_index(ids, T0 + t + 1 if ragged is None else Tcap, NBC, out=idx_all[t], seq_lens=sl_all[t])
-    pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    pol = Policy() if post else Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
     first_planned = 1 if dense_layer0 else 0
     ctx = f"T {T0}" if ragged is None else f"ragged T in [{min(ragged)}, {max(ragged)}], sum {sum(ragged)}"
     log(f"{tag}: {layers} layers x {steps} steps, B {B}, {Hq} / {Hkv} heads, {ctx}, generated in "
@@ -631,12 +637,19 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
             k, v = kv(l, t)
             if t == 0:
                 planners[l].first(qs[t, l], k, v, run.scale, seq_lens=sl_all[t])
+            elif post:
+                planners[l].step(qs[t, l], k, v, run.scale)
             else:
                 planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t], seq_lens=sl_all[t])
 
+    def make(count, carrier):
+        return [None] * first_planned + [PostPlanner(pol, count=count, carrier=carrier) if post else
+                                         FusedPlanner(pol, count=count, carrier=carrier)
+                                         for _ in range(first_planned, layers)]
+
     # eager pass with counters
     carrier = UpdateCarrier()
-    planners = [None] * first_planned + [FusedPlanner(pol, carrier=carrier) for _ in range(first_planned, layers)]
+    planners = make(True, carrier)
     for t in range(steps):
         planner_pass(planners, t)
     carrier.flush()
@@ -678,21 +691,22 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     # timed: updates carried by the next layer's pass (the loop's default form here), then beside
     # the merge of their own layer
     carrier = UpdateCarrier()
-    planners = [None] * first_planned + [FusedPlanner(pol, count=False, carrier=carrier)
-                                         for _ in range(first_planned, layers)]
+    planners = make(False, carrier)
     us_plan = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0), tail=carrier.flush)
     del planners
-    planners = [None] * first_planned + [FusedPlanner(pol, count=False) for _ in range(first_planned, layers)]
+    planners = make(False, None)
     us_plan_own = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
     del planners
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
     us_replay, n_replay = replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0) \
-        if ragged is None and B == 1 else (math.nan, 0)
+        if ragged is None and B == 1 and not post else (math.nan, 0)
     out = {"layers": layers, "steps": steps, "B": B, "Hq": Hq, "Hkv": Hkv,
            "T0": T0 if ragged is None else list(ragged), "query_noise": noise, "query_revert": revert,
            "query_jump_prob": p_jump,
-           "policy": "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)"
+           "mode": "refresh (trigger after the masked pass)" if post else "refresh_pre (trigger before the pass)",
+           "policy": ("delta 0.05, max age 32" if post else
+                      "stage 4 (delta 0.05, max age 32, calib 0.05 peak, warm (32, 8), auto index 0.1)")
                      + (", layer 0 dense" if dense_layer0 else ""),
            "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
@@ -702,8 +716,8 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
            "dense_GBs": (B * Hkv * (T0 + steps // 2) * D * 4 / (us_dense / n) / 1e3) if ragged is None else None,
            "ms_per_decode_step_policy": us_plan / (steps - 1) / 1e3,
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
-    log(f"{tag}: policy {us_plan / n:.2f} us/layer-step (updates carried; {us_plan_own / n:.2f} with their own "
-        f"launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
+    log(f"{tag}: policy {us_plan / n:.2f} us/layer-step ({'refresh mode, ' if post else ''}updates carried; "
+        f"{us_plan_own / n:.2f} with their own launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
         f"{layers}-layer step" + (f"; one graph replayed per step: {us_replay / n_replay:.2f}" if n_replay else ""))
     del run, qs
     return out

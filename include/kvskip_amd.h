@@ -96,6 +96,11 @@ typedef struct kvskip_attn_args {
   const int32_t* block_table;
   int64_t bt_stride;
   int32_t num_pages;
+
+  /* Not in the reference: nonzero = a query head that attends nothing (an empty block list) keeps
+   * out, out_f32 and lse as they are instead of 0 / -inf, so a second pass over some heads' lists
+   * (the refresh mode's dense pass of the refreshing heads) replaces only those heads' results. */
+  int32_t keep_empty;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block
@@ -200,6 +205,13 @@ typedef struct kvskip_plan_args {
    * empty, so the split merge takes num_splits as usual. The grid is pass_budget + B * Hkv
    * workgroups. */
   int32_t pass_budget;
+  /* Read by kvskip_decode_splits_planned only (not in the reference; kvskip_plan_decide takes its
+   * mode as an argument): the decision the pass makes, a KVSKIP_DECIDE_* value. PLAN (0) is plan's;
+   * LISTS reads every head's attended set and writes no trig / est; POST decides against lse_att
+   * (the log-sum-exp of an earlier pass of this step over the attended sets) and reads every block
+   * of a refreshing head and nothing of the others (with kvskip_attn_args.keep_empty in that pass,
+   * the others keep their first-pass output). */
+  int32_t decide_mode;
 } kvskip_plan_args;
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);

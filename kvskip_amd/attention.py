@@ -184,7 +184,8 @@ def _refresh_post(layer, q, k, v, scale):
     st = KVSKIP.state.setdefault(layer, {})
     pp = st.get("post")
     if pp is None:
-        pp = st["post"] = PostPlanner(KVSKIP.policy(layer), count=KVSKIP.count)
+        pp = st["post"] = PostPlanner(KVSKIP.policy(layer), count=KVSKIP.count,
+                                      carrier=KVSKIP.carrier if KVSKIP.carry else None)
         if KVSKIP.count:
             KVSKIP.log[layer] = pp.counters
         return pp.first(q, k, v, scale)

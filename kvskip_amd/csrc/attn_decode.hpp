@@ -88,7 +88,8 @@ __device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, 
   for (int k = 0; k < NH; ++k) lists[k] = min(wave + NWAVE * k, P - 1);
   uint32_t mk[NH][DCL];
   bool tr[NH];
-  decide_heads<G, NH>(pa, lists, lane, mk, tr, bid == 0, false);
+  decide_heads<G, NH>(pa, lists, lane, mk, tr, bid == 0 && pa.decide_mode != DECIDE_LISTS, false);
+  apply_decide_mode<NH>(pa.decide_mode, mk, tr);
 #pragma unroll
   for (int k = 0; k < NH; ++k) {
     int c = 0;
@@ -220,7 +221,8 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       }
       if (wave == 0) {
         int pre[DCL];
-        const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0, false);
+        const int mode = pa->decide_mode;
+        const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0 && mode != DECIDE_LISTS, false, mode);
         const int cnt = t ? nbb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
         if (!t) {
 #pragma unroll

@@ -104,6 +104,7 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->block_table = a->block_table;
   p->bt_stride = a->bt_stride;
   p->num_pages = a->num_pages;
+  p->keep_empty = a->keep_empty != 0 ? 1 : 0;
   return KVSKIP_OK;
 }
 
@@ -412,6 +413,8 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
                                       "separately for a ragged batch)");
   if (a->B != pl->B || a->Hq != pl->Hq || a->Hkv != pl->Hkv || a->T != pl->T || a->D != pl->D)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
+  if (pl->decide_mode < KVSKIP_DECIDE_PLAN || pl->decide_mode > KVSKIP_DECIDE_POST)
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: decide_mode in {0, 1, 2} (got %d)", pl->decide_mode);
   if (pl->pass_budget < 0 || pl->pass_budget > 65536)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: pass_budget in 0..65536");
   if (pl->pass_budget > 0 && a->B * a->Hkv > 16)

@@ -402,14 +402,6 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   }
 }
 
-// What a decision launch after the scores pass writes.
-enum DecideMode {
-  DECIDE_PLAN = 0,   // plan's decision (trig, est, age) and the list to read: every block or the attended set
-  DECIDE_LISTS = 1,  // the attended set's list alone, no decision (trig, est, age untouched)
-  DECIDE_POST = 2,   // the decision against a pass's lse_att, and the refresh pass's list: every block
-                     // of a refreshing head, none of the others
-};
-
 // One wavefront per (b, KV head): the decision from the C = ceil(nb / 32) partials (decide_head,
 // the arithmetic the planned pass's prologue repeats) and the list compacted from the chunk masks.
 template <int G, int MODE>
@@ -430,13 +422,9 @@ __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_arg
       mk[j] = c < C ? m : 0u;
     }
     write_block_list(p, bh, nb, false, mk, lane);
-  } else {
-    const bool tr = decide_head<G>(p, b, h, lane, mk, true, true);
-    if (MODE == DECIDE_PLAN || tr) {
-      write_block_list(p, bh, nb, tr, mk, lane);
-    } else if (lane == 0) {
-      p.block_cnt[bh] = 0;
-    }
+  } else {  // POST: the masks of a head that does not refresh are emptied (count 0)
+    const bool tr = decide_head<G>(p, b, h, lane, mk, true, true, MODE);
+    write_block_list(p, bh, nb, tr, mk, lane);
   }
 }
 

@@ -174,13 +174,36 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
   }
 }
 
+// What a decision after the scores pass yields (kvskip_plan_decide's mode, the planned pass's
+// kvskip_plan_args.decide_mode).
+enum DecideMode {
+  DECIDE_PLAN = 0,   // plan's decision (trig, est, age) and the list to read: every block or the attended set
+  DECIDE_LISTS = 1,  // the attended set's list alone, no decision (trig, est, age untouched)
+  DECIDE_POST = 2,   // the decision against a pass's lse_att, and the refresh pass's list: every block
+                     // of a refreshing head, none of the others
+};
+
+// A decision's lists under a mode: LISTS refreshes nothing (the attended sets), POST empties the
+// list of every head that does not refresh.
+template <int NH>
+__device__ __forceinline__ void apply_decide_mode(int mode, uint32_t (&mk)[NH][DCL], bool (&tr)[NH]) {
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    if (mode == DECIDE_LISTS) tr[k] = false;
+#pragma unroll
+    for (int j = 0; j < DCL; ++j)
+      if (mode == DECIDE_POST && !tr[k]) mk[k][j] = 0u;
+  }
+}
+
 template <int G>
 __device__ __forceinline__ bool decide_head(const kvskip_plan_args& p, int b, int h, int lane, uint32_t (&mk)[DCL],
-                                            bool write, bool write_age = true) {
+                                            bool write, bool write_age = true, int mode = DECIDE_PLAN) {
   const int bh[1] = {b * p.Hkv + h};
   uint32_t m[1][DCL];
   bool tr[1];
   decide_heads<G, 1>(p, bh, lane, m, tr, write, write_age);
+  apply_decide_mode<1>(mode, m, tr);
 #pragma unroll
   for (int j = 0; j < DCL; ++j) mk[j] = m[0][j];
   return tr[0];

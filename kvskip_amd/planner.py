@@ -411,25 +411,31 @@ class PostPlanner(FusedPlanner):
     """The reference's "refresh" mode (src/kvskip_attn.py:215-270) on the device: the trigger is
     decided AFTER a masked pass over the stored sets, against that pass's own log-sum-exp, and the
     refreshing heads then get a dense + statistics pass whose output replaces their masked one.
-    Per later step, all on the current stream with no host synchronisation: plan's scores pass
-    (estimate partials, the appended key's sum) -> the attended sets' lists -> masked split pass
-    (no statistics; writes the lse the decision reads) -> the decision and the refresh pass's lists
-    (every block of a refreshing head, none of the others) -> dense + statistics split pass -> the
-    two outputs joined per head -> update of the refreshing heads. The first step is
-    FusedPlanner.first (dense + statistics and the state initialisation, src/kvskip_attn.py:223-231).
-    The mode has no calibration, token index or warm-up age, and takes contiguous caches without
-    seq_lens (as the reference's, which reads k.shape[2] as every sequence's length)."""
+    Per later step, four launches on the current stream, no host synchronisation: plan's scores pass
+    (estimate partials, the appended key's sum) -> the masked split pass over the attended sets
+    (every workgroup takes its list from the partials, kvskip_decode_splits_planned with
+    DECIDE_LISTS) -> its split merge (out, and the lse the decision reads) -> the refresh pass
+    (DECIDE_POST: every workgroup makes the decision against that lse; a refreshing head reads every
+    block, the others nothing) -> its merge, which leaves the heads that read nothing as the first
+    merge wrote them (keep_empty), with the update of the refreshing heads in the same launch.
+    Up to BALANCE_MAX_LISTS lists, both passes cut all lists by one chunk length (pass_budget), so a
+    single refreshing head's blocks spread over the whole GPU. With an UpdateCarrier shared by the
+    layers' planners, the update runs inside the next layer's first pass instead (the merge then
+    runs alone), as FusedPlanner's does. The first step is FusedPlanner.first
+    (dense + statistics and the state initialisation, src/kvskip_attn.py:223-231). The mode has no
+    calibration, token index or warm-up age, and takes contiguous caches without seq_lens (as the
+    reference's, which reads k.shape[2] as every sequence's length)."""
 
-    def __init__(self, policy: Policy, count: bool = True):
+    def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None, balance: bool = True):
         if (policy.calib is not None or policy.index_heads or policy.calib_warm
                 or policy.calib_auto_ix is not None):
             raise ValueError("the refresh mode has no calibration, token index or warm-up age")
-        super().__init__(policy, count, carrier=None, decide_in_pass=False, balance=False, batch_balance=False)
+        super().__init__(policy, count, carrier=carrier, decide_in_pass=False, balance=balance, batch_balance=False)
         self.post = None
 
-    def _post_bufs(self, q, S, nb):
-        """The two passes' buffers: out / lse of the masked pass, out2 / lse2 + statistics of the
-        refresh pass, shared split partials (the passes run one after the other)."""
+    def _post_bufs(self, q, S):
+        """Buffers of both passes: out / lse (the second pass's merge rewrites the refreshing heads'),
+        statistics and split partials."""
         B, Hq, D = q.shape
         p = self.post
         n_st = B * Hq * self.NBC
@@ -438,17 +444,13 @@ class PostPlanner(FusedPlanner):
             f32 = dict(dtype=torch.float32, device=dev)
             p = self.post = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
                                  lse=torch.empty(B, Hq, **f32),
-                                 out2=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
-                                 lse2=torch.empty(B, Hq, **f32),
                                  blk_max=torch.empty(n_st, **f32), blk_sum=torch.empty(n_st, **f32),
                                  part_acc=torch.empty(B * Hq * S * D, **f32), part_ml=torch.empty(B * Hq * S * 2, **f32))
-        first = dict(out=p["out"], lse=p["lse"], part_acc=p["part_acc"], part_ml=p["part_ml"])
-        second = dict(out=p["out2"], lse=p["lse2"], blk_max=p["blk_max"], blk_sum=p["blk_sum"],
-                      part_acc=p["part_acc"], part_ml=p["part_ml"])
-        return first, second
+        return p
 
     def step(self, q, k, v, scale, seq_lens=None, block_table=None, T=None):
-        """One decode step (k, v grown by one token, or several: the key sums are then rebuilt)."""
+        """One decode step (k, v grown by one token, or several: the key sums are then rebuilt).
+        Returns out [B, Hq, D], valid until the next step."""
         if seq_lens is not None or block_table is not None:
             raise ValueError("the refresh mode takes a contiguous cache without seq_lens")
         if self.state is None:
@@ -457,39 +459,52 @@ class PostPlanner(FusedPlanner):
             q = q.squeeze(2)
         B, Hq, D = q.shape
         Hkv, T = k.shape[1], k.shape[2]
-        G = Hq // Hkv
         nb = math.ceil(T / TILE)
         dev = q.device
+        self.flush()                                                  # this layer's last update
         if nb > self.NBC:
             self._grow(nb + MARGIN)
         s = self.state
         pol = self.policy
+        G = Hq // Hkv
         add_token = T == self.T + 1
         if not add_token and T != self.T:
             E.block_sums(k, self.NBC, out=s["csum"])
         self.t += 1
         self.T = T
         S = K.num_splits_for(B * Hkv, nb)
-        first, second = self._post_bufs(q, S, nb)
-        pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], first["lse"], s["age"],
+        budget = 0
+        if self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
+            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 256)
+        S = max(S, 2)                       # the second pass's merge keeps the heads it skips
+        b = self._post_bufs(q, S)
+        pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], b["lse"], s["age"],
                               s["flags"], s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale),
                               float(pol.delta), int(pol.max_age), int(pol.local), add_token, est=s["est"],
                               part=s["part"])
+        pargs.pass_budget = budget
         E.plan_scores(pargs, dev)
-        E.plan_decide(pargs, E.DECIDE_LISTS, dev)
+        pargs.decide_mode = E.DECIDE_LISTS
+        carried = self.carrier.take(self, G) if self.carrier is not None else None
+        E.decode_splits_planned(q, k, v, scale, b, pargs, S, carried)
+        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, phase=2)
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
-        E.decode_into(q, k, v, scale, first, s["block_idx"], s["block_cnt"], stats=False, num_splits=S)
-        E.plan_decide(pargs, E.DECIDE_POST, dev)
-        E.decode_into(q, k, v, scale, second, s["block_idx"], s["block_cnt"], stats=True, num_splits=S)
-        out = torch.where(s["trig"].bool().repeat_interleave(G, 1)[..., None], second["out"], first["out"])
+        pargs.decide_mode = E.DECIDE_POST
+        E.decode_splits_planned(q, k, v, scale, b, pargs, S)
         n = B * Hq * nb
-        E.update(second["blk_max"][:n].view(B, Hq, nb), second["blk_sum"][:n].view(B, Hq, nb), s["trig"],
-                 s["cs_now"], s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T, float(pol.level),
-                 int(pol.local), s["flags"], list_stats=True)
+        uargs = (b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb), s["trig"], s["cs_now"],
+                 s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T, float(pol.level), int(pol.local), s["flags"])
+        ukw = dict(list_stats=True, age=s["age"])
+        if self.carrier is not None:
+            E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, phase=2,
+                          keep_empty=True)
+            self.carrier.put(self, G, E.update_struct(*uargs, **ukw), (dict(s), b, uargs, ukw))
+        else:
+            E.merge_update(q, k, v, scale, b, S, uargs, ukw, s["block_idx"], s["block_cnt"], keep_empty=True)
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
             self._count("blocks_total", B * Hkv * nb)
             self._count("masked_heads", B * Hkv)
             self._count("dense_heads", s["trig"].sum())
-        return out
+        return b["out"]

@@ -168,11 +168,13 @@ def test_refresh_mode_matches_oracle():
     (the attended set from the device's previous stored set, plus every block of a refreshing head)
     identical on every head-step, the refresh pass's lists every block of a refreshing head and none
     of the others, stored sets identical after each step, outputs within 2e-3; the device counters
-    add up the blocks of both passes (src/kvskip_attn.py:256,269)."""
+    add up the blocks of both passes (src/kvskip_attn.py:256,269). Then the same with the updates
+    carried by the next layer's pass: the same triggers, outputs and final state."""
     ks, vs, qs, _ = _data(35)
-    cfg = A.KvskipConfig(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),))
+    kw = dict(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),))
+    cfg = A.KvskipConfig(carry=False, **kw)
     orc = {l: LayerOracle(oracle_policy(cfg.policy(l)), SCALE, post=True) for l in range(1, LAYERS)}
-    prev_keep = {}
+    prev_keep, orc_trig = {}, {}
     seen = dict(refresh=0, kept=0, read=0)
 
     def check(t, l, out):
@@ -187,6 +189,7 @@ def test_refresh_mode_matches_oracle():
         nb = O.nblocks(n)
         if t > 0:
             dev_trig = st["trig"].bool().cpu()
+            orc_trig[t, l] = trig
             sel = torch.nn.functional.pad(prev_keep[l], (0, nb - prev_keep[l].shape[-1])) | O.always_keep(nb, cfg.local)
             same_decisions(sel | dev_trig[..., None], read, trig, dev_trig, margin, (t, l))
             assert torch.equal(st["block_cnt"].cpu(), torch.where(trig, nb, 0).to(torch.int32)), (t, l)
@@ -199,9 +202,29 @@ def test_refresh_mode_matches_oracle():
         prev_keep[l] = st["keep"][:, :, :nb].bool().cpu()
         assert torch.equal(prev_keep[l], orc[l].st.keep), (t, l)
 
-    _drive(cfg, ks, vs, qs, after=check)
+    outs, _ = _drive(cfg, ks, vs, qs, after=check)
     assert seen["refresh"] > 0 and seen["kept"] > 0, seen
     assert int(A.log_totals()["blocks_read"]) == seen["read"], (A.log_totals(), seen)
+
+    # with each layer's update carried by the next layer's first pass: the same triggers on every
+    # step, the same outputs (within the merge's summation order) and the same final state
+    trigs = {}
+
+    def record(t, l, out):
+        if l > 0:
+            trigs[t, l] = cfg2.state[l]["post"].state["trig"].clone()
+
+    cfg2 = A.KvskipConfig(carry=True, **kw)
+    outs2, _ = _drive(cfg2, ks, vs, qs, after=record)
+    for t in range(STEPS):
+        for l in range(1, LAYERS):
+            if t > 0:
+                assert torch.equal(trigs[t, l].bool().cpu(), orc_trig[t, l]), (t, l)
+            a, b = outs[t][l].float(), outs2[t][l].float()
+            assert ((a - b).norm() / a.norm()).item() <= 1e-6, (t, l)
+    for l in range(1, LAYERS):
+        for key in ("keep", "lse_ref", "cs_ref", "age", "trig"):
+            assert torch.equal(cfg.state[l]["post"].state[key], cfg2.state[l]["post"].state[key]), (l, key)
 
 
 def test_replay_of_recorded_lists():
