@@ -205,42 +205,30 @@ typedef struct kvskip_plan_args {
    * empty, so the split merge takes num_splits as usual. The grid is pass_budget + B * Hkv
    * workgroups. */
   int32_t pass_budget;
-  /* Read by kvskip_decode_splits_planned only (not in the reference; kvskip_plan_decide takes its
-   * mode as an argument): the decision the pass makes, a KVSKIP_DECIDE_* value. PLAN (0) is plan's;
-   * LISTS reads every head's attended set and writes no trig / est; POST decides against lse_att
-   * (the log-sum-exp of an earlier pass of this step over the attended sets) and reads every block
-   * of a refreshing head and nothing of the others (with kvskip_attn_args.keep_empty in that pass,
-   * the others keep their first-pass output). */
+  /* Read by kvskip_decode_splits_planned only (not in the reference): the decision the pass makes.
+   *   KVSKIP_DECIDE_PLAN (0)  plan's: the refreshing heads read every block, the others their
+   *                           attended set (stored set + block 0 + the `local` newest).
+   *   KVSKIP_DECIDE_LISTS     no decision: every head reads its attended set; trig and est are not
+   *                           written.
+   *   KVSKIP_DECIDE_POST      the decision against lse_att = the log-sum-exp of this step's LISTS
+   *                           pass (its merge's lse output): a refreshing head reads every block,
+   *                           the others nothing (with kvskip_attn_args.keep_empty in that pass's
+   *                           merge they keep the LISTS pass's output).
+   * LISTS then POST is the reference's "refresh" mode (src/kvskip_attn.py:233-263: make_plan of the
+   * stored sets, the estimate and trigger against the masked pass's lse, make_plan of the
+   * refreshing heads), with no host work between the passes. */
   int32_t decide_mode;
 } kvskip_plan_args;
+
+#define KVSKIP_DECIDE_PLAN 0
+#define KVSKIP_DECIDE_LISTS 1
+#define KVSKIP_DECIDE_POST 2
 
 int kvskip_plan(const kvskip_plan_args* p, void* stream);
 
 /* The first launch of kvskip_plan with a workspace alone: the scores pass (needs part). Not in the
  * reference: with kvskip_decode_splits_planned after it, the decision runs inside the masked pass. */
 int kvskip_plan_scores(const kvskip_plan_args* p, void* stream);
-
-/* A decision launch after kvskip_plan_scores(p) (same arguments, needs part), by mode:
- *   KVSKIP_DECIDE_PLAN  plan's second launch: the decision (trig, est, age) and the list to read,
- *                       every block of a refreshing head or the attended set (kvskip_plan with part
- *                       is kvskip_plan_scores followed by this).
- *   KVSKIP_DECIDE_LISTS block_idx / block_cnt = the attended set of every head (stored set + block 0
- *                       + the `local` newest, + the index blocks of an index-union head): the list
- *                       of the refresh mode's masked pass. trig, est and age are not written.
- *   KVSKIP_DECIDE_POST  the decision with lse_att = the log-sum-exp of THIS step's pass over the
- *                       attended set (the lse output of that kvskip_decode): est, trig and the
- *                       advanced age as kvskip_plan writes them; block_idx / block_cnt = every block
- *                       of a refreshing head and none (count 0) of the others: the list of the
- *                       refresh pass. The stored set and the partials are only read, so LISTS, the
- *                       masked pass and POST may follow one scores pass.
- * LISTS and POST replace the torch steps of the reference's "refresh" mode around its two decode
- * calls: make_plan of the stored set (src/kvskip_attn.py:233-238), the estimate and trigger after
- * the pass (src/kvskip_attn.py:241-254) and make_plan of the refreshing heads
- * (src/kvskip_attn.py:259-263). Not in the reference's C++ interface. */
-#define KVSKIP_DECIDE_PLAN 0
-#define KVSKIP_DECIDE_LISTS 1
-#define KVSKIP_DECIDE_POST 2
-int kvskip_plan_decide(const kvskip_plan_args* p, int32_t mode, void* stream);
 
 /* Floats of kvskip_plan_args.part for a state of capacity NBC blocks (-1 for invalid sizes).
  * Not in the reference: sizes the optional multi-workgroup plan workspace. */

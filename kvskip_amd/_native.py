@@ -92,7 +92,6 @@ SIGNATURES = {
     "kvskip_merge_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_decode_splits_update": ([POINTER(AttnArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_plan_scores": ([POINTER(PlanArgs), c_void_p], c_int),
-    "kvskip_plan_decide": ([POINTER(PlanArgs), c_int32, c_void_p], c_int),
     "kvskip_decode_splits_planned": ([POINTER(AttnArgs), POINTER(PlanArgs), POINTER(UpdateArgs), c_void_p], c_int),
     "kvskip_block_sums": ([c_void_p, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_void_p,
                            c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p], c_int),

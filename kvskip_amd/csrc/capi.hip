@@ -333,15 +333,6 @@ int kvskip_plan_scores(const kvskip_plan_args* p, void* stream) {
   return launched(kvs::launch_plan_scores(*p, static_cast<hipStream_t>(stream)), "kvskip_plan_scores");
 }
 
-int kvskip_plan_decide(const kvskip_plan_args* p, int32_t mode, void* stream) {
-  const int rc = check_plan(p);
-  if (rc != KVSKIP_OK) return rc;
-  if (p->part == nullptr) return fail(KVSKIP_E_INVALID, "plan_decide needs the part workspace of plan_scores");
-  if (mode < KVSKIP_DECIDE_PLAN || mode > KVSKIP_DECIDE_POST)
-    return fail(KVSKIP_E_INVALID, "plan_decide: mode in {0, 1, 2} (got %d)", mode);
-  return launched(kvs::launch_plan_decide(*p, mode, static_cast<hipStream_t>(stream)), "kvskip_plan_decide");
-}
-
 int64_t kvskip_plan_part_floats(int32_t B, int32_t Hq, int32_t Hkv, int32_t NBC) {
   if (B < 1 || Hkv < 1 || Hq < 1 || NBC < 1 || Hq % Hkv != 0) return -1;
   return kvs::plan_part_floats(B, Hq, Hkv, NBC);

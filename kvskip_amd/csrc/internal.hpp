@@ -84,9 +84,6 @@ hipError_t launch_planned_paged(const AttnP& a, const kvskip_plan_args& pa, cons
                                 hipStream_t s);
 // The plan's first launch alone (the scores pass; needs part).
 hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s);
-// A decision launch after the scores pass (needs part): mode 0 plan's decision and list, 1 the
-// attended set's list alone, 2 the decision against the pass's lse_att and the refresh pass's list.
-hipError_t launch_plan_decide(const kvskip_plan_args& p, int mode, hipStream_t s);
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,
                              int D, float* csum, int NBC, const int32_t* seq_lens, const int32_t* tbl, int64_t bt,
                              int npages, hipStream_t s);

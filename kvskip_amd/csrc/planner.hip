@@ -404,28 +404,15 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
 
 // One wavefront per (b, KV head): the decision from the C = ceil(nb / 32) partials (decide_head,
 // the arithmetic the planned pass's prologue repeats) and the list compacted from the chunk masks.
-template <int G, int MODE>
+template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int Tb = seq_T(p.seq_lens, b, p.T);
   const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
-  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
   uint32_t mk[DCL];
-  if constexpr (MODE == DECIDE_LISTS) {
-    const int C = plan_chunks(p.T);
-    const float* pb = p.part + bh * C * part_stride(G);
-#pragma unroll
-    for (int j = 0; j < DCL; ++j) {
-      const int c = lane + WAVE * j;
-      const uint32_t m = __float_as_uint(pb[min(c, C - 1) * part_stride(G) + 2 * G]);
-      mk[j] = c < C ? m : 0u;
-    }
-    write_block_list(p, bh, nb, false, mk, lane);
-  } else {  // POST: the masks of a head that does not refresh are emptied (count 0)
-    const bool tr = decide_head<G>(p, b, h, lane, mk, true, true, MODE);
-    write_block_list(p, bh, nb, tr, mk, lane);
-  }
+  const bool tr = decide_head<G>(p, b, h, lane, mk, true, true);
+  write_block_list(p, static_cast<int64_t>(b) * p.Hkv + h, nb, tr, mk, lane);
 }
 
 template <int G, int R>
@@ -520,7 +507,7 @@ hipError_t launch_plan_t(const kvskip_plan_args& p, hipStream_t s) {
   if (p.part != nullptr) {
     const int nb = (p.T + BLK - 1) / BLK;
     hipLaunchKernelGGL((plan_scores_kernel<D, G>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p);
-    hipLaunchKernelGGL((plan_decide_kernel<G, DECIDE_PLAN>), dim3(p.Hkv, p.B), dim3(WAVE), 0, s, p);
+    hipLaunchKernelGGL((plan_decide_kernel<G>), dim3(p.Hkv, p.B), dim3(WAVE), 0, s, p);
   } else {
     hipLaunchKernelGGL((plan_kernel<D, G>), dim3(p.Hkv, p.B), dim3(PNT), 0, s, p);
   }
@@ -598,21 +585,6 @@ hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s) {
   }
   KVS_CASE(64, 1) KVS_CASE(64, 2) KVS_CASE(64, 4) KVS_CASE(64, 7) KVS_CASE(64, 8)
   KVS_CASE(128, 1) KVS_CASE(128, 2) KVS_CASE(128, 4) KVS_CASE(128, 7) KVS_CASE(128, 8)
-#undef KVS_CASE
-  return hipErrorInvalidValue;
-}
-
-hipError_t launch_plan_decide(const kvskip_plan_args& p, int mode, hipStream_t s) {
-  const int G = p.Hq / p.Hkv;
-  const dim3 grid(p.Hkv, p.B), blk(WAVE);
-#define KVS_CASE(GG)                                                                                       \
-  if (G == GG) {                                                                                           \
-    if (mode == DECIDE_LISTS) hipLaunchKernelGGL((plan_decide_kernel<GG, DECIDE_LISTS>), grid, blk, 0, s, p); \
-    else if (mode == DECIDE_POST) hipLaunchKernelGGL((plan_decide_kernel<GG, DECIDE_POST>), grid, blk, 0, s, p); \
-    else hipLaunchKernelGGL((plan_decide_kernel<GG, DECIDE_PLAN>), grid, blk, 0, s, p);                    \
-    return hipGetLastError();                                                                              \
-  }
-  KVS_CASE(1) KVS_CASE(2) KVS_CASE(4) KVS_CASE(7) KVS_CASE(8)
 #undef KVS_CASE
   return hipErrorInvalidValue;
 }

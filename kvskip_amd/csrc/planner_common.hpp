@@ -174,8 +174,7 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
   }
 }
 
-// What a decision after the scores pass yields (kvskip_plan_decide's mode, the planned pass's
-// kvskip_plan_args.decide_mode).
+// What the planned pass's decision yields (kvskip_plan_args.decide_mode, KVSKIP_DECIDE_*).
 enum DecideMode {
   DECIDE_PLAN = 0,   // plan's decision (trig, est, age) and the list to read: every block or the attended set
   DECIDE_LISTS = 1,  // the attended set's list alone, no decision (trig, est, age untouched)

@@ -383,17 +383,7 @@ def plan_scores(pargs: PlanArgs, device):
         _native.check(_native.lib().kvskip_plan_scores(ctypes.byref(pargs), _stream(dev)))
 
 
-DECIDE_PLAN, DECIDE_LISTS, DECIDE_POST = 0, 1, 2
-
-
-def plan_decide(pargs: PlanArgs, mode: int, device):
-    """A decision launch after plan_scores(pargs) (kvskip_plan_decide; needs part): DECIDE_PLAN plan's
-    own decision and list; DECIDE_LISTS the attended set's lists alone (no decision); DECIDE_POST the
-    decision against pargs' lse_att taken from this step's pass over those lists, with the lists of
-    the refresh pass (every block of a refreshing head, none of the others). Not in the reference."""
-    dev = torch.device(device)
-    with torch.cuda.device(dev):
-        _native.check(_native.lib().kvskip_plan_decide(ctypes.byref(pargs), int(mode), _stream(dev)))
+DECIDE_PLAN, DECIDE_LISTS, DECIDE_POST = 0, 1, 2      # kvskip_plan_args.decide_mode
 
 
 def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None,
