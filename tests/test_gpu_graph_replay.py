@@ -95,3 +95,61 @@ def test_one_graph_replayed_every_step(gpu, carried):
         for l in range(layers):
             for k in STATE:
                 assert torch.equal(planners[l].state[k], eager[l].state[k]), ("final", l, k)
+
+
+def test_refresh_mode_steps_in_a_graph(gpu):
+    """The refresh mode (PostPlanner) captured: four decode steps of two layers in one HIP graph
+    (each step's length in its launches), replayed three times from the same saved state with eager
+    work and synchronisations between the replays; every replay must give the eager loop's outputs
+    and final state bit for bit (no memset nodes: the keep_empty merge and the passes write every
+    byte they hand on)."""
+    from kvskip_amd import kvskip as K
+    from kvskip_amd.planner import PostPlanner
+
+    layers, T0, warm, n = 2, 3000, 5, 4
+    steps = warm + n
+    run = W.planner_run(layers=layers, B=1, Hq=32, Hkv=8, D=128, T0=T0, steps=steps, seed=37)
+    ks = [k.cuda() for k in run.k]
+    vs = [v.cuda() for v in run.v]
+    qps = [W.QueryProcess(run, l, p_jump=0.2) for l in range(layers)]
+    qs = torch.stack([torch.stack([qps[l].next() for l in range(layers)]) for _ in range(steps)]).cuda()
+    pol = Policy(delta=0.01, max_age=3)
+
+    def step(planners, t):
+        T = T0 + t + 1
+        return [planners[l].step(qs[t][l], ks[l][:, :, :T], vs[l][:, :, :T], run.scale) for l in range(layers)]
+
+    eager = [PostPlanner(pol, count=False) for _ in range(layers)]
+    ref, refreshed = [], 0
+    for t in range(steps):
+        ref.append([o.clone() for o in step(eager, t)])
+        if t >= warm:
+            refreshed += sum(int(p.state["trig"].sum()) for p in eager)
+    assert 0 < refreshed < n * layers * 8      # the captured steps refresh some heads and keep others
+    keys = [k for k in eager[0].state if k != "part"]      # part: the scores pass's workspace
+
+    planners = [PostPlanner(pol, count=False) for _ in range(layers)]
+    for t in range(warm):
+        step(planners, t)
+    torch.cuda.synchronize()
+    saved = [{k: p.state[k].clone() for k in keys} for p in planners]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = [[o.clone() for o in step(planners, t)] for t in range(warm, steps)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for p, sv in zip(planners, saved):
+            for k in keys:
+                p.state[k].copy_(sv[k])
+        K.decode(qs[0][0], ks[0], vs[0], run.scale)       # the program's own eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, t in enumerate(range(warm, steps)):
+            for l in range(layers):
+                assert torch.equal(outs[i][l], ref[t][l]), (rep, t, l)
+        for l in range(layers):
+            for k in keys:
+                assert torch.equal(planners[l].state[k], eager[l].state[k]), (rep, l, k)

@@ -297,9 +297,9 @@ def test_paged_planner_loop_matches_contiguous(ragged, G, D):
         for l in range(layers):
             kv = (ks[l], vs[l]) if ragged else (ks[l][:, :, :T], vs[l][:, :, :T])
             kp, vp, table = pools[l]
-            if t == 0:
+            if t == 0:   # the paged planner's first call is step(), which starts the state on the pages
                 a = ref[l].first(qs[t][l], *kv, run.scale, seq_lens=sl)
-                b = dut[l].first(qs[t][l], kp, vp, run.scale, seq_lens=sl, block_table=table, T=T)
+                b = dut[l].step(qs[t][l], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
             else:
                 a = ref[l].step(qs[t][l], *kv, run.scale, ids=ids, seq_lens=sl)
                 b = dut[l].step(qs[t][l], kp, vp, run.scale, ids=ids, seq_lens=sl, block_table=table, T=T)
