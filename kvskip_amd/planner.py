@@ -411,7 +411,7 @@ class PostPlanner(FusedPlanner):
     """The reference's "refresh" mode (src/kvskip_attn.py:215-270) on the device: the trigger is
     decided AFTER a masked pass over the stored sets, against that pass's own log-sum-exp, and the
     refreshing heads then get a dense + statistics pass whose output replaces their masked one.
-    Per later step, four launches on the current stream, no host synchronisation: plan's scores pass
+    Per later step, five launches on the current stream, no host synchronisation: plan's scores pass
     (estimate partials, the appended key's sum) -> the masked split pass over the attended sets
     (every workgroup takes its list from the partials, kvskip_decode_splits_planned with
     DECIDE_LISTS) -> its split merge (out, and the lse the decision reads) -> the refresh pass
