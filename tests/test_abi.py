@@ -141,3 +141,32 @@ def test_select_validation():
         assert msg in lib.kvskip_last_error().decode(), kw
     assert lib.kvskip_block_list(0, 1, 1, 4, 0x1000, 0x2000, None) == -1
     assert lib.kvskip_block_list(0x1000, 1, 0, 4, 0x1000, 0x2000, None) == -1
+
+
+def test_planned_pass_validation():
+    """kvskip_decode_splits_planned refuses an unknown decide_mode, a pass budget out of range or over
+    more than 16 lists, and mismatched shapes, before any device work."""
+    lib = _native.lib()
+    p = PlanArgs()
+    p.q, p.k, p.k_sb, p.k_sh, p.k_st = 0x1000, 0x2000, 8 * 4096 * 128, 4096 * 128, 128
+    for f in ("csum", "lse_ref", "cs_ref", "keep", "lse_att", "age", "flags", "cs_now", "trig", "block_idx",
+              "block_cnt", "part"):
+        setattr(p, f, 0x10000)
+    p.B, p.Hq, p.Hkv, p.T, p.D, p.NBC = 1, 32, 8, 4096, 128, 128
+    for kw, code, msg in ((dict(decide_mode=3), -1, "decide_mode in {0, 1, 2}"),
+                          (dict(decide_mode=-1), -1, "decide_mode in {0, 1, 2}"),
+                          (dict(pass_budget=-1), -1, "pass_budget in 0..65536"),
+                          (dict(pass_budget=70000), -1, "pass_budget in 0..65536")):
+        q = PlanArgs.from_buffer_copy(p)
+        for k_, v_ in kw.items():
+            setattr(q, k_, v_)
+        assert lib.kvskip_decode_splits_planned(ctypes.byref(_args(num_splits=4, part_acc=0x8000, part_ml=0x9000)),
+                                                ctypes.byref(q), None, None) == code, kw
+        assert msg in lib.kvskip_last_error().decode(), kw
+    q = PlanArgs.from_buffer_copy(p)
+    q.B, q.Hkv, q.Hq, q.pass_budget = 4, 8, 32, 100
+    a = _args(B=4, num_splits=4, part_acc=0x8000, part_ml=0x9000)
+    assert lib.kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(q), None, None) == -2
+    assert "pass_budget needs B * Hkv <= 16" in lib.kvskip_last_error().decode()
+    assert lib.kvskip_decode_splits_planned(ctypes.byref(_args(T=2048)), ctypes.byref(p), None, None) == -1
+    assert "attention and plan shapes differ" in lib.kvskip_last_error().decode()
