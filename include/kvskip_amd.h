@@ -96,11 +96,6 @@ typedef struct kvskip_attn_args {
   const int32_t* block_table;
   int64_t bt_stride;
   int32_t num_pages;
-
-  /* Not in the reference: nonzero = a query head that attends nothing (an empty block list) keeps
-   * out, out_f32 and lse as they are instead of 0 / -inf, so a second pass over some heads' lists
-   * (the refresh mode's dense pass of the refreshing heads) replaces only those heads' results. */
-  int32_t keep_empty;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block
@@ -210,14 +205,28 @@ typedef struct kvskip_plan_args {
    *                           attended set (stored set + block 0 + the `local` newest).
    *   KVSKIP_DECIDE_LISTS     no decision: every head reads its attended set; trig and est are not
    *                           written.
-   *   KVSKIP_DECIDE_POST      the decision against lse_att = the log-sum-exp of this step's LISTS
-   *                           pass (its merge's lse output): a refreshing head reads every block,
-   *                           the others nothing (with kvskip_attn_args.keep_empty in that pass's
-   *                           merge they keep the LISTS pass's output).
-   * LISTS then POST is the reference's "refresh" mode (src/kvskip_attn.py:233-263: make_plan of the
-   * stored sets, the estimate and trigger against the masked pass's lse, make_plan of the
-   * refreshing heads), with no host work between the passes. */
+   *   KVSKIP_DECIDE_POST      the decision against the log-sum-exp of this step's LISTS pass
+   *                           (lse_part below, or lse_att): a refreshing head reads the blocks
+   *                           OUTSIDE its attended set, the others nothing, and no (-inf, 0)
+   *                           statistics are written for unlisted blocks (the LISTS pass wrote the
+   *                           attended blocks' statistics and (-inf, 0) for the rest; a refreshing
+   *                           head's rest comes from this pass). The lists written are these.
+   * LISTS into partial slots [0, S), then POST into [S, 2S), then one split merge over the 2S slots
+   * is the reference's "refresh" mode (src/kvskip_attn.py:233-270: attention over the stored sets,
+   * the estimate and trigger against that pass's lse, attention and statistics over every block
+   * for the refreshing heads, whose outputs replace the masked ones): a refreshing head's merge
+   * joins its attended and its other blocks, every block read once. */
   int32_t decide_mode;
+  /* Read by kvskip_decode_splits_planned only (not in the reference): the pass's partials go to slots
+   * [slot_base, slot_base + slot_count) of each query head's num_splits slots (slot_count 0: all
+   * num_splits from 0), and a list gets at most slot_count chunks. */
+  int32_t slot_base, slot_count;
+  /* Read by the POST decision only (not in the reference): if not NULL, the attended log-sum-exp
+   * comes from the split partials of the step's LISTS pass instead of lse_att: lse_part is that
+   * pass's part_ml ([B, Hq, lse_stride, 2], max and sum in log2 units), slots [0, lse_slots)
+   * (lse_slots <= 128). */
+  const float* lse_part;
+  int32_t lse_slots, lse_stride;
 } kvskip_plan_args;
 
 #define KVSKIP_DECIDE_PLAN 0

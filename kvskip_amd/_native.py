@@ -30,7 +30,6 @@ class AttnArgs(ctypes.Structure):
         ("p_out", c_void_p), ("p_in", c_void_p), ("blk_scale", c_void_p),
         ("tau", c_float), ("local", c_int32), ("vcount", c_void_p), ("lse_prev", c_void_p),
         ("seq_lens", c_void_p), ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32),
-        ("keep_empty", c_int32),
     ]
 
 
@@ -50,7 +49,8 @@ class PlanArgs(ctypes.Structure):
         ("part", c_void_p), ("seq_lens", c_void_p), ("seq_lens_out", c_void_p),
         ("ids", c_void_p), ("ids_sb", c_int64), ("idx_out", c_void_p),
         ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32), ("pass_budget", c_int32),
-        ("decide_mode", c_int32),
+        ("decide_mode", c_int32), ("slot_base", c_int32), ("slot_count", c_int32),
+        ("lse_part", c_void_p), ("lse_slots", c_int32), ("lse_stride", c_int32),
     ]
 
 

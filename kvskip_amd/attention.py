@@ -14,8 +14,9 @@ on KVSKIP.mode (layers in dense_layers always run dense):
                    as the same loop: the fused loop reproduces that mode's decisions
                    (src/kvskip_attn.py:399-478), here on the device from the first step on
   "refresh"        the trigger decided after a masked pass over the stored sets, against that
-                   pass's log-sum-exp, with a dense + statistics pass for the refreshing heads
-                   (src/kvskip_attn.py:215-270; planner.PostPlanner, on the device, no host
+                   pass's log-sum-exp; a refreshing head's output is its attention over every
+                   block, with every block's statistics (src/kvskip_attn.py:215-270;
+                   planner.PostPlanner, on the device, each block read once, no host
                    synchronisation where the reference syncs once per step to skip an empty
                    second pass)
   "replay"         masked + statistics decode over KVSKIP.plans[layer][t] (one kvskip.Plan per step)

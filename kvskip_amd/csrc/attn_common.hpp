@@ -351,10 +351,8 @@ __device__ __forceinline__ void finish(const AttnP& p, float (&m)[G], float (&l)
       const int64_t hq = hq0 + g;
       if (S == 1) {
         const float o_ = Ls > 0.f ? A / Ls : 0.f;
-        if (Ls > 0.f || !p.keep_empty) {
-          p.out[hq * D + d] = f2bf(o_);
-          if (p.out_f32) p.out_f32[hq * D + d] = o_;
-        }
+        p.out[hq * D + d] = f2bf(o_);
+        if (p.out_f32) p.out_f32[hq * D + d] = o_;
       } else {
         p.part_acc[(hq * S + split) * D + d] = A;
       }
@@ -370,7 +368,7 @@ __device__ __forceinline__ void finish(const AttnP& p, float (&m)[G], float (&l)
     for (int w = 0; w < NWAVE; ++w) Ls += L.ml[(w * G + g) * 2 + 1] * fexp2(L.ml[(w * G + g) * 2] - mu);
     const int64_t hq = hq0 + g;
     if (S == 1) {
-      if (p.lse && (Ls > 0.f || !p.keep_empty)) p.lse[hq] = Ls > 0.f ? (M + flog2(Ls)) * LN2 : NEG_INF;
+      if (p.lse) p.lse[hq] = Ls > 0.f ? (M + flog2(Ls)) * LN2 : NEG_INF;
     } else {
       p.part_ml[(hq * S + split) * 2] = M;
       p.part_ml[(hq * S + split) * 2 + 1] = Ls;
@@ -536,7 +534,6 @@ __device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq
       a += rA[c][tid];
       l += rL[c];
     }
-    if (!plain && l == 0.f && p.keep_empty) return;  // nothing attended: out and lse stay as they are
     if (plain) l = 1.f;
     if constexpr (WITH_V) {
       const float o = l > 0.f ? a / l : 0.f;

@@ -89,7 +89,7 @@ __device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, 
   uint32_t mk[NH][DCL];
   bool tr[NH];
   decide_heads<G, NH>(pa, lists, lane, mk, tr, bid == 0 && pa.decide_mode != DECIDE_LISTS, false);
-  apply_decide_mode<NH>(pa.decide_mode, mk, tr);
+  apply_decide_mode<NH>(pa.decide_mode, mk, tr, lane, nbb);
 #pragma unroll
   for (int k = 0; k < NH; ++k) {
     int c = 0;
@@ -106,7 +106,7 @@ __device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, 
   const int cq = lane < P ? sCnt[lane] : 0;
   const int total = static_cast<int>(wave_sum(static_cast<float>(cq)));  // exact: <= 16 * MAX_NB
   const int most = static_cast<int>(wave_max(static_cast<float>(cq)));
-  const int slots = p.num_splits, budget = pa.pass_budget;
+  const int slots = pa.slot_count > 0 ? pa.slot_count : p.num_splits, budget = pa.pass_budget;
   const int C = max(1, max((total + budget - 1) / budget, (most + slots - 1) / slots));
   const int ch = lane < P ? max(1, (cq + C - 1) / C) : 0;
   const int incl = wave_incl_scan(ch);
@@ -143,7 +143,7 @@ __device__ bool planned_balanced_nh(const AttnP& p, const kvskip_plan_args& pa, 
   if (split == 0) {  // the slots [ch_sel, slots) of the list's query heads: empty partials
     const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
     for (int t = threadIdx.x; t < G * (slots - ch_sel); t += NT) {
-      float* ml = p.part_ml + ((hq0 + t % G) * slots + ch_sel + t / G) * 2;
+      float* ml = p.part_ml + ((hq0 + t % G) * p.num_splits + pa.slot_base + ch_sel + t / G) * 2;
       ml[0] = NEG_INF;
       ml[1] = 0.f;
     }
@@ -204,6 +204,12 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   bool dense = false;                             // planned: a refresh (every block, in order)
   const bool balanced = PLANNED && pa->pass_budget > 0;  // every list cut by one chunk length
   bool list_writer = false;                               // balanced: this wavefront writes the list
+  // planned: the pass's partial slots [slot_base, slot_base + nslot) of the num_splits per head
+  const int nslot = PLANNED && pa->slot_count > 0 ? pa->slot_count : p.num_splits;
+  const int slot_base = PLANNED ? pa->slot_base : 0;
+  // a refresh pass of the post-pass decision reads blocks whose neighbours' statistics the attended
+  // pass wrote: it writes no gap statistics
+  const bool gaps = !(PLANNED && pa->decide_mode == DECIDE_POST);
   if constexpr (PLANNED) {
     if (balanced) {
       if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
@@ -214,7 +220,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
                                list_writer, pmk))
         return;
     } else {
-      work_coords(bid, p.num_splits, p.Hkv, p.B, split, h, b);
+      work_coords(bid, nslot, p.Hkv, p.B, split, h, b);
       if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
         Tb = seq_len(p, b);
         nbb = (Tb + BLK - 1) / BLK;
@@ -222,7 +228,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       if (wave == 0) {
         int pre[DCL];
         const int mode = pa->decide_mode;
-        const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0 && mode != DECIDE_LISTS, false, mode);
+        const bool t = decide_head<G>(*pa, b, h, lane, pmk, split == 0 && mode != DECIDE_LISTS, false, mode, nbb);
         const int cnt = t ? nbb : mask_prefix(pmk, lane, plan_chunks(pa->T), pre);
         if (!t) {
 #pragma unroll
@@ -239,7 +245,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       __syncthreads();
       dense = sPi[0] != 0;
       n_items = sPi[1];
-      const int per = (n_items + p.num_splits - 1) / p.num_splits;
+      const int per = (n_items + nslot - 1) / nslot;
       i0 = min(n_items, split * per);
       n = min(n_items, i0 + per) - i0;
       if (!dense) {  // this split's slice, positions i0 - 1 .. i0 + n - 1, by every thread
@@ -602,8 +608,9 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
       }
     }
   }
-  finish<D, G, LOAD_V>(p, m, l, acc, b, h, split, sL, false);
-  if constexpr (MASKED && STATS) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
+  finish<D, G, LOAD_V>(p, m, l, acc, b, h, slot_base + split, sL, false);
+  if constexpr (MASKED && STATS)
+    if (gaps) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
   if constexpr (PLANNED) {
     if (balanced ? list_writer : (split == 0 && wave == 0))
       write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, nbb, dense, pmk, lane);

@@ -104,7 +104,6 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->block_table = a->block_table;
   p->bt_stride = a->bt_stride;
   p->num_pages = a->num_pages;
-  p->keep_empty = a->keep_empty != 0 ? 1 : 0;
   return KVSKIP_OK;
 }
 
@@ -406,6 +405,12 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
   if (pl->decide_mode < KVSKIP_DECIDE_PLAN || pl->decide_mode > KVSKIP_DECIDE_POST)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: decide_mode in {0, 1, 2} (got %d)", pl->decide_mode);
+  if (pl->slot_base < 0 || pl->slot_count < 0 ||
+      (pl->slot_count > 0 ? pl->slot_base + pl->slot_count : pl->slot_base + a->num_splits) > a->num_splits)
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: slots [slot_base, slot_base + slot_count) within num_splits");
+  if (pl->lse_part != nullptr &&
+      (pl->lse_slots < 1 || pl->lse_slots > 128 || pl->lse_stride < pl->lse_slots))
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: lse_slots in 1..128, lse_stride >= lse_slots");
   if (pl->pass_budget < 0 || pl->pass_budget > 65536)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: pass_budget in 0..65536");
   if (pl->pass_budget > 0 && a->B * a->Hkv > 16)

@@ -42,7 +42,6 @@ struct AttnP {
   const int* block_table;  // [B, bt_stride] or null: paged K / V (page stride k_sb / v_sb)
   int64_t bt_stride;
   int num_pages;
-  int keep_empty;  // split merge: a head with nothing attended keeps out / out_f32 / lse
 };
 
 constexpr int MAX_RAGGED_B = 256;  // batch bound of the ragged partition (one scan per 64)

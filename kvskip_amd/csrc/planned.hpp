@@ -31,7 +31,8 @@ __global__ void __launch_bounds__(NT, 2) planned_split_kernel(const AttnP a, con
 template <int D, int G, bool PAGED>
 hipError_t launch_planned_p(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, hipStream_t s) {
   const dim3 blk(NT);
-  const int n_pass = pa.pass_budget > 0 ? pa.pass_budget + a.Hkv * a.B : a.num_splits * a.Hkv * a.B;
+  const int nslot = pa.slot_count > 0 ? pa.slot_count : a.num_splits;
+  const int n_pass = pa.pass_budget > 0 ? pa.pass_budget + a.Hkv * a.B : nslot * a.Hkv * a.B;
   if (u == nullptr) {
     hipLaunchKernelGGL((planned_split_kernel<D, G, 0, PAGED>), dim3(n_pass), blk, 0, s, a, pa, kvskip_update_args{});
     return hipGetLastError();

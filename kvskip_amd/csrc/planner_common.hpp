@@ -80,6 +80,7 @@ __device__ __forceinline__ int plan_chunks(int T) { return ((T + BLK - 1) / BLK 
 // `write_age` (a decision repeated by every workgroup of a pass leaves the age to the update: the
 // others still read the old one).
 constexpr int DLP = 8;
+constexpr int LSI = 8;   // partial slots per team lane of an attended log-sum-exp from partials (<= 64 slots)
 
 template <int CTRL>
 __device__ __forceinline__ void lse_dpp(float& m, float& s) {
@@ -123,7 +124,23 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
     asm volatile("" : "+v"(v));
     const int b = v / p.Hkv, h = v - b * p.Hkv;
     const float* pb = p.part + static_cast<int64_t>(v) * C * SP;
-    const float la = p.lse_att[static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + g];
+    const int64_t hq = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + g;
+    // the attended log-sum-exp: lse_att, or from the split partials of this step's attended pass
+    // (max and sum in log2 units; team lane t takes slots t, t + 8, ...)
+    float lm[LSI], ls[LSI];
+    const bool from_part = p.lse_part != nullptr;
+#pragma unroll
+    for (int i = 0; i < LSI; ++i) {
+      const int sl = t + DLP * i;
+      lm[i] = NEG_INF;
+      ls[i] = 0.f;
+      if (from_part && sl < p.lse_slots) {
+        const float2 x = *reinterpret_cast<const float2*>(p.lse_part + (hq * p.lse_stride + sl) * 2);
+        lm[i] = x.x * LN2;
+        ls[i] = x.y;
+      }
+    }
+    const float la_mem = from_part ? 0.f : p.lse_att[hq];
     const int NI = (C + DLP - 1) / DLP;  // chunk rounds of the team (uniform)
     float pm[CPL], ps[CPL];
 #pragma unroll
@@ -144,6 +161,16 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
     lse_dpp<DPP_XOR1>(m, sv);
     lse_dpp<DPP_XOR2>(m, sv);
     lse_dpp<DPP_HALF_MIRROR>(m, sv);
+    float la = la_mem;
+    if (from_part) {
+      float am = NEG_INF, as = 0.f;
+#pragma unroll
+      for (int i = 0; i < LSI; ++i) lse_merge(am, as, lm[i], ls[i]);
+      lse_dpp<DPP_XOR1>(am, as);
+      lse_dpp<DPP_XOR2>(am, as);
+      lse_dpp<DPP_HALF_MIRROR>(am, as);
+      la = as > 0.f ? am + __logf(as) : NEG_INF;
+    }
     const float e = sv > 0.f ? 1.f / (1.f + __expf(la - (m + __logf(sv)))) : 0.f;
 #pragma unroll
     for (int q = 0; q < KW; ++q) {
@@ -182,27 +209,33 @@ enum DecideMode {
                      // of a refreshing head, none of the others
 };
 
-// A decision's lists under a mode: LISTS refreshes nothing (the attended sets), POST empties the
-// list of every head that does not refresh.
+// A decision's lists under a mode (lane holds chunks lane + 64 j of blocks 32 c .. 32 c + 31; nb
+// blocks): LISTS refreshes nothing (the attended sets); POST gives a refreshing head the blocks
+// outside its attended set (no longer a "read every block" list: tr is cleared) and every other head
+// an empty list.
 template <int NH>
-__device__ __forceinline__ void apply_decide_mode(int mode, uint32_t (&mk)[NH][DCL], bool (&tr)[NH]) {
+__device__ __forceinline__ void apply_decide_mode(int mode, uint32_t (&mk)[NH][DCL], bool (&tr)[NH], int lane,
+                                                  int nb) {
 #pragma unroll
   for (int k = 0; k < NH; ++k) {
-    if (mode == DECIDE_LISTS) tr[k] = false;
 #pragma unroll
-    for (int j = 0; j < DCL; ++j)
-      if (mode == DECIDE_POST && !tr[k]) mk[k][j] = 0u;
+    for (int j = 0; j < DCL; ++j) {
+      const int left = nb - WCB * (lane + WAVE * j);  // blocks of this chunk in the sequence
+      const uint32_t valid = left >= WCB ? ~0u : (left > 0 ? (1u << left) - 1u : 0u);
+      if (mode == DECIDE_POST) mk[k][j] = tr[k] ? ~mk[k][j] & valid : 0u;
+    }
+    if (mode != DECIDE_PLAN) tr[k] = false;
   }
 }
 
 template <int G>
 __device__ __forceinline__ bool decide_head(const kvskip_plan_args& p, int b, int h, int lane, uint32_t (&mk)[DCL],
-                                            bool write, bool write_age = true, int mode = DECIDE_PLAN) {
+                                            bool write, bool write_age = true, int mode = DECIDE_PLAN, int nb = 0) {
   const int bh[1] = {b * p.Hkv + h};
   uint32_t m[1][DCL];
   bool tr[1];
   decide_heads<G, 1>(p, bh, lane, m, tr, write, write_age);
-  apply_decide_mode<1>(mode, m, tr);
+  apply_decide_mode<1>(mode, m, tr, lane, nb);
 #pragma unroll
   for (int j = 0; j < DCL; ++j) mk[j] = m[0][j];
   return tr[0];

@@ -159,14 +159,13 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
 
 
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,
-                seq_lens=None, phase=3, block_table=None, T=None, keep_empty=False):
+                seq_lens=None, phase=3, block_table=None, T=None):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
     [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
     (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way.
     phase: 3 = the whole op, 1 = the split pass only (its merge left to merge_splits / merge_update),
-    2 = that merge alone. block_table, T: a paged cache (see _kv_dims). keep_empty (not in the
-    reference): a head that attends nothing keeps out / lse as they are."""
+    2 = that merge alone. block_table, T: a paged cache (see _kv_dims)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -188,7 +187,7 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
         _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
-                   part_acc, part_ml, seq_lens, phase, block_table, T, keep_empty)
+                   part_acc, part_ml, seq_lens, phase, block_table, T)
 
 
 class DecodeOp:
@@ -261,10 +260,9 @@ _PHASES = {3: "kvskip_decode", 1: "kvskip_decode_splits", 2: "kvskip_merge_split
 
 
 def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens=None, phase=3, block_table=None, T=None, keep_empty=False):
+                   pbuf, part_acc, part_ml, seq_lens=None, phase=3, block_table=None, T=None):
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
                      part_ml, seq_lens, block_table, T)
-    a.keep_empty = int(bool(keep_empty))
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(getattr(_native.lib(), _PHASES[phase])(ctypes.byref(a), int(bool(stats)), int(bool(load_v)),
@@ -387,12 +385,12 @@ DECIDE_PLAN, DECIDE_LISTS, DECIDE_POST = 0, 1, 2      # kvskip_plan_args.decide_
 
 
 def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_splits, update: UpdateArgs | None = None,
-                          seq_lens=None, block_table=None, T=None, keep_empty=False):
+                          seq_lens=None, block_table=None, T=None):
     """plan's decision and the masked + statistics split pass in one launch (kvskip_decode_splits_planned;
     after plan_scores(pargs)); the whole op when num_splits == 1. The layer's update must advance the
     age (update_struct(..., age=...)). update: another layer's update to carry, or None. seq_lens: the
     plan's (one sequence, B 1). pargs.decide_mode picks the decision (DECIDE_PLAN, DECIDE_LISTS,
-    DECIDE_POST); keep_empty: heads with an empty list keep out / lse (with num_splits == 1)."""
+    DECIDE_POST), pargs.slot_base / slot_count the partial slots the pass writes."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -410,7 +408,6 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
                  "bufs: split partials")
     a = _decode_args(q, k, v, scale, None, None, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None, None,
                      part_acc, part_ml, seq_lens, block_table, T)
-    a.keep_empty = int(bool(keep_empty))
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(pargs),
@@ -558,16 +555,14 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
 
 
 def merge_update(q, k, v, scale, bufs: dict, num_splits, update_args: tuple, update_kwargs: dict,
-                 block_idx=None, block_cnt=None, seq_lens=None, block_table=None, T=None, keep_empty=False):
+                 block_idx=None, block_cnt=None, seq_lens=None, block_table=None, T=None):
     """The split merge of a decode_into(..., phase=1) pass (same q, k, v, bufs, list, num_splits >= 2)
     and update(*update_args, **update_kwargs), in one launch (kvskip_merge_update; not in the
-    reference). block_table, T: the pass's paged cache (see _kv_dims). keep_empty: a head whose
-    splits hold nothing keeps out / lse."""
+    reference). block_table, T: the pass's paged cache (see _kv_dims)."""
     B, Hq, D = q.shape
     _require(num_splits >= 2, "merge_update needs num_splits >= 2")
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], None, None, None,
                      None, bufs["part_acc"], bufs["part_ml"], seq_lens, block_table, T)
-    a.keep_empty = int(bool(keep_empty))
     u = _update_args(*update_args, **update_kwargs)
     dev = q.device
     with torch.cuda.device(dev):

@@ -409,22 +409,26 @@ class FusedPlanner:
 
 class PostPlanner(FusedPlanner):
     """The reference's "refresh" mode (src/kvskip_attn.py:215-270) on the device: the trigger is
-    decided AFTER a masked pass over the stored sets, against that pass's own log-sum-exp, and the
-    refreshing heads then get a dense + statistics pass whose output replaces their masked one.
-    Per later step, five launches on the current stream, no host synchronisation: plan's scores pass
-    (estimate partials, the appended key's sum) -> the masked split pass over the attended sets
-    (every workgroup takes its list from the partials, kvskip_decode_splits_planned with
-    DECIDE_LISTS) -> its split merge (out, and the lse the decision reads) -> the refresh pass
-    (DECIDE_POST: every workgroup makes the decision against that lse; a refreshing head reads every
-    block, the others nothing) -> its merge, which leaves the heads that read nothing as the first
-    merge wrote them (keep_empty), with the update of the refreshing heads in the same launch.
+    decided AFTER a masked pass over the stored sets, against that pass's own log-sum-exp, and a
+    refreshing head's output is then its attention over every block (with the statistics of every
+    block, from which the update rebuilds its set).
+    Per later step, four launches on the current stream, no host synchronisation: plan's scores pass
+    (estimate partials, the appended key's sum) -> the masked + statistics split pass over the
+    attended sets (kvskip_decode_splits_planned, DECIDE_LISTS: every workgroup takes its list from
+    the scores partials) into partial slots [0, S) -> the refresh pass (DECIDE_POST: every workgroup
+    merges the first pass's partials of its heads into their log-sum-exp, decides against it, and a
+    refreshing head reads the blocks OUTSIDE its attended set) into slots [S, 2S) -> one split merge
+    over the 2S slots with the update of the refreshing heads. A head that does not refresh has only
+    first-pass partials, so its output is its masked attention; a refreshing head's merge joins its
+    attended and its other blocks, so every block is read once per step (the reference reads the
+    attended blocks of a refreshing head twice, and counts them twice).
     Up to BALANCE_MAX_LISTS lists, both passes cut all lists by one chunk length (pass_budget), so a
     single refreshing head's blocks spread over the whole GPU. With an UpdateCarrier shared by the
     layers' planners, the update runs inside the next layer's first pass instead (the merge then
-    runs alone), as FusedPlanner's does. The first step is FusedPlanner.first
-    (dense + statistics and the state initialisation, src/kvskip_attn.py:223-231). The mode has no
-    calibration, token index or warm-up age, and takes contiguous caches without seq_lens (as the
-    reference's, which reads k.shape[2] as every sequence's length)."""
+    runs alone), as FusedPlanner's does. The first step is FusedPlanner.first (dense + statistics and
+    the state initialisation, src/kvskip_attn.py:223-231). The mode has no calibration, token index or
+    warm-up age, and takes contiguous caches without seq_lens (as the reference's, which reads
+    k.shape[2] as every sequence's length)."""
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None, balance: bool = True):
         if (policy.calib is not None or policy.index_heads or policy.calib_warm
@@ -434,18 +438,20 @@ class PostPlanner(FusedPlanner):
         self.post = None
 
     def _post_bufs(self, q, S):
-        """Buffers of both passes: out / lse (the second pass's merge rewrites the refreshing heads'),
-        statistics and split partials."""
+        """Buffers of both passes: out / lse of the merge, statistics, and 2 S partial slots per
+        query head (the first pass's S, then the refresh pass's S)."""
         B, Hq, D = q.shape
         p = self.post
         n_st = B * Hq * self.NBC
-        if p is None or p["blk_max"].numel() < n_st or p["part_acc"].numel() < B * Hq * S * D or p["out"].shape != q.shape:
+        if (p is None or p["blk_max"].numel() < n_st or p["part_acc"].numel() < B * Hq * 2 * S * D
+                or p["out"].shape != q.shape):
             dev = q.device
             f32 = dict(dtype=torch.float32, device=dev)
             p = self.post = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
                                  lse=torch.empty(B, Hq, **f32),
                                  blk_max=torch.empty(n_st, **f32), blk_sum=torch.empty(n_st, **f32),
-                                 part_acc=torch.empty(B * Hq * S * D, **f32), part_ml=torch.empty(B * Hq * S * 2, **f32))
+                                 part_acc=torch.empty(B * Hq * 2 * S * D, **f32),
+                                 part_ml=torch.empty(B * Hq * 2 * S * 2, **f32))
         return p
 
     def step(self, q, k, v, scale, seq_lens=None, block_table=None, T=None):
@@ -472,36 +478,35 @@ class PostPlanner(FusedPlanner):
             E.block_sums(k, self.NBC, out=s["csum"])
         self.t += 1
         self.T = T
-        S = K.num_splits_for(B * Hkv, nb)
+        S = min(K.num_splits_for(B * Hkv, nb), 128)       # 2 S slots per head in all, <= 256
         budget = 0
         if self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
-            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 256)
-        S = max(S, 2)                       # the second pass's merge keeps the heads it skips
+            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 128)
         b = self._post_bufs(q, S)
-        pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], b["lse"], s["age"],
+        pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"],
                               s["flags"], s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale),
                               float(pol.delta), int(pol.max_age), int(pol.local), add_token, est=s["est"],
                               part=s["part"])
         pargs.pass_budget = budget
+        pargs.slot_count = S
         E.plan_scores(pargs, dev)
-        pargs.decide_mode = E.DECIDE_LISTS
+        pargs.decide_mode, pargs.slot_base = E.DECIDE_LISTS, 0
         carried = self.carrier.take(self, G) if self.carrier is not None else None
-        E.decode_splits_planned(q, k, v, scale, b, pargs, S, carried)
-        E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, phase=2)
+        E.decode_splits_planned(q, k, v, scale, b, pargs, 2 * S, carried)
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
-        pargs.decide_mode = E.DECIDE_POST
-        E.decode_splits_planned(q, k, v, scale, b, pargs, S)
+        pargs.decide_mode, pargs.slot_base = E.DECIDE_POST, S
+        pargs.lse_part, pargs.lse_slots, pargs.lse_stride = b["part_ml"].data_ptr(), S, 2 * S
+        E.decode_splits_planned(q, k, v, scale, b, pargs, 2 * S)
         n = B * Hq * nb
         uargs = (b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb), s["trig"], s["cs_now"],
                  s["keep"], s["lse_ref"], s["cs_ref"], s["lse_att"], T, float(pol.level), int(pol.local), s["flags"])
         ukw = dict(list_stats=True, age=s["age"])
         if self.carrier is not None:
-            E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S, phase=2,
-                          keep_empty=True)
+            E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=2 * S, phase=2)
             self.carrier.put(self, G, E.update_struct(*uargs, **ukw), (dict(s), b, uargs, ukw))
         else:
-            E.merge_update(q, k, v, scale, b, S, uargs, ukw, s["block_idx"], s["block_cnt"], keep_empty=True)
+            E.merge_update(q, k, v, scale, b, 2 * S, uargs, ukw, s["block_idx"], s["block_cnt"])
         if self.count:
             self._count("blocks_read", s["block_cnt"].sum())
             self._count("blocks_total", B * Hkv * nb)

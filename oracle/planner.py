@@ -264,7 +264,7 @@ def post_step(st: State, q, k, v, policy: Policy, dtype=torch.float64):
     Reuses plan() with st.lse_att set to the pass's log-sum-exp (the estimate, age and trigger
     arithmetic of src/kvskip_attn.py:241-254 is the same as :366-376) and update() for the rebuild
     (its attended log-sum-exp is not read by this mode). Returns (out, plan dict + "lse" of the
-    masked pass)."""
+    masked pass + "attended", the blocks that pass read)."""
     assert policy.calib is None and not policy.index_heads and not policy.calib_warm \
         and policy.calib_auto_ix is None, "the refresh mode has no calibration, index or warm-up"
     update_csum(st, k)
@@ -280,6 +280,7 @@ def post_step(st: State, q, k, v, policy: Policy, dtype=torch.float64):
     M, S = A.block_stats(q, k, st.scale, keep=full, dtype=dtype)
     update(st, pr, A.block_logw(M.double(), S.double()), policy)
     pr["read"] = sel | trig[..., None]
+    pr["attended"] = sel
     pr["lse"] = lse
     return out, pr
 

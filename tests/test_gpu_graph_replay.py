@@ -101,8 +101,8 @@ def test_refresh_mode_steps_in_a_graph(gpu):
     """The refresh mode (PostPlanner) captured: four decode steps of two layers in one HIP graph
     (each step's length in its launches), replayed three times from the same saved state with eager
     work and synchronisations between the replays; every replay must give the eager loop's outputs
-    and final state bit for bit (no memset nodes: the keep_empty merge and the passes write every
-    byte they hand on)."""
+    and final state bit for bit (no memset nodes: the passes and the merge write every byte they
+    hand on)."""
     from kvskip_amd import kvskip as K
     from kvskip_amd.planner import PostPlanner
 

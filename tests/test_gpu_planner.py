@@ -243,8 +243,9 @@ def test_post_planner_loop(gpu, pol, B, G, Hkv):
     """The refresh mode's device loop (PostPlanner: scores, attended lists, masked pass, decision
     against that pass's lse, refresh pass, update) against the oracle's post_step, free-running for
     30 steps with query drift and jumps: refresh decisions identical on every head-step (failures
-    name the oracle's margin), the refresh pass's lists every block of a refreshing head and none of
-    the others, stored sets identical after every step, estimates within 1e-4, outputs within 2e-3."""
+    name the oracle's margin), the refresh pass's lists the blocks outside a refreshing head's
+    attended set and none of the others, stored sets identical after every step, estimates within
+    1e-4, outputs within 2e-3."""
     T0, steps = 4096, 30
     run = W.planner_run(layers=1, B=B, Hq=G * Hkv, Hkv=Hkv, D=128, T0=T0, steps=steps, seed=6)
     qp = W.QueryProcess(run, 0, p_jump=0.05)
@@ -267,7 +268,8 @@ def test_post_planner_loop(gpu, pol, B, G, Hkv):
             out_r, pr = OP.post_step(st, q, k_cpu[:, :, :T], v_cpu[:, :, :T], pol)
             s = pp.state
             margin_min = min(margin_min, _agree(s["trig"].bool().cpu(), pr["trig"], pr["margin"], f"trigger at step {t}"))
-            assert torch.equal(s["block_cnt"].cpu(), torch.where(pr["trig"], nb, 0).to(torch.int32)), t
+            rest = nb - pr["attended"].sum(-1)             # a refreshing head's blocks outside its attended set
+            assert torch.equal(s["block_cnt"].cpu(), torch.where(pr["trig"], rest, 0).to(torch.int32)), t
             assert (s["est"].double().cpu() - pr["miss"]).abs().max().item() <= 1e-4, t
             n_trig += int(pr["trig"].sum())
             n_kept += int((~pr["trig"]).sum())

@@ -166,9 +166,10 @@ def test_refresh_mode_matches_oracle():
     """Mode "refresh" (the trigger after the masked pass, src/kvskip_attn.py:215-270) against the
     oracle's loop of that mode on the same inputs (layer 0 dense): refresh decisions and read sets
     (the attended set from the device's previous stored set, plus every block of a refreshing head)
-    identical on every head-step, the refresh pass's lists every block of a refreshing head and none
-    of the others, stored sets identical after each step, outputs within 2e-3; the device counters
-    add up the blocks of both passes (src/kvskip_attn.py:256,269). Then the same with the updates
+    identical on every head-step, the refresh pass's lists the blocks outside a refreshing head's
+    attended set and none of the others' blocks, stored sets identical after each step, outputs within
+    2e-3; the device counters add up the blocks of both passes (src/kvskip_attn.py:256,269), each
+    block once. Then the same with the updates
     carried by the next layer's pass: the same triggers, outputs and final state."""
     ks, vs, qs, _ = _data(35)
     kw = dict(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),))
@@ -192,11 +193,13 @@ def test_refresh_mode_matches_oracle():
             orc_trig[t, l] = trig
             sel = torch.nn.functional.pad(prev_keep[l], (0, nb - prev_keep[l].shape[-1])) | O.always_keep(nb, cfg.local)
             same_decisions(sel | dev_trig[..., None], read, trig, dev_trig, margin, (t, l))
-            assert torch.equal(st["block_cnt"].cpu(), torch.where(trig, nb, 0).to(torch.int32)), (t, l)
+            rest = nb - sel.sum(-1)          # a refreshing head's blocks outside its attended set
+            assert torch.equal(st["block_cnt"].cpu(), torch.where(trig, rest, 0).to(torch.int32)), (t, l)
             seen["refresh"] += int(trig.sum())
             seen["kept"] += int((~trig).sum())
-            # as the reference counts them: the masked pass's blocks, then the refresh pass's
-            seen["read"] += int(sel.sum()) + int(trig.sum()) * nb
+            # the masked pass's blocks, then the refresh pass's (the reference counts a refreshing
+            # head's attended blocks again, since its refresh pass reads them again)
+            seen["read"] += int(sel.sum()) + int(torch.where(trig, rest, 0).sum())
         else:
             seen["read"] += int(read.sum())
         prev_keep[l] = st["keep"][:, :, :nb].bool().cpu()
