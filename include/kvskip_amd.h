@@ -294,9 +294,12 @@ int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_a
  * (b, KV head), makes plan's decision (the same result in every workgroup) and takes its slice of
  * the block list from the attended-block masks; p's trig, est, block_idx and block_cnt are written
  * as by kvskip_plan, but NOT the age: the layer's update must advance it (u->age). a: as for
- * kvskip_decode_splits with stats and load_v (its block list fields are ignored); seq_lens only with
- * B == 1 (the step's length in device memory), the same array in a and p; no ragged batches of
- * B > 1. u: NULL, or the update of another layer to carry (as kvskip_decode_splits_update). */
+ * kvskip_decode_splits with stats and load_v (its block list fields are ignored); seq_lens, the same
+ * array in a and p: with B == 1 the step's length in device memory; with 1 < B <= 16 a ragged batch
+ * of a contiguous cache (the ragged grid and partition of kvskip_decode_splits, cut over the lists
+ * the workgroups decide; then pass_budget, slot_base, slot_count are 0, lse_part NULL and decide_mode
+ * PLAN or LISTS; its merge is kvskip_merge_splits with the same seq_lens and lists).
+ * u: NULL, or the update of another layer to carry (as kvskip_decode_splits_update). */
 int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_args* p, const kvskip_update_args* u,
                                  void* stream);
 

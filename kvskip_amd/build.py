@@ -14,7 +14,7 @@ CSRC = ROOT / "kvskip_amd" / "csrc"
 OUT = ROOT / "kvskip_amd" / "libkvskip_amd.so"
 BUILD = ROOT / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["attn_decode.hip", "attn_decode_paged.hip", "attn_vskip.hip", "planner.hip", "split_update.hip", "split_update_paged.hip", "planned.hip", "planned_paged.hip", "select.hip", "capi.hip"]
+SOURCES = ["attn_decode.hip", "attn_decode_paged.hip", "attn_vskip.hip", "planner.hip", "split_update.hip", "split_update_paged.hip", "planned.hip", "planned_paged.hip", "planned_ragged.hip", "select.hip", "capi.hip"]
 # Packed FP32 (v_pk_*_f32) stays off: hipcc would otherwise form it from plain float code.
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", f"-I{ROOT / 'include'}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

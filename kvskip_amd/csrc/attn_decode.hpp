@@ -172,6 +172,116 @@ __device__ bool planned_balanced(const AttnP& p, const kvskip_plan_args& pa, int
                                                         n_items, i0, n, dense, writer, omk);
 }
 
+// A planned pass over a ragged batch (seq_lens, B <= BAL_MAX_LISTS): workgroup `it` of KV head h
+// decides the head's B lists (b, h) in its prologue (wavefront w: b = w + NWAVE j; the head's
+// workgroup 0 stores trig and est) and takes chunk `it` of the ragged partition over their lengths
+// (a refreshing list: the sequence's blocks; C = ceil(sum / num_splits) items per chunk, numbered
+// sequence by sequence, as ragged_lookup does over the block counts this pass writes, so that the
+// ragged merge finds the same chunks). Outputs as planned_balanced_nh's, plus the sequence's length
+// Tb and blocks nbb; the head's workgroup 0 also writes the statistics and the zero count of a list
+// with nothing to read. Returns false for a workgroup past the head's chunks. Uniform results.
+template <int G, int NH>
+__device__ bool planned_ragged_nh(const AttnP& p, const kvskip_plan_args& pa, int h, int it, int wave, int lane,
+                                  int* sPl, uint32_t* sMk, int* sPre, int& split, int& b, int& n_items, int& i0,
+                                  int& n, bool& dense, bool& writer, uint32_t (&omk)[DCL], int& Tb, int& nbb) {
+  __shared__ int sCnt[BAL_MAX_LISTS];
+  __shared__ int sTr[BAL_MAX_LISTS];
+  const int B = p.B;
+  int lists[NH], nbl[NH];  // this wavefront's lists (clamped: a repeat is decided, not stored)
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    const int bb = min(wave + NWAVE * k, B - 1);
+    lists[k] = bb * p.Hkv + h;
+    nbl[k] = (seq_len(p, bb) + BLK - 1) / BLK;
+  }
+  uint32_t mk[NH][DCL];
+  bool tr[NH];
+  decide_heads<G, NH>(pa, lists, lane, mk, tr, it == 0 && pa.decide_mode != DECIDE_LISTS, false);
+  apply_decide_mode<NH>(pa.decide_mode, mk, tr, lane, 0);  // PLAN or LISTS (POST is not ragged)
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    int c = 0;
+#pragma unroll
+    for (int d = 0; d < DCL; ++d) c += __popc(mk[k][d]);
+    c = wave_sum_int(c);
+    if (lane == 0 && wave + NWAVE * k < B) {
+      sCnt[wave + NWAVE * k] = tr[k] ? nbl[k] : c;
+      sTr[wave + NWAVE * k] = tr[k] ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  // the partition, lane q holding list q (every wavefront computes the same)
+  const int cq = lane < B ? sCnt[lane] : 0;
+  const int tot = wave_sum_int(cq);
+  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  const int ch = (cq + C - 1) / C;  // none for an empty list
+  const int incl = wave_incl_scan(ch);
+  if (it == 0) {  // the head's lists with nothing to read: statistics (-inf, 0) and count 0
+    uint64_t empty = __ballot(lane < B && cq == 0);
+    while (empty != 0) {
+      const int be = __builtin_ctzll(empty);
+      empty &= empty - 1;
+      if (wave == 0 && lane == 0) pa.block_cnt[static_cast<int64_t>(be) * p.Hkv + h] = 0;
+      const int64_t q0 = static_cast<int64_t>(be) * p.Hq + static_cast<int64_t>(h) * G;
+      for (int t = threadIdx.x; t < G * p.nb; t += NT) {
+        p.blk_max[(q0 + t / p.nb) * p.nb + t % p.nb] = NEG_INF;
+        p.blk_sum[(q0 + t / p.nb) * p.nb + t % p.nb] = 0.f;
+      }
+    }
+  }
+  const uint64_t hit = __ballot(lane < B && ch > 0 && it >= incl - ch && it < incl);
+  if (hit == 0) return false;
+  const int q_sel = __builtin_ctzll(hit);
+  const int ch_sel = __builtin_amdgcn_readlane(ch, q_sel);
+  split = it - (__builtin_amdgcn_readlane(incl, q_sel) - ch_sel);
+  b = q_sel;
+  n_items = __builtin_amdgcn_readlane(cq, q_sel);
+  dense = sTr[q_sel] != 0;
+  i0 = min(n_items, split * C);
+  n = min(n_items, i0 + C) - i0;
+  Tb = seq_len(p, b);
+  nbb = (Tb + BLK - 1) / BLK;
+  writer = false;  // the list's last chunk writes the list at its end
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    if (wave + NWAVE * k == q_sel) {  // the wavefront that decided this list holds its masks
+      if (!dense) {
+        int pre[DCL];
+        mask_prefix(mk[k], lane, plan_chunks(pa.T), pre);
+#pragma unroll
+        for (int d = 0; d < DCL; ++d) {
+          sMk[lane + WAVE * d] = mk[k][d];
+          sPre[lane + WAVE * d] = pre[d];
+        }
+      }
+      writer = split == ch_sel - 1;
+#pragma unroll
+      for (int d = 0; d < DCL; ++d) omk[d] = mk[k][d];
+    }
+  }
+  if (!dense) {  // this workgroup's slice, positions i0 - 1 .. i0 + n - 1, by every thread
+    __syncthreads();  // the masks and prefixes in LDS
+    slice_from_masks(sMk, sPre, plan_chunks(pa.T), i0, i0 + n, sPl, threadIdx.x, NT);
+    if (threadIdx.x == 0 && i0 == 0) sPl[0] = -1;
+    __syncthreads();
+  }
+  return true;
+}
+
+template <int G>
+__device__ bool planned_ragged(const AttnP& p, const kvskip_plan_args& pa, int h, int it, int wave, int lane,
+                               int* sPl, uint32_t* sMk, int* sPre, int& split, int& b, int& n_items, int& i0, int& n,
+                               bool& dense, bool& writer, uint32_t (&omk)[DCL], int& Tb, int& nbb) {
+  if (p.B <= NWAVE)
+    return planned_ragged_nh<G, 1>(p, pa, h, it, wave, lane, sPl, sMk, sPre, split, b, n_items, i0, n, dense, writer,
+                                   omk, Tb, nbb);
+  if (p.B <= 2 * NWAVE)
+    return planned_ragged_nh<G, 2>(p, pa, h, it, wave, lane, sPl, sMk, sPre, split, b, n_items, i0, n, dense, writer,
+                                   omk, Tb, nbb);
+  return planned_ragged_nh<G, BAL_MAX_LISTS / NWAVE>(p, pa, h, it, wave, lane, sPl, sMk, sPre, split, b, n_items, i0,
+                                                      n, dense, writer, omk, Tb, nbb);
+}
+
 // The split pass of workgroup `bid` of the decode grid (attn_grid): NT threads. PLANNED (masked,
 // unragged partition): the list is the plan's decision for (b, h), made in this workgroup's
 // prologue from the scores pass's partials (pa): wavefront 0 decides (as plan_decide; every
@@ -183,7 +293,8 @@ __device__ bool planned_balanced(const AttnP& p, const kvskip_plan_args& pa, int
 template <int D, int G, bool MASKED, bool STATS, bool LOAD_V, bool MF, bool RAG, bool PLANNED = false,
           bool PAGED = false>
 __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvskip_plan_args* pa = nullptr) {
-  static_assert(!PLANNED || (MASKED && !RAG), "a planned pass is masked and not ragged");
+  static_assert(!PLANNED || MASKED, "a planned pass is masked");
+  static_assert(!(PLANNED && RAG && PAGED), "a planned ragged pass reads a contiguous cache");
   static_assert(!PAGED || MF, "a paged cache is read by the MFMA engine");
   constexpr int GP = gpad<G>();
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
@@ -210,7 +321,14 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   // a refresh pass of the post-pass decision reads blocks whose neighbours' statistics the attended
   // pass wrote: it writes no gap statistics
   const bool gaps = !(PLANNED && pa->decide_mode == DECIDE_POST);
-  if constexpr (PLANNED) {
+  if constexpr (PLANNED && RAG) {
+    const int W = p.num_splits + p.B;
+    const int it = xcd_remap(bid, W * p.Hkv);
+    h = it / W;
+    if (!planned_ragged<G>(p, *pa, h, it % W, wave, lane, sPl, sMk, sPre, split, b, n_items, i0, n, dense,
+                           list_writer, pmk, Tb, nbb))
+      return;
+  } else if constexpr (PLANNED) {
     if (balanced) {
       if (p.seq_lens != nullptr) {  // one sequence whose length is in device memory
         Tb = seq_len(p, 0);
@@ -612,7 +730,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
   if constexpr (MASKED && STATS)
     if (gaps) write_gap_stats<G>(p, list, n_items, i0, n, split, hq0, wave, lane, gap_prev, gap_cur);
   if constexpr (PLANNED) {
-    if (balanced ? list_writer : (split == 0 && wave == 0))
+    if ((balanced || RAG) ? list_writer : (split == 0 && wave == 0))
       write_block_list(*pa, static_cast<int64_t>(b) * p.Hkv + h, nbb, dense, pmk, lane);
   }
   if constexpr (!MASKED && STATS && RAG) {  // the blocks past the sequence's end read (-inf, 0)

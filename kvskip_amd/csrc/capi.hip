@@ -398,9 +398,17 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
   if (pl->part == nullptr) return fail(KVSKIP_E_INVALID, "decode_splits_planned needs the plan's part workspace");
   if (pl->seq_lens != a->seq_lens)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: the plan and the pass must share seq_lens");
-  if (a->seq_lens != nullptr && a->B != 1)
-    return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: seq_lens only for one sequence (B 1; plan and decide "
-                                      "separately for a ragged batch)");
+  if (a->seq_lens != nullptr && a->B > 1) {  // a ragged batch: the ragged partition over the decided lists
+    if (a->B > 16)
+      return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch of at most 16 sequences (got %d; plan "
+                                        "and decide separately for more)", a->B);
+    if (a->block_table != nullptr)
+      return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch reads a contiguous cache");
+    if (pl->pass_budget != 0 || pl->slot_base != 0 || pl->slot_count != 0 || pl->lse_part != nullptr ||
+        pl->decide_mode == KVSKIP_DECIDE_POST)
+      return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch takes no pass_budget, slots, lse_part "
+                                        "or DECIDE_POST");
+  }
   if (a->B != pl->B || a->Hq != pl->Hq || a->Hkv != pl->Hkv || a->T != pl->T || a->D != pl->D)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: attention and plan shapes differ");
   if (pl->decide_mode < KVSKIP_DECIDE_PLAN || pl->decide_mode > KVSKIP_DECIDE_POST)

@@ -81,6 +81,10 @@ hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, cons
 // unit).
 hipError_t launch_planned_paged(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
                                 hipStream_t s);
+// launch_planned_split over a ragged batch (seq_lens, B > 1) of a contiguous cache, after any
+// unfused carried update (its own translation unit).
+hipError_t launch_planned_ragged(const AttnP& a, const kvskip_plan_args& pa, const kvskip_update_args* u, int D,
+                                 hipStream_t s);
 // The plan's first launch alone (the scores pass; needs part).
 hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s);
 hipError_t launch_block_sums(const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st, int B, int Hkv, int T,

@@ -13,6 +13,7 @@ hipError_t launch_planned_split(const AttnP& a, const kvskip_plan_args& pa, cons
     u = nullptr;
   }
   if (a.block_table != nullptr) return launch_planned_paged(a, pa, u, D, s);
+  if (a.seq_lens != nullptr && a.B > 1) return launch_planned_ragged(a, pa, u, D, s);
 #define KVS_CASE(DD, GG) \
   if (D == DD && G == GG) return launch_planned_p<DD, GG, false>(a, pa, u, s);
   KVS_FOR_G(KVS_CASE, 64)

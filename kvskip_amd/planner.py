@@ -29,6 +29,7 @@ from . import kvskip as K
 TILE = 64
 MARGIN = 64                      # spare block capacity of the state (src/kvskip_attn.py:399)
 BALANCE_MAX_LISTS = 16           # (b, KV head) lists a balanced planned pass decides in every workgroup
+RAGGED_DECIDE_MAX_B = 16         # sequences of a ragged batch whose lists a planned pass decides per KV head
 KINDS = {"logit": 0, "add": 1, "peak": 2}
 
 
@@ -118,12 +119,18 @@ class FusedPlanner:
     out = p.step(q, k, v, scale, idx=...) on every later one (k, v grown by one token)."""
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
-                 decide_in_pass: bool = True, balance: bool = True, batch_balance: bool = True):
+                 decide_in_pass: bool = True, balance: bool = True, batch_balance: bool = True,
+                 ragged_in_pass: bool | None = None):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
-        # plan's decision inside the masked pass (batches without seq_lens): one launch fewer per
-        # step, the same decisions and lists as plan's own decision launch
+        # plan's decision inside the masked pass: one launch fewer per step, the same decisions and
+        # lists as plan's own decision launch
         self.decide_in_pass = decide_in_pass
+        # a ragged batch (seq_lens, B > 1) of a contiguous cache: every workgroup of the pass decides
+        # its KV head's B lists (B <= RAGGED_DECIDE_MAX_B); None: when that prologue is cheaper than
+        # plan's decision launch (measured: groups of <= 4 query heads and B <= 8: config 4's shape
+        # at B 8 -1.2%; config 5, G 7 and B 16: +2.9%), True / False: always / never
+        self.ragged_in_pass = ragged_in_pass
         # with the decision in the pass and B * Hkv <= 16: the lists of all heads cut by one chunk
         # length (kvskip_plan_args.pass_budget), so a refreshing head gets more workgroups than a
         # light one; the partials get twice the split count's slots
@@ -194,7 +201,8 @@ class FusedPlanner:
         Hkv = k.shape[1]
         S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv)
         budget = 0
-        if self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
+        if (self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1
+                and (seq_lens is None or B == 1)):
             # workgroups: S per head less the partition's B*Hkv spare chunks and room for a carried
             # update of this shape, so that the pass fits the CUs the per-head split fills (a CU
             # given a second full chunk would double the critical path); the same with and without
@@ -243,10 +251,18 @@ class FusedPlanner:
             E.update(*update_args, **update_kwargs)
 
     def _plan(self, q, plan_args, plan_kwargs, seq_lens):
-        """plan (scores + decision), or, with decide_in_pass and no ragged batch (seq_lens absent or
-        one sequence), its scores pass alone: the decision then runs in the masked pass
-        (kvskip_decode_splits_planned) and the update advances the age."""
-        if self.decide_in_pass and (seq_lens is None or q.shape[0] == 1):
+        """plan (scores + decision), or, with decide_in_pass, its scores pass alone: the decision then
+        runs in the masked pass (kvskip_decode_splits_planned) and the update advances the age. A
+        ragged batch decides in the pass as ragged_in_pass says (up to RAGGED_DECIDE_MAX_B sequences
+        of a contiguous cache: every workgroup decides its KV head's lists over the batch); else plan
+        decides."""
+        B, Hq = q.shape[0], q.shape[1]
+        G = Hq // plan_args[1].shape[1]
+        rag = self.ragged_in_pass
+        if rag is None:
+            rag = B <= 8 and G <= 4
+        if self.decide_in_pass and (seq_lens is None or B == 1
+                                    or (rag and B <= RAGGED_DECIDE_MAX_B and not self._pg)):
             self._pargs = E.plan_struct(*plan_args, **plan_kwargs)
             E.plan_scores(self._pargs, q.device)
         else:

@@ -133,6 +133,43 @@ def test_batch_balanced_partition(gpu, carry):
         _same_state(ref, dut, t)
 
 
+@pytest.mark.parametrize("lens,Hkv,G,D", [((1700, 2900, 1100), 4, 4, 128), ((900, 4100, 2500, 3300, 1800), 2, 7, 128),
+                                           ((2100,) * 8, 8, 2, 64), ((600, 3900, 2200, 1500, 3000, 2600, 800, 1900,
+                                                                      3500, 1200, 2800, 700, 3300, 2400, 1000, 3100),
+                                                                     2, 4, 64)])
+@pytest.mark.parametrize("carry", [False, True])
+def test_ragged_decision_in_pass(gpu, lens, Hkv, G, D, carry):
+    """A ragged batch decided inside the masked pass (every workgroup decides its KV head's B lists,
+    then takes its chunk of the ragged partition over them: B 3, 5, 8 and 16, so one, two, two and four
+    lists per wavefront) against plan's own decision launch followed by the ragged pass over the
+    plan's lists: bit-identical state on every step (lists, triggers, ages, references,
+    calibration, latches) and bit-identical outputs (the same chunks of the same lists)."""
+    layers, steps = 2, 6
+    run = W.planner_run(layers=layers, B=len(lens), Hq=Hkv * G, Hkv=Hkv, D=D, T0=max(lens), steps=steps,
+                        seed=90 + len(lens) + G, ragged=list(lens))
+    ks = [k.cuda() for k in run.k]
+    vs = [v.cuda() for v in run.v]
+    ids = run.ids.to(torch.int32).cuda()
+    qps = [W.QueryProcess(run, l, p_jump=0.1, revert=True) for l in range(layers)]
+    qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
+    pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
+    cr = [UpdateCarrier(), UpdateCarrier()] if carry else [None, None]
+    ref = [FusedPlanner(pol(), count=False, carrier=cr[0], decide_in_pass=False) for _ in range(layers)]
+    dut = [FusedPlanner(pol(), count=False, carrier=cr[1], ragged_in_pass=True) for _ in range(layers)]
+    for t in range(steps):
+        sl = torch.tensor([T + t + 1 for T in lens], dtype=torch.int32, device="cuda")
+        for l in range(layers):
+            outs = [(fp.first(qs[t][l], ks[l], vs[l], run.scale, seq_lens=sl) if t == 0 else
+                     fp.step(qs[t][l], ks[l], vs[l], run.scale, ids=ids, seq_lens=sl)).clone() for fp in (ref[l], dut[l])]
+            assert torch.isfinite(outs[0].float()).all()
+            assert torch.equal(outs[0], outs[1]), (t, l)
+        for c in cr:
+            if c is not None:
+                c.flush()
+        _same_state(ref, dut, t)
+    assert dut[0]._pargs is not None          # the decision ran in the pass
+
+
 @pytest.mark.parametrize("B,Hkv,G", [(2, 8, 2), (1, 12, 8), (4, 4, 4), (1, 1, 7)])
 def test_balanced_pass_many_lists(gpu, B, Hkv, G):
     """The balanced planned pass (every workgroup decides all B * Hkv lists: 16, 12, 16 and 1 here,
