@@ -341,6 +341,8 @@ def main():
     # ---- config 4: 32-layer decode loop with the device-side planner (stage-4 policy, layer 0 dense)
     if not args.no_planner:
         res["planner_cfg4"] = bench_planner(dev, layers=args.planner_layers, T0=32768, steps=args.planner_steps)
+        res["planner_cfg4"]["oracle_agreement"] = planner_agreement(dev)
+        torch.cuda.empty_cache()
         # the same loop with queries that revert to their planted direction between jumps:
         # attention stays on the planted blocks, so the policy skips most of the cache
         res["planner_cfg4_focused"] = bench_planner(dev, layers=args.planner_layers, T0=32768,
@@ -720,6 +722,61 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
         f"{us_plan_own / n:.2f} with their own launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
         f"{layers}-layer step" + (f"; one graph replayed per step: {us_replay / n_replay:.2f}" if n_replay else ""))
     del run, qs
+    return out
+
+
+def planner_agreement(dev):
+    """Decision agreement of the config-4 planner loop with the oracle's refresh_pre loop as frozen in
+    tests/golden/planner_cfg4.npz (its two planned layers, 128 steps, updates carried, the decision in
+    the pass, the token index found from the ids; untimed). Inputs regenerated on the CPU and checked
+    against the fixture's digest. Per (layer, step, KV head): identical read sets (the reference's
+    criterion, bench/test_planner.py:100-133) and identical refresh decisions; the oracle's smallest
+    decision margin |estimate - delta| over the run (a refresh by age or a forced head has none), and
+    the margins of the head-steps whose decision differs."""
+    import numpy as np
+    import torch
+
+    from kvskip_amd import workloads as W
+    from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
+
+    d = np.load(Path(__file__).resolve().parent / "tests" / "golden" / "planner_cfg4.npz", allow_pickle=False)
+    run, layers, qs = W.loop_inputs(4)
+    if W.input_digest(run, layers, qs) != str(d["digest"]):
+        return {"error": "the regenerated config-4 inputs differ from the fixture's"}
+    pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
+    carrier = UpdateCarrier()
+    fps = {l: FusedPlanner(pol, count=False, carrier=carrier) for l in layers}
+    kv = {l: (run.k[l].to(dev), run.v[l].to(dev)) for l in layers}
+    ids = run.ids.to(dev)
+    n = same_read = same_trig = 0
+    min_margin, differ = math.inf, []
+    for t in range(run.steps):
+        T = run.T0[0] + t + 1
+        nb = math.ceil(T / 64)
+        for i, l in enumerate(layers):
+            k, v = kv[l][0][:, :, :T], kv[l][1][:, :, :T]
+            q = qs[l][t].to(dev)
+            if t == 0:
+                fps[l].first(q, k, v, run.scale)
+                continue
+            fps[l].step(q, k, v, run.scale, ids=ids)
+            read = fps[l].read_mask(nb).cpu().numpy()[0]
+            trig = fps[l].state["trig"].bool().cpu().numpy()[0]
+            rr = d["read"][i, t]
+            ref_read = np.unpackbits(rr, axis=-1, count=rr.shape[-1] * 8)[..., :nb].astype(bool)
+            ref_trig, m = d["trig"][i, t], d["margin"][i, t]
+            n += trig.size
+            same_read += int((~(read != ref_read).any(-1)).sum())
+            same_trig += int((trig == ref_trig).sum())
+            fin = m[np.isfinite(m)]
+            if fin.size:
+                min_margin = min(min_margin, float(fin.min()))
+            differ += [float(m[h]) for h in np.nonzero(trig != ref_trig)[0]]
+    out = {"fixture": "tests/golden/planner_cfg4.npz", "layers": len(layers), "steps": run.steps - 1,
+           "head_steps": n, "read_sets_identical": same_read / n, "decisions_identical": same_trig / n,
+           "min_oracle_decision_margin": min_margin, "differing_decision_margins": differ}
+    log(f"cfg4 vs oracle: read sets identical on {same_read}/{n} head-steps, decisions on {same_trig}/{n}; "
+        f"smallest oracle decision margin {min_margin:.2e}; differing decisions' margins {differ}")
     return out
 
 

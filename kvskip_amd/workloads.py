@@ -13,6 +13,7 @@ there is ~`sink_mass`.
 
 from __future__ import annotations
 
+import hashlib
 import math
 from dataclasses import dataclass
 
@@ -275,3 +276,42 @@ class QueryProcess:
             self.aim = torch.where(jump, new, self.aim)
             self.q = torch.where(jump[..., None], self.run.alpha * self._aimed(G) + self.noise * eps, self.q)
         return self.q.to(torch.bfloat16)
+
+
+def cfg5_lens() -> list[int]:
+    """Config 5's 16 contexts, log-uniform in [4096, 65536] from seed 5."""
+    g = torch.Generator().manual_seed(5)
+    return [int(round(math.exp(x))) for x in
+            (torch.rand(16, generator=g, dtype=torch.float64) * math.log(16) + math.log(4096)).tolist()]
+
+
+def loop_inputs(cfg: int):
+    """The inputs of the full-size planner loops that the golden fixtures record: (run, planned
+    layers, query sequences qs[layer][t] bf16 [B, Hq, D]) of config 4 (B 1, 32 / 8 heads, D 128, T0
+    32768, 128 steps, jumps 0.03; layer 0 dense, layers 1 and 2 planned) or config 5 (B 16 ragged
+    contexts, 28 / 4 heads, 64 steps; one planned layer), generated on the CPU."""
+    if cfg == 4:
+        run = planner_run(layers=3, B=1, Hq=32, Hkv=8, D=128, T0=32768, steps=128, seed=4)
+        layers = [1, 2]
+    elif cfg == 5:
+        run = planner_run(layers=1, B=16, Hq=28, Hkv=4, D=128, T0=65536, steps=64, seed=5, ragged=cfg5_lens())
+        layers = [0]
+    else:
+        raise ValueError(cfg)
+    qs = {}
+    for l in layers:
+        qp = QueryProcess(run, l, p_jump=0.03)
+        qs[l] = [qp.next() for _ in range(run.steps)]
+    return run, layers, qs
+
+
+def input_digest(run, layers, qs) -> str:
+    """sha256 over the planned layers' K / V, the query sequences and the token ids."""
+    h = hashlib.sha256()
+    for l in layers:
+        h.update(run.k[l].view(torch.int16).numpy().tobytes())
+        h.update(run.v[l].view(torch.int16).numpy().tobytes())
+        for q in qs[l]:
+            h.update(q.view(torch.int16).numpy().tobytes())
+    h.update(run.ids.numpy().tobytes())
+    return h.hexdigest()
