@@ -265,26 +265,15 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
 
   // Token index (ids given; kvskip_token_index's rule): lane l checks the 8 tokens 8 (l % 8) + [0, 8)
   // of block base + l / 8, so the wavefront finds its own 8 blocks (bit i: block base + i); the
-  // workgroups of KV head 0 also write them to idx_out for the update.
-  uint32_t ixw = 0;
-  if (p.ids != nullptr) {
-    const int32_t* ids = p.ids + b * p.ids_sb;
-    const int32_t cur = ids[Tb - 1];
-    const int blk = base + (lane >> 3);
-    const int j0 = blk * BLK + 8 * (lane & 7);
-    int32_t x[9];  // tokens j0 - 1 .. j0 + 7 (clamped loads, masked below)
+  // workgroups of KV head 0 also write them to idx_out for the update. The ids are loaded here and
+  // compared after the pass's other loads are issued (the comparison waits for them).
+  const int32_t* ids = p.ids != nullptr ? p.ids + b * p.ids_sb : nullptr;
+  const int ix_blk = base + (lane >> 3), ix_j0 = ix_blk * BLK + 8 * (lane & 7);
+  int32_t ix_cur = 0, ix_x[9];  // the current token; tokens j0 - 1 .. j0 + 7 (clamped loads)
+  if (ids != nullptr) {
+    ix_cur = ids[Tb - 1];
 #pragma unroll
-    for (int e = 0; e < 9; ++e) x[e] = ids[min(max(j0 - 1 + e, 0), Tb - 1)];
-    bool hit = false;
-#pragma unroll
-    for (int e = 1; e < 9; ++e) {
-      const int j = j0 + e - 1;
-      hit |= (j < Tb - 1 && x[e] == cur) || (j < Tb && j >= 1 && x[e - 1] == cur);
-    }
-    const uint64_t bal = __ballot(hit);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ixw |= ((bal >> (8 * i)) & 0xffu) != 0 ? 1u << i : 0u;
-    if (h == 0 && (lane & 7) == 0 && blk < nb) p.idx_out[static_cast<int64_t>(b) * p.NBC + blk] = (ixw >> (lane >> 3)) & 1;
+    for (int e = 0; e < 9; ++e) ix_x[e] = ids[min(max(ix_j0 - 1 + e, 0), Tb - 1)];
   }
 
   // Every load is issued without waiting for the flags (an index head's extra loads are unused).
@@ -333,7 +322,23 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
       cr[u] = p.cs_ref[r];
     }
     kb[u] = keep[rc];
-    ib[u] = p.ids != nullptr ? (ixw >> (4 * u + rs)) & 1 : idx[rc];
+    ib[u] = ids != nullptr ? 0u : idx[rc];
+  }
+  if (ids != nullptr) {
+    bool hit = false;
+#pragma unroll
+    for (int e = 1; e < 9; ++e) {
+      const int j = ix_j0 + e - 1;
+      hit |= (j < Tb - 1 && ix_x[e] == ix_cur) || (j < Tb && j >= 1 && ix_x[e - 1] == ix_cur);
+    }
+    const uint64_t bal = __ballot(hit);
+    uint32_t ixw = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ixw |= ((bal >> (8 * i)) & 0xffu) != 0 ? 1u << i : 0u;
+    if (h == 0 && (lane & 7) == 0 && ix_blk < nb)
+      p.idx_out[static_cast<int64_t>(b) * p.NBC + ix_blk] = (ixw >> (lane >> 3)) & 1;
+#pragma unroll
+    for (int u = 0; u < WU; ++u) ib[u] = (ixw >> (4 * u + rs)) & 1;
   }
   float em = NEG_INF, es = 0.f;
   uint32_t wmask = 0;  // attended blocks of this wavefront: bit 4 u + rs

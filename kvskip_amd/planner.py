@@ -199,7 +199,8 @@ class FusedPlanner:
         split) and the [B, Hq, nb] statistics views."""
         B, Hq, D = q.shape
         Hkv = k.shape[1]
-        S = K.num_splits_for(B * Hkv, nb) if seq_lens is None else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv)
+        # one sequence (its length in device memory) is split as an unragged batch
+        S = K.num_splits_for(B * Hkv, nb) if seq_lens is None or B == 1 else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv)
         budget = 0
         if (self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1
                 and (seq_lens is None or B == 1)):
