@@ -170,3 +170,28 @@ def test_planned_pass_validation():
     assert "pass_budget needs B * Hkv <= 16" in lib.kvskip_last_error().decode()
     assert lib.kvskip_decode_splits_planned(ctypes.byref(_args(T=2048)), ctypes.byref(p), None, None) == -1
     assert "attention and plan shapes differ" in lib.kvskip_last_error().decode()
+
+
+def test_planned_ragged_validation():
+    """A ragged batch (seq_lens, B > 1) in kvskip_decode_splits_planned: at most 16 sequences, a
+    contiguous cache, and no pass budget, partial slots, lse_part or DECIDE_POST; refused before any
+    device work."""
+    lib = _native.lib()
+    p = PlanArgs()
+    p.q, p.k, p.k_sb, p.k_sh, p.k_st = 0x1000, 0x2000, 8 * 4096 * 128, 4096 * 128, 128
+    for f in ("csum", "lse_ref", "cs_ref", "keep", "lse_att", "age", "flags", "cs_now", "trig", "block_idx",
+              "block_cnt", "part"):
+        setattr(p, f, 0x10000)
+    p.Hq, p.Hkv, p.T, p.D, p.NBC, p.seq_lens = 32, 8, 4096, 128, 128, 0x20000
+    cases = ((dict(B=17), {}, "at most 16 sequences"),
+             (dict(B=4, pass_budget=100), {}, "takes no pass_budget"),
+             (dict(B=4, slot_count=2), {}, "takes no pass_budget"),
+             (dict(B=4, decide_mode=2), {}, "takes no pass_budget"),
+             (dict(B=4), dict(block_table=0x30000, bt_stride=64, num_pages=64), "contiguous cache"))
+    for pk, ak, msg in cases:
+        q = PlanArgs.from_buffer_copy(p)
+        for k_, v_ in pk.items():
+            setattr(q, k_, v_)
+        a = _args(B=q.B, num_splits=4, part_acc=0x8000, part_ml=0x9000, seq_lens=0x20000, **ak)
+        assert lib.kvskip_decode_splits_planned(ctypes.byref(a), ctypes.byref(q), None, None) == -2, (pk, ak)
+        assert msg in lib.kvskip_last_error().decode(), (pk, ak, lib.kvskip_last_error())
