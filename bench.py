@@ -312,6 +312,15 @@ def main():
     torch.cuda.synchronize()
     us_v = statistics.median(time_events(vsk, args.events, n3, flush))
     us_d3 = statistics.median(time_events(dense3, args.events, n3, flush))
+    # config 2's shape at T 65536 (config 3's K / V, cycled over its copies): the whole dense op
+    # graph-timed as the headline is
+    us_d3g = timed_steps(dense3, args.steps // 2, args.warmup) / (args.steps // 2) * 1e6
+    bytes_d3 = attn_bytes(1, Hq, Hkv, D, Hkv * T3)
+    res["dense_64k"] = {"us_per_step": us_d3g, "GBs": bytes_d3 / us_d3g / 1e3,
+                        "pct_peak": 100 * bytes_d3 / us_d3g / 1e3 / PEAK_GBS, "T": T3, "num_splits": S3,
+                        "kv_copies": n3}
+    log(f"dense 64k: {us_d3g:.2f} us/step, {bytes_d3 / us_d3g / 1e3:.0f} GB/s "
+        f"({100 * bytes_d3 / us_d3g / 1e3 / PEAK_GBS:.1f}% of peak)")
     res["vskip1_cfg3"] = {"us_per_op_median": us_v, "bytes": bytes_v1, "GBs_event_median": bytes_v1 / us_v / 1e3,
                           "v_block_frac": v_blocks / (Hkv * nb3), "dense_us_per_op_median": us_d3,
                           "time_vs_dense": us_v / us_d3, "num_splits": S3}
