@@ -423,9 +423,11 @@ def main():
 
 def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
     """Two-pass V-skip on one layer (NCOPY KV copies), top-p 0.99 GQA union: pass 1 (stats-only + fp16
-    P; its split pass alone, as the op runs it), the device selection (kvskip_select: kept set, lists, per-block scales) and pass 2 (pv over the
-    kept blocks) each timed as a graph-replayed region, and the whole op as the front-end runs it
-    without a host read-back (kvskip.vskip_two_pass(sync=False): pass 2 sized by nb), also replayed."""
+    P; its split pass alone, as the op runs it), the device selection (kvskip_select: kept set, lists,
+    per-block scales), pass 2 (pv over the kept blocks, sized by the longest list) and pass 2 with the
+    selection in it (kvskip_pv_select, sized by nb) each timed as a graph-replayed region, and the
+    whole op as the front-end runs it without a host read-back (kvskip.vskip_two_pass(sync=False):
+    pass 1, then pass 2 with the selection), also replayed."""
     import torch
 
     B, Hq, D = q.shape
@@ -449,6 +451,9 @@ def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
                                             merge=False), args.steps // 2, args.warmup)
     t_sel = events_region(select, args.steps // 2, args.warmup)
     t_p2 = events_region(lambda i: E.pv(P1, vs[i], scales, idx, cnt, S2, False), args.steps // 2, args.warmup)
+    S2n = K.num_splits_for(B * Hkv, nb)             # the op's pass 2 split count (sized by nb)
+    t_p2s = events_region(lambda i: E.pv_select(P1, vs[i], r1[2], r1[3], "topp", 0.99, 2, S2n, False),
+                          args.steps // 2, args.warmup)
     t_op = events_region(lambda i: K.vskip_two_pass(q, ks[i], vs[i], scale, sync=False), args.steps // 2,
                          args.warmup)
     bytes_p1 = B * Hkv * T * D * 2 + B * Hq * D * 2 + B * Hq * nb * 64 * 2 + 2 * B * Hq * nb * 4
@@ -456,11 +461,13 @@ def bench_two_pass(E, K, q, ks, vs, scale, S1, us_dense, args, flush, tag):
     out = {"kept_block_frac": kept / (B * Hkv * nb), "pass1_us": t_p1, "select_us": t_sel, "pass2_us": t_p2,
            "pass1_bytes": bytes_p1, "pass2_bytes": bytes_p2, "pass1_GBs": bytes_p1 / t_p1 / 1e3,
            "pass2_GBs": bytes_p2 / t_p2 / 1e3, "kernels_vs_dense": (t_p1 + t_sel + t_p2) / us_dense,
-           "num_splits_pass2": S2, "op_us": t_op, "op_vs_dense": t_op / us_dense,
-           "op_vs_passes": t_op / (t_p1 + t_p2)}
+           "num_splits_pass2": S2, "pass2_with_select_us": t_p2s, "num_splits_pass2_with_select": S2n,
+           "op_us": t_op, "op_vs_dense": t_op / us_dense, "op_vs_passes": t_op / (t_p1 + t_p2),
+           "op_vs_pass1_and_pass2_with_select": t_op / (t_p1 + t_p2s)}
     log(f"{tag}: kept {kept / (B * Hkv * nb):.3f}; pass 1 {t_p1:.2f} us ({bytes_p1 / t_p1 / 1e3:.0f} GB/s), select "
-        f"{t_sel:.2f} us, pass 2 {t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s); whole op {t_op:.2f} us "
-        f"(x{t_op / us_dense:.3f} of dense, x{t_op / (t_p1 + t_p2):.3f} of the two passes)")
+        f"{t_sel:.2f} us, pass 2 {t_p2:.2f} us ({bytes_p2 / t_p2 / 1e3:.0f} GB/s); pass 2 with the selection in it "
+        f"{t_p2s:.2f} us; whole op {t_op:.2f} us (x{t_op / us_dense:.3f} of dense, x{t_op / (t_p1 + t_p2):.3f} of "
+        f"pass 1 + pass 2, x{t_op / (t_p1 + t_p2s):.3f} of pass 1 + pass 2 with the selection)")
     return out
 
 

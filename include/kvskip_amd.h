@@ -343,6 +343,15 @@ typedef struct kvskip_select_args {
 
 int kvskip_select(const kvskip_select_args* s, void* stream);
 
+/* Two-pass V-skip pass 2 with the selection in it (not in the reference, which selects with torch
+ * ops between its two decode calls, kernels/kvskip.py:157-179): kvskip_select(s) followed by
+ * kvskip_pv(a) over the lists and scales it writes, in one launch (+ the split merge): every
+ * workgroup of the pass makes its (b, KV head)'s selection, takes its split of the kept blocks
+ * (ascending) and computes their scales. Same results bit for bit. a: as for kvskip_pv without
+ * block_idx / block_cnt / blk_scale (contiguous cache, no seq_lens); s: the selection, over the
+ * same B, Hq, Hkv and nb; its outputs (keep, block_idx / block_cnt, blk_scale) are optional. */
+int kvskip_pv_select(const kvskip_attn_args* a, const kvskip_select_args* s, void* stream);
+
 /* The kept-first block list of a keep mask keep [B, Hkv, nb] (uint8, nonzero = kept): block_idx
  * [B, Hkv, nb] the kept blocks ascending then the others ascending, block_cnt [B, Hkv]. The device
  * form of make_plan (kernels/kvskip.py:79-85, a stable argsort of ~keep). */

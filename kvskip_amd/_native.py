@@ -97,6 +97,7 @@ SIGNATURES = {
                            c_int32, c_void_p, c_void_p, c_int64, c_int32, c_void_p], c_int),
     "kvskip_token_index": ([c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int32, c_void_p, c_void_p], c_int),
     "kvskip_select": ([POINTER(SelectArgs), c_void_p], c_int),
+    "kvskip_pv_select": ([POINTER(AttnArgs), POINTER(SelectArgs), c_void_p], c_int),
     "kvskip_block_list": ([c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p], c_int),
     "kvskip_last_error": ([], c_char_p),
     "kvskip_version": ([], c_char_p),

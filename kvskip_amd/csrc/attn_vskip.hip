@@ -2,6 +2,7 @@
 // ceiling; see attn_common.hpp for the shared decomposition and layouts.
 #include "attn_common.hpp"
 #include "planner_common.hpp"
+#include "select.hpp"
 
 namespace kvs {
 namespace {
@@ -267,19 +268,19 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
 // Two-pass V-skip, pass 2: acc = sum over listed blocks of (blk_scale * P) . V; the weights
 // are normalised already, so no softmax and the splits simply add up.
 // PAGED: V in pages of a pool through p.block_table; the listed blocks' pages are gathered into LDS.
-template <int D, int G, bool PAGED = false>
-__global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
+// The workgroup body of pass 2 for split `split` of (b, KV head h), whose list holds n_items blocks:
+// list_at(pos) is the block at list position pos (this split's positions [i0, i0 + n)), scale_at(blk,
+// g) query head g's weight scale of block blk.
+template <int D, int G, bool PAGED, class ListAt, class ScaleAt>
+__device__ __forceinline__ void pv_body(const AttnP& p, int split, int h, int b, int n_items, ListAt list_at,
+                                        ScaleAt scale_at) {
   constexpr int GP = gpad<G>();
   __shared__ int sPg[PAGED ? MAX_NB : 1];
   __shared__ int sBk[PAGED ? MAX_NB : 1];
   __shared__ __attribute__((aligned(16))) float sP[NWAVE][BLK * GP];
   __shared__ __attribute__((aligned(16))) MergeLds<D, G> sL;
 
-  int split, h, b;
-  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
-  const int n_items = min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
-  const int* list = p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks;
   const int per = (n_items + p.num_splits - 1) / p.num_splits;
   const int i0 = min(n_items, split * per);
   const int n = min(n_items, i0 + per) - i0;
@@ -304,7 +305,7 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
   // item they read nothing from memory (below) and nothing is accumulated.
   constexpr int R = 2;
   const int nw = n > wave ? (n - wave + NWAVE - 1) / NWAVE : 0;
-  auto entry_of = [&](int k) -> int { return list[i0 + wave + NWAVE * min(k, nw - 1)]; };
+  auto entry_of = [&](int k) -> int { return list_at(i0 + wave + NWAVE * min(k, nw - 1)); };
   auto block_of = [&](int e) -> int {
     const int blk = __builtin_amdgcn_readfirstlane(e);
     return (blk >= 0 && blk < p.nb) ? blk : -1;
@@ -324,7 +325,7 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
     else
       load_v_block<D>(it.vr, rv, voff, p.v_st, blk == PAST ? p.nb * BLK : t0);
     const int g = pg < G ? pg : 0;
-    it.f = p.blk_scale[((static_cast<int64_t>(b) * p.Hkv + h) * p.nb + max(blk, 0)) * G + g];
+    it.f = scale_at(max(blk, 0), g);
     it.raw = ld16(p.p_in + (hq0 + g) * p.t_pad + t0 + 8 * ppart);
   };
   auto accumulate = [&](const Item& it, int blk) {
@@ -342,7 +343,7 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
     pv_block<D, G>(acc, it.vr, sPw, lane);
     __builtin_amdgcn_wave_barrier();
   };
-  if constexpr (PAGED) gather_pages(p, b, n, p.nb, [&](int t) { return list[i0 + t]; }, sPg, sBk);
+  if constexpr (PAGED) gather_pages(p, b, n, p.nb, [&](int t) { return list_at(i0 + t); }, sPg, sBk);
   if (PAGED && nw > 0) {
     // the same ring over the LDS copy of this split's entries and their pages
     Item I0, I1;
@@ -401,6 +402,58 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
     }
   }
   finish<D, G, true>(p, m, l, acc, b, h, split, sL, true);
+}
+
+template <int D, int G, bool PAGED = false>
+__global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
+  int split, h, b;
+  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+  const int n_items = min(max(p.block_cnt[b * p.Hkv + h], 0), p.max_blocks);
+  const int* list = p.block_idx + static_cast<int64_t>(b * p.Hkv + h) * p.max_blocks;
+  const float* scale = p.blk_scale + (static_cast<int64_t>(b) * p.Hkv + h) * p.nb * G;
+  pv_body<D, G, PAGED>(p, split, h, b, n_items, [&](int pos) { return list[pos]; },
+                       [&](int blk, int g) { return scale[static_cast<int64_t>(blk) * G + g]; });
+}
+
+// Pass 2 with the selection in its prologue (kvskip_pv_select): every workgroup of (b, KV head h)
+// makes the head's selection (select_core over the statistics in sel; split 0 also writes its
+// outputs), takes split `split` of the kept blocks ascending (the list kvskip_select writes) and
+// computes each block's scale exp(blk_max - lse over the kept blocks) as kvskip_select does, so the
+// result is kvskip_select then kvskip_pv's, bit for bit, without the selection's launch.
+template <int D, int G, int R>
+__global__ void __launch_bounds__(NT, R > 16 ? 1 : 2) pv_select_kernel(const AttnP p, const kvskip_select_args sel) {
+  __shared__ uint64_t sKeep[R];
+  __shared__ float sLk[SEL_MAX_G];
+  __shared__ int sPre[R + 1];                 // kept blocks before slot r
+  __shared__ int sList[MAX_NB];               // this split's kept blocks, positions i0 ..
+  int split, h, b;
+  work_coords(p.num_splits, p.Hkv, p.B, split, h, b);
+  select_core<R>(sel, h, b, sKeep, sLk, split == 0);
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    int acc = 0;
+    for (int r = 0; r < R; ++r) {
+      sPre[r] = acc;
+      acc += __popcll(sKeep[r]);
+    }
+    sPre[R] = acc;
+  }
+  __syncthreads();
+  const int n_items = sPre[R];
+  const int per = (n_items + p.num_splits - 1) / p.num_splits;
+  const int i0 = min(n_items, split * per), i1 = min(n_items, i0 + per);
+  const int nb = sel.nb;
+  for (int i = tid; i < nb; i += NT) {
+    const uint64_t w = sKeep[i / WAVE];
+    if ((w >> (i % WAVE)) & 1) {
+      const int rank = sPre[i / WAVE] + __popcll(w & ((1ull << (i % WAVE)) - 1));
+      if (rank >= i0 && rank < i1) sList[rank - i0] = i;
+    }
+  }
+  __syncthreads();
+  const int64_t hq0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;
+  pv_body<D, G, false>(p, split, h, b, n_items, [&](int pos) { return sList[pos - i0]; },
+                       [&](int blk, int g) { return __expf(sel.blk_max[(hq0 + g) * nb + blk] - sLk[g]); });
 }
 
 // Streaming read: workgroup i reads the i-th contiguous chunk of n 16-byte words, each thread
@@ -471,6 +524,29 @@ hipError_t launch_vskip1(const AttnP& p, int D, int G, hipStream_t s) {
 hipError_t launch_pv(const AttnP& p, int D, int G, hipStream_t s) {
 #define KVS_CASE(DD, GG) \
   if (D == DD && G == GG) return launch_pv_t<DD, GG>(p, s);
+  KVS_FOR_G(KVS_CASE, 64)
+  KVS_FOR_G(KVS_CASE, 128)
+#undef KVS_CASE
+  return hipErrorInvalidValue;
+}
+
+template <int D, int G>
+hipError_t launch_pv_select_t(const AttnP& p, const kvskip_select_args& sel, hipStream_t s) {
+  const int r = (sel.nb + WAVE - 1) / WAVE;
+  const dim3 grid = attn_grid(p), blk(NT);
+  if (r <= 4) hipLaunchKernelGGL((pv_select_kernel<D, G, 4>), grid, blk, 0, s, p, sel);
+  else if (r <= 8) hipLaunchKernelGGL((pv_select_kernel<D, G, 8>), grid, blk, 0, s, p, sel);
+  else if (r <= 16) hipLaunchKernelGGL((pv_select_kernel<D, G, 16>), grid, blk, 0, s, p, sel);
+  else hipLaunchKernelGGL((pv_select_kernel<D, G, 64>), grid, blk, 0, s, p, sel);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.num_splits > 1) e = launch_combine(p, D, true, s);
+  return e;
+}
+
+hipError_t launch_pv_select(const AttnP& p, const kvskip_select_args& sel, int D, int G, hipStream_t s) {
+#define KVS_CASE(DD, GG) \
+  if (D == DD && G == GG) return launch_pv_select_t<DD, GG>(p, sel, s);
   KVS_FOR_G(KVS_CASE, 64)
   KVS_FOR_G(KVS_CASE, 128)
 #undef KVS_CASE

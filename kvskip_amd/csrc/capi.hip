@@ -434,7 +434,7 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
                   "kvskip_decode_splits_planned");
 }
 
-int kvskip_select(const kvskip_select_args* s, void* stream) {
+static int check_select(const kvskip_select_args* s) {
   if (s == nullptr) return fail(KVSKIP_E_INVALID, "null argument block");
   if (s->blk_max == nullptr || s->blk_sum == nullptr) return fail(KVSKIP_E_INVALID, "select: blk_max / blk_sum");
   if (s->B < 1 || s->Hq < 1 || s->Hkv < 1 || s->nb < 1) return fail(KVSKIP_E_INVALID, "sizes must be positive");
@@ -445,7 +445,31 @@ int kvskip_select(const kvskip_select_args* s, void* stream) {
   if (s->rule != 0 && s->rule != 1) return fail(KVSKIP_E_INVALID, "rule must be tau or topp");
   if (!(s->value > 0.f) || s->local < 0) return fail(KVSKIP_E_INVALID, "select: value > 0, local >= 0");
   if (s->block_idx != nullptr && s->block_cnt == nullptr) return fail(KVSKIP_E_INVALID, "block_cnt is required with block_idx");
+  return KVSKIP_OK;
+}
+
+int kvskip_select(const kvskip_select_args* s, void* stream) {
+  const int rc = check_select(s);
+  if (rc != KVSKIP_OK) return rc;
   return launched(kvs::launch_select(*s, static_cast<hipStream_t>(stream)), "kvskip_select");
+}
+
+int kvskip_pv_select(const kvskip_attn_args* a, const kvskip_select_args* s, void* stream) {
+  int rc = check_select(s);
+  if (rc != KVSKIP_OK) return rc;
+  kvs::AttnP p;
+  if ((rc = prepare_attn(a, false, false, true, &p)) != KVSKIP_OK) return rc;
+  if (a->seq_lens != nullptr || a->block_table != nullptr)
+    return fail(KVSKIP_E_UNSUPPORTED, "pv_select: a contiguous cache without seq_lens (else kvskip_select, kvskip_pv)");
+  if (s->B != a->B || s->Hq != a->Hq || s->Hkv != a->Hkv || s->nb != p.nb)
+    return fail(KVSKIP_E_INVALID, "pv_select: the selection's B, Hq, Hkv, nb differ from the pass's");
+  if (a->p_in == nullptr) return fail(KVSKIP_E_INVALID, "P: fp16 [B, Hq, t_pad]");
+  if (!aligned16(a->p_in)) return fail(KVSKIP_E_INVALID, "P must be 16-byte aligned");
+  if (a->out == nullptr) return fail(KVSKIP_E_INVALID, "out is required");
+  if (a->num_splits > 1 && a->part_acc == nullptr)
+    return fail(KVSKIP_E_INVALID, "num_splits > 1 needs the split partial buffers");
+  return launched(kvs::launch_pv_select(p, *s, a->D, a->Hq / a->Hkv, static_cast<hipStream_t>(stream)),
+                  "kvskip_pv_select");
 }
 
 int kvskip_block_list(const uint8_t* keep, int32_t B, int32_t Hkv, int32_t nb, int32_t* block_idx,

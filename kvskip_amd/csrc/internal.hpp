@@ -63,6 +63,8 @@ hipError_t launch_decode_paged(const AttnP& p, int D, int G, bool masked, bool s
                                hipStream_t s);
 hipError_t launch_vskip1(const AttnP& p, int D, int G, hipStream_t s);
 hipError_t launch_pv(const AttnP& p, int D, int G, hipStream_t s);
+// Two-pass V-skip pass 2 with the selection of sel in its prologue (then its split merge).
+hipError_t launch_pv_select(const AttnP& p, const kvskip_select_args& sel, int D, int G, hipStream_t s);
 hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, hipStream_t s);
 
 hipError_t launch_plan(const kvskip_plan_args& p, hipStream_t s);

@@ -678,6 +678,13 @@ def select(blk_max, blk_sum, Hkv, rule, value, local=2, keep=None, block_idx=Non
     Fills whichever outputs are given: keep uint8 [B, Hkv, nb], block_idx / block_cnt int32 ([B, Hkv, nb]
     kept first ascending, [B, Hkv]) and blk_scale fp32 [B, Hkv, nb, G] (exp(blk_max - lse over the kept
     blocks), 0 off the set)."""
+    a = _select_args(blk_max, blk_sum, Hkv, rule, value, local, keep, block_idx, block_cnt, blk_scale)
+    dev = blk_max.device
+    with torch.cuda.device(dev):
+        _native.check(_native.lib().kvskip_select(ctypes.byref(a), _stream(dev)))
+
+
+def _select_args(blk_max, blk_sum, Hkv, rule, value, local, keep, block_idx, block_cnt, blk_scale):
     _require(rule in _RULES, "rule must be tau or topp")
     check_f32(blk_max, "blk_max")
     check_f32(blk_sum, "blk_sum")
@@ -697,9 +704,38 @@ def select(blk_max, blk_sum, Hkv, rule, value, local=2, keep=None, block_idx=Non
                      f"{name}: contiguous {dtype} {list(shape)} on the device")
             setattr(a, name, t.data_ptr())
     _require(block_idx is None or block_cnt is not None, "block_cnt is required with block_idx")
-    dev = blk_max.device
+    return a
+
+
+def pv_select(P, v, blk_max, blk_sum, rule, value, local=2, num_splits=1, want_f32=False, keep=None,
+              block_idx=None, block_cnt=None, blk_scale=None):
+    """Two-pass V-skip pass 2 with the selection in it (kvskip_pv_select; not in kvskip_ext): select()
+    on pass 1's statistics, then pv() over the kept blocks and their scales, in one launch (+ the split
+    merge), the same results bit for bit. Contiguous cache. keep / block_idx / block_cnt / blk_scale:
+    select()'s outputs, filled if given. Returns [out bf16, out_f32 or None]."""
+    check_kv(v, "v")
+    _require(P.is_cuda and P.dtype == torch.float16 and P.dim() == 3 and P.is_contiguous(), "P: fp16 [B, Hq, t_pad]")
+    B, Hkv, T, D = v.shape
+    Hq = P.shape[1]
+    nb = (T + TILE - 1) // TILE
+    _require(P.shape[0] == B and P.shape[2] == nb * TILE, "P shape")
+    _require(tuple(blk_max.shape) == (B, Hq, nb), "blk_max: [B, Hq, nb] of the pass's cache")
+    _require(num_splits >= 1, "num_splits >= 1")
+    sa = _select_args(blk_max, blk_sum, Hkv, rule, value, local, keep, block_idx, block_cnt, blk_scale)
+    dev = v.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    out32 = torch.empty(B, Hq, D, **f32) if want_f32 else None
+    part_acc = torch.empty(B, Hq, num_splits, D, **f32) if num_splits > 1 else None
+    part_ml = torch.empty(B, Hq, num_splits, 2, **f32) if num_splits > 1 else None
+    a = _attn_args(None, None, v, 1.0, B, Hq, Hkv, T, D)
+    a.num_splits = int(num_splits)
+    a.part_acc, a.part_ml = _ptr(part_acc), _ptr(part_ml)
+    a.out, a.out_f32 = out.data_ptr(), _ptr(out32)
+    a.p_in = P.data_ptr()
     with torch.cuda.device(dev):
-        _native.check(_native.lib().kvskip_select(ctypes.byref(a), _stream(dev)))
+        _native.check(_native.lib().kvskip_pv_select(ctypes.byref(a), ctypes.byref(sa), _stream(dev)))
+    return [out, out32]
 
 
 def block_list(keep, block_idx, block_cnt):

@@ -181,11 +181,13 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
                    sync: bool = True, out_f32: bool = False, block_table: torch.Tensor | None = None,
                    T: int | None = None) -> dict:
     """Two-pass V-skip (kernels/kvskip.py:157-179). Pass 1 reads K once, writing the block statistics
-    and P (its split pass alone: the log-sum-exp merge is not needed); the device selection
-    (kvskip_select) turns the statistics into the kept set, its lists and the per-block scales
-    exp(blk_max - lse over the kept set); pass 2 reads P and V of the kept blocks.
-    Returns out, keep [B, Hkv, nb] bool and, with sync=True, kept_frac (that read-back also sizes pass
-    2's split count by the longest list). block_table, T (not in the reference): page pools."""
+    and P (its split pass alone: the log-sum-exp merge is not needed); the device selection turns
+    the statistics into the kept set and the per-block scales exp(blk_max - lse over the kept set);
+    pass 2 reads P and V of the kept blocks. Over a contiguous cache the selection runs inside pass 2
+    (kvskip_pv_select: two launches and the merge); over pages it is its own launch (kvskip_select)
+    and, with sync=True, the read-back of the longest list sizes pass 2's split count.
+    Returns out, keep [B, Hkv, nb] bool and, with sync=True, kept_frac. block_table, T (not in the
+    reference): page pools."""
     q = _as_bhd(q)
     B, Hq = q.shape[:2]
     Hkv = k.shape[1]
@@ -193,6 +195,14 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
     nb = first["blk_max"].shape[-1]
     dev = q.device
     keep = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=dev)
+    if block_table is None:
+        out, o32 = ext().pv_select(first["p"], v, first["blk_max"], first["blk_sum"], rule, value, local,
+                                   num_splits_for(B * Hkv, nb), out_f32, keep=keep)
+        res = {"out": out, "keep": keep.view(torch.bool),
+               "kept_frac": float(keep.sum()) / (B * Hkv * nb) if sync else None}
+        if out_f32:
+            res["out_f32"] = o32
+        return res
     idx, cnt = _lists(B, Hkv, nb, dev)
     scales = torch.empty(B, Hkv, nb, Hq // Hkv, dtype=torch.float32, device=dev)
     ext().select(first["blk_max"], first["blk_sum"], Hkv, rule, value, local, keep=keep, block_idx=idx,

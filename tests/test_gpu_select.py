@@ -120,3 +120,41 @@ def test_vskip_two_pass_on_device(gpu, G, D, T):
     r2 = K.vskip_two_pass(q, k, v, run.scale, sync=False)
     assert r2["kept_frac"] is None and torch.equal(r2["keep"], r["keep"])
     rel_ok(r2["out"], ref, (G, D, T, "no sync"))
+
+
+@pytest.mark.parametrize("G,D,T", [(4, 128, 32768), (1, 64, 200), (2, 128, 9000), (7, 128, 5000), (8, 64, 3001),
+                                   (4, 64, 65536 * 4)])
+@pytest.mark.parametrize("rule,value", [("topp", 0.99), ("tau", 0.004)])
+def test_pv_select_matches_select_then_pv(gpu, G, D, T, rule, value):
+    """kvskip_pv_select (the selection in pass 2's prologue) against kvskip_select followed by kvskip_pv
+    over its lists and scales, on pass 1's statistics and P, at the same split count: every output
+    bit for bit (out, out_f32, the keep mask, the lists and counts, the scales), for 1..64 statistics
+    slots of 64 blocks per lane (nb 4 .. 4096)."""
+    from kvskip_amd import workloads as W
+    B, Hkv = (1, 8) if T <= 65536 else (1, 2)
+    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=T, steps=1, seed=70 + G)
+    q, k, v = run.q0[0].to(torch.bfloat16).cuda(), run.k[0][:, :, :T].cuda(), run.v[0][:, :, :T].cuda()
+    first = K.decode(q, k, v, run.scale, stats=True, load_v=False, write_p=True, merge=False)
+    bm, bs, P = first["blk_max"], first["blk_sum"], first["p"]
+    Hq, nb = Hkv * G, bm.shape[-1]
+    dev = q.device
+    outs = []
+    for fused in (False, True):
+        keep = torch.full((B, Hkv, nb), 7, dtype=torch.uint8, device=dev)
+        idx = torch.full((B, Hkv, nb), -7, dtype=torch.int32, device=dev)
+        cnt = torch.full((B, Hkv), -7, dtype=torch.int32, device=dev)
+        sc = torch.full((B, Hkv, nb, G), math.nan, dtype=torch.float32, device=dev)
+        for S in (1, K.num_splits_for(B * Hkv, nb)):
+            if fused:
+                o, o32 = E.pv_select(P, v, bm, bs, rule, value, 2, S, True, keep=keep, block_idx=idx,
+                                     block_cnt=cnt, blk_scale=sc)
+            else:
+                E.select(bm, bs, Hkv, rule, value, 2, keep=keep, block_idx=idx, block_cnt=cnt, blk_scale=sc)
+                o, o32 = E.pv(P, v, sc, idx, cnt, S, True)
+            outs.append((S, o, o32, keep.clone(), idx.clone(), cnt.clone(), sc.clone()))
+    n = len(outs) // 2
+    for a, b in zip(outs[:n], outs[n:]):
+        assert a[0] == b[0]
+        for x, y in zip(a[1:], b[1:]):
+            assert torch.equal(x, y), (G, D, T, rule, a[0])
+    assert 0 < int(outs[0][5].sum()) <= B * Hkv * nb
