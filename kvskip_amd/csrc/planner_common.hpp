@@ -127,18 +127,17 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
     const int64_t hq = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G + g;
     // the attended log-sum-exp: lse_att, or from the split partials of this step's attended pass
     // (max and sum in log2 units; team lane t takes slots t, t + 8, ...)
+    // Every load of the round is issued before any value is used: a load whose value is used in
+    // the branch that issues it waits there, one memory round trip per branch.
     float lm[LSI], ls[LSI];
     const bool from_part = p.lse_part != nullptr;
+    float2 lx[LSI];
 #pragma unroll
-    for (int i = 0; i < LSI; ++i) {
-      const int sl = t + DLP * i;
-      lm[i] = NEG_INF;
-      ls[i] = 0.f;
-      if (from_part && sl < p.lse_slots) {
-        const float2 x = *reinterpret_cast<const float2*>(p.lse_part + (hq * p.lse_stride + sl) * 2);
-        lm[i] = x.x * LN2;
-        ls[i] = x.y;
-      }
+    for (int i = 0; i < LSI; ++i) lx[i] = make_float2(NEG_INF, 0.f);
+    if (from_part) {  // uniform; slots clamped into [0, lse_slots), the ones past it masked below
+#pragma unroll
+      for (int i = 0; i < LSI; ++i)
+        lx[i] = *reinterpret_cast<const float2*>(p.lse_part + (hq * p.lse_stride + min(t + DLP * i, p.lse_slots - 1)) * 2);
     }
     const float la_mem = from_part ? 0.f : p.lse_att[hq];
     const int NI = (C + DLP - 1) / DLP;  // chunk rounds of the team (uniform)
@@ -148,11 +147,22 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
       pm[i] = NEG_INF;
       ps[i] = 0.f;
       if (i < NI) {
-        const int c = t + DLP * i, cc = min(c, C - 1);
-        const float mv = pb[cc * SP + g], sv = pb[cc * SP + G + g];
-        pm[i] = c < C ? mv : NEG_INF;
-        ps[i] = c < C ? sv : 0.f;
+        const int cc = min(t + DLP * i, C - 1);
+        pm[i] = pb[cc * SP + g];
+        ps[i] = pb[cc * SP + G + g];
       }
+    }
+#pragma unroll
+    for (int i = 0; i < LSI; ++i) {
+      const bool in = from_part && t + DLP * i < p.lse_slots;
+      lm[i] = in ? lx[i].x * LN2 : NEG_INF;
+      ls[i] = in ? lx[i].y : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const bool in = i < NI && t + DLP * i < C;
+      pm[i] = in ? pm[i] : NEG_INF;
+      ps[i] = in ? ps[i] : 0.f;
     }
     float m = NEG_INF, sv = 0.f;
 #pragma unroll
