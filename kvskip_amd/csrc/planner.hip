@@ -252,11 +252,17 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;
   float* csum = p.csum + bh * p.NBC * D;
   const uint8_t* keep = p.keep + bh * p.NBC;
-  const int fl = p.flags[h];
+  // The head's flags and latch are read through indices the compiler takes for per-lane ones: as
+  // uniform values they went to scalar registers, a wait for each load before the pass's other loads
+  // were issued (the code branching on them was hoisted above those loads).
+  int hv = h, bhv = static_cast<int>(bh);
+  asm volatile("" : "+v"(hv), "+v"(bhv));
+  const int fl = p.flags[hv];
   const bool ixh = (fl & 2) != 0;  // token-index head: index + sink + local, no estimate
-  const bool ax = p.aix != nullptr && p.aix[bh] != 0;
+  const uint8_t axv = (p.aix != nullptr ? p.aix : p.keep)[bhv];  // p.keep: in-bounds stand-in
+  const bool ax = (p.aix != nullptr) & (axv != 0);
   const bool have_ix = p.idx != nullptr || p.ids != nullptr;  // ids: the index is found here
-  const bool uni = have_ix && ((fl & 4) || ax);
+  const bool uni = have_ix & (((fl & 4) != 0) | ax);  // no short circuit: a branch here waited for the loads
   const uint8_t* idx = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
   const bool use_idx = have_ix && (ixh || uni);
   __shared__ float sM[WW][G], sS[WW][G];
@@ -280,6 +286,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   const int rs = lane >> 4, c16 = lane & 15, gl = min(c16, G - 1);
   float qf[G][DL];
   uint2 kx[DW];
+  bool have_kr = true;
   {
     const uint16_t* q = reinterpret_cast<const uint16_t*>(p.q);
 #pragma unroll
@@ -294,11 +301,14 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
         qf[g][4 * w + 3] = bf_hi(t.y) * p.scale;
       }
     }
+    // the appended key row (none on an invalid page: read from the pool's first row, added as zeros),
+    // loaded unconditionally so that no wait for it precedes the loads below
     const uint16_t* kr = key_row(reinterpret_cast<const uint16_t*>(p.k), p.k_sb, p.k_sh, p.k_st, b, h, Tb - 1,
                                  p.block_table, p.bt_stride, p.num_pages);
+    have_kr = kr != nullptr;
+    const uint16_t* krs = have_kr ? kr : reinterpret_cast<const uint16_t*>(p.k);
 #pragma unroll
-    for (int w = 0; w < DW; ++w)
-      kx[w] = kr != nullptr ? *reinterpret_cast<const uint2*>(kr + 64 * w + 4 * c16) : make_uint2(0u, 0u);
+    for (int w = 0; w < DW; ++w) kx[w] = *reinterpret_cast<const uint2*>(krs + 64 * w + 4 * c16);
   }
   const bool add = p.add_token != 0 && !ixh;
 
@@ -354,10 +364,11 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
     if (add && blk == nb - 1) {
 #pragma unroll
       for (int w = 0; w < DW; ++w) {
-        cv[u][4 * w] += bf_lo(kx[w].x);
-        cv[u][4 * w + 1] += bf_hi(kx[w].x);
-        cv[u][4 * w + 2] += bf_lo(kx[w].y);
-        cv[u][4 * w + 3] += bf_hi(kx[w].y);
+        const uint2 kv = have_kr ? kx[w] : make_uint2(0u, 0u);
+        cv[u][4 * w] += bf_lo(kv.x);
+        cv[u][4 * w + 1] += bf_hi(kv.x);
+        cv[u][4 * w + 2] += bf_lo(kv.y);
+        cv[u][4 * w + 3] += bf_hi(kv.y);
         *reinterpret_cast<float4*>(csum + static_cast<int64_t>(blk) * D + 64 * w + 4 * c16) =
             make_float4(cv[u][4 * w], cv[u][4 * w + 1], cv[u][4 * w + 2], cv[u][4 * w + 3]);
       }
