@@ -133,6 +133,9 @@ def main():
     ap.add_argument("--pmc-paths", action="store_true",
                     help="profiling target only: config 2 masked + stats, the peaked two-pass V-skip op, a short "
                          "config-4 planner loop, + copy kernels of known size, then exit")
+    ap.add_argument("--planner-only", action="store_true",
+                    help="profiling target only: the config-4 planner loop (--planner-layers x --planner-steps), "
+                         "its result as one JSON line, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -149,6 +152,10 @@ def main():
     torch.cuda.set_device(dev)
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name}, {props.multi_processor_count} CUs")
+    if args.planner_only:
+        res = bench_planner(dev, layers=args.planner_layers, steps=args.planner_steps)
+        print(json.dumps({"planner_cfg4": res}, default=float))
+        return
 
     # ---- config 2 inputs: one structured layer, NCOPY distinct copies of K/V in HBM
     L, keep = W.cfg2(device=dev)
