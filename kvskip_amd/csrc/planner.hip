@@ -423,11 +423,18 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
 template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int Tb = seq_T(p.seq_lens, b, p.T);
-  const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
-  if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
+  // The sequence's length, used only after the decision: loaded first through an index the
+  // compiler takes for a per-lane one (a vector load, waited for at its use; as a scalar load its
+  // wait came before the decision's loads were issued). Without lengths lse_ref stands in (read
+  // only here, at least B entries), its value unused.
+  int bv = b;
+  asm volatile("" : "+v"(bv));
+  const int32_t sl = (p.seq_lens != nullptr ? p.seq_lens : reinterpret_cast<const int32_t*>(p.lse_ref))[bv];
   uint32_t mk[DCL];
   const bool tr = decide_head<G>(p, b, h, lane, mk, true, true);
+  const int Tb = p.seq_lens != nullptr ? min(max(sl, 1), p.T) : p.T;  // seq_T's rule
+  const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
+  if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
   write_block_list(p, static_cast<int64_t>(b) * p.Hkv + h, nb, tr, mk, lane);
 }
 
