@@ -459,7 +459,6 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
   }
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int nbl = (p.T + BLK - 1) / BLK;                       // row length of the statistics
-  const int nb = (seq_T(p.seq_lens, b, p.T) + BLK - 1) / BLK;   // the sequence's blocks
   const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
   const int64_t hrow0 = static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G;  // head g: hrow0 + g
   __shared__ uint64_t sKm[G][R];  // each query head's top-p blocks (lane bits of r)
@@ -467,13 +466,27 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
   __shared__ uint64_t sHist[NWV][256];  // each wavefront's top-p histogram
   uint8_t* keep = p.keep + bh * p.NBC;
   const uint8_t* ixp = p.idx != nullptr ? p.idx + static_cast<int64_t>(b) * p.NBC : keep;  // keep: stand-in
-  const bool tr = p.trig[bh] != 0;
-  const int fl = p.flags != nullptr ? p.flags[h] : 0;
-  const bool uni = p.idx != nullptr && ((fl & 4) || (p.aix != nullptr && p.aix[bh] != 0));
+  // The sequence's length and the head's flags, trigger, latch and calibration are read through
+  // indices the compiler takes for per-lane ones, without branches: as uniform values they went to
+  // scalar registers, a wait for each load before the statistics loads below were issued. Where a
+  // pointer may be null, the block statistics stand in (read only here, at least B Hkv entries;
+  // the value is then unused).
+  int bv = b, hv = h, bhv = static_cast<int>(bh);
+  asm volatile("" : "+v"(bv), "+v"(hv), "+v"(bhv));
+  const float* sti = p.blk_max;
+  const int32_t sl = (p.seq_lens != nullptr ? p.seq_lens : reinterpret_cast<const int32_t*>(sti))[bv];
+  const bool tr = p.trig[bhv] != 0;
+  const int fl_raw = (p.flags != nullptr ? p.flags : reinterpret_cast<const int32_t*>(sti))[hv];
+  const uint8_t ax_raw = (p.aix != nullptr ? p.aix : reinterpret_cast<const uint8_t*>(sti))[bhv];
+  const float est_raw = (p.calib != nullptr ? p.est : sti)[bhv];
+  const float cal_raw = (p.calib != nullptr ? p.calib : sti)[bhv];
+  const int fl = p.flags != nullptr ? fl_raw : 0;
+  const bool uni = (p.idx != nullptr) & (((fl & 4) != 0) | ((p.aix != nullptr) & (ax_raw != 0)));
   const bool ixh = (fl & 2) != 0;  // token-index head: read index + sink + local (list_stats)
-  const float est0 = p.calib != nullptr ? p.est[bh] : 0.f;
-  const float cal0 = p.calib != nullptr ? p.calib[bh] : 0.f;
+  const float est0 = p.calib != nullptr ? est_raw : 0.f;
+  const float cal0 = p.calib != nullptr ? cal_raw : 0.f;
 
+  const int nb = ((p.seq_lens != nullptr ? min(max(sl, 1), p.T) : p.T) + BLK - 1) / BLK;  // the sequence's blocks (seq_T's rule)
   float x[HPW][R];     // block log-weights blk_max + log blk_sum (-inf where not read / past nb)
   uint64_t kp = 0;     // bit r: block in the stored set before this update
   uint64_t att = 0;    // bit r: block attended this step (stored set + sink + local + index union)
@@ -482,8 +495,8 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
     float bm[HPW][RC], bs[HPW][RC];
     uint32_t kb[RC], ib[RC];
 #pragma unroll
-    for (int r = 0; r < RC; ++r) {  // loads of the chunk first, clamped in range
-      const int ic = min(lane + WAVE * (c + r), nb - 1);
+    for (int r = 0; r < RC; ++r) {  // loads of the chunk first, clamped into the row (slots past nb masked)
+      const int ic = min(lane + WAVE * (c + r), nbl - 1);
 #pragma unroll
       for (int j = 0; j < HPW; ++j) {
         const int64_t row = hrow0 + min(wave + NWV * j, G - 1);
