@@ -396,6 +396,8 @@ def main():
                                             Hq=28, Hkv=4, ragged=lens5, dense_layer0=False, seed=5, chunk=8,
                                             tag="cfg5")
         torch.cuda.empty_cache()
+        res["planner_cfg5"]["oracle_agreement"] = planner_agreement(dev, cfg=5)
+        torch.cuda.empty_cache()
 
     achieved = bytes_split / t_split / 1e3
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -748,57 +750,85 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     return out
 
 
-def planner_agreement(dev):
-    """Decision agreement of the config-4 planner loop with the oracle's refresh_pre loop as frozen in
-    tests/golden/planner_cfg4.npz (its two planned layers, 128 steps, updates carried, the decision in
-    the pass, the token index found from the ids; untimed). Inputs regenerated on the CPU and checked
-    against the fixture's digest. Per (layer, step, KV head): identical read sets (the reference's
-    criterion, bench/test_planner.py:100-133) and identical refresh decisions; the oracle's smallest
-    decision margin |estimate - delta| over the run (a refresh by age or a forced head has none), and
-    the margins of the head-steps whose decision differs."""
+def planner_agreement(dev, cfg=4):
+    """Decision agreement of the device planner loop with the oracle's refresh_pre loop as frozen in
+    tests/golden/planner_cfg{4,5}.npz (untimed). Config 4: its two planned layers, 128 steps, updates
+    carried, the decision in the pass, the token index found from the ids. Config 5: B 16 ragged
+    contexts, 28 / 4 heads, 64 steps, one layer (plan's decision launch). Inputs regenerated on the
+    CPU and checked against the fixture's digest. Per (layer or sequence, step, KV head): identical
+    read sets (the reference's criterion, bench/test_planner.py:100-133) and identical refresh
+    decisions; the oracle's smallest decision margin |estimate - delta| over the run (a refresh by
+    age or a forced head has none), and the margins of the head-steps whose decision differs (a
+    free-running loop that leaves the oracle at a float32 near tie stays apart until a common
+    refresh: tests/test_gpu_loop_full.py tracks that)."""
     import numpy as np
     import torch
 
     from kvskip_amd import workloads as W
     from kvskip_amd.planner import FusedPlanner, Policy, UpdateCarrier
 
-    d = np.load(Path(__file__).resolve().parent / "tests" / "golden" / "planner_cfg4.npz", allow_pickle=False)
-    run, layers, qs = W.loop_inputs(4)
+    d = np.load(Path(__file__).resolve().parent / "tests" / "golden" / f"planner_cfg{cfg}.npz", allow_pickle=False)
+    run, layers, qs = W.loop_inputs(cfg)
     if W.input_digest(run, layers, qs) != str(d["digest"]):
-        return {"error": "the regenerated config-4 inputs differ from the fixture's"}
+        return {"error": f"the regenerated config-{cfg} inputs differ from the fixture's"}
     pol = Policy(calib=0.05, calib_kind="peak", calib_warm=(32, 8), calib_auto_ix=0.1)
-    carrier = UpdateCarrier()
-    fps = {l: FusedPlanner(pol, count=False, carrier=carrier) for l in layers}
-    kv = {l: (run.k[l].to(dev), run.v[l].to(dev)) for l in layers}
-    ids = run.ids.to(dev)
     n = same_read = same_trig = 0
     min_margin, differ = math.inf, []
-    for t in range(run.steps):
-        T = run.T0[0] + t + 1
-        nb = math.ceil(T / 64)
-        for i, l in enumerate(layers):
-            k, v = kv[l][0][:, :, :T], kv[l][1][:, :, :T]
-            q = qs[l][t].to(dev)
+
+    def compare(rec, t, read, trig):
+        nonlocal n, same_read, same_trig, min_margin, differ
+        rr = d["read"][rec, t]
+        ref_read = np.unpackbits(rr, axis=-1, count=rr.shape[-1] * 8)[..., :read.shape[-1]].astype(bool)
+        ref_trig, m = d["trig"][rec, t], d["margin"][rec, t]
+        n += trig.size
+        same_read += int((~(read != ref_read).any(-1)).sum())
+        same_trig += int((trig == ref_trig).sum())
+        fin = m[np.isfinite(m)]
+        if fin.size:
+            min_margin = min(min_margin, float(fin.min()))
+        differ += [float(m[h]) for h in np.nonzero(trig != ref_trig)[0]]
+
+    ids = run.ids.to(dev)
+    if cfg == 4:
+        carrier = UpdateCarrier()
+        fps = {l: FusedPlanner(pol, count=False, carrier=carrier) for l in layers}
+        kv = {l: (run.k[l].to(dev), run.v[l].to(dev)) for l in layers}
+        for t in range(run.steps):
+            T = run.T0[0] + t + 1
+            for i, l in enumerate(layers):
+                k, v = kv[l][0][:, :, :T], kv[l][1][:, :, :T]
+                q = qs[l][t].to(dev)
+                if t == 0:
+                    fps[l].first(q, k, v, run.scale)
+                    continue
+                fps[l].step(q, k, v, run.scale, ids=ids)
+                compare(i, t, fps[l].read_mask(math.ceil(T / 64)).cpu().numpy()[0],
+                        fps[l].state["trig"].bool().cpu().numpy()[0])
+        what = f"{len(layers)} layers"
+    else:
+        fp = FusedPlanner(pol, count=False)
+        k, v = run.k[0].to(dev), run.v[0].to(dev)
+        base = torch.tensor(run.T0, dtype=torch.int32)
+        for t in range(run.steps):
+            sl = (base + t + 1).to(dev)
+            q = qs[0][t].to(dev)
             if t == 0:
-                fps[l].first(q, k, v, run.scale)
+                fp.first(q, k, v, run.scale, seq_lens=sl)
                 continue
-            fps[l].step(q, k, v, run.scale, ids=ids)
-            read = fps[l].read_mask(nb).cpu().numpy()[0]
-            trig = fps[l].state["trig"].bool().cpu().numpy()[0]
-            rr = d["read"][i, t]
-            ref_read = np.unpackbits(rr, axis=-1, count=rr.shape[-1] * 8)[..., :nb].astype(bool)
-            ref_trig, m = d["trig"][i, t], d["margin"][i, t]
-            n += trig.size
-            same_read += int((~(read != ref_read).any(-1)).sum())
-            same_trig += int((trig == ref_trig).sum())
-            fin = m[np.isfinite(m)]
-            if fin.size:
-                min_margin = min(min_margin, float(fin.min()))
-            differ += [float(m[h]) for h in np.nonzero(trig != ref_trig)[0]]
-    out = {"fixture": "tests/golden/planner_cfg4.npz", "layers": len(layers), "steps": run.steps - 1,
+            fp.step(q, k, v, run.scale, ids=ids, seq_lens=sl)
+            bi, bc = fp.state["block_idx"].cpu().numpy(), fp.state["block_cnt"].cpu().numpy()
+            trig = fp.state["trig"].bool().cpu().numpy()
+            for b, T0 in enumerate(run.T0):
+                nb = math.ceil((T0 + t + 1) / 64)
+                read = np.zeros((bi.shape[1], nb), dtype=bool)
+                for h in range(bi.shape[1]):
+                    read[h, bi[b, h, :bc[b, h]]] = True
+                compare(b, t, read, trig[b])
+        what = f"{len(run.T0)} ragged sequences"
+    out = {"fixture": f"tests/golden/planner_cfg{cfg}.npz", "records": what, "steps": run.steps - 1,
            "head_steps": n, "read_sets_identical": same_read / n, "decisions_identical": same_trig / n,
            "min_oracle_decision_margin": min_margin, "differing_decision_margins": differ}
-    log(f"cfg4 vs oracle: read sets identical on {same_read}/{n} head-steps, decisions on {same_trig}/{n}; "
+    log(f"cfg{cfg} vs oracle: read sets identical on {same_read}/{n} head-steps, decisions on {same_trig}/{n}; "
         f"smallest oracle decision margin {min_margin:.2e}; differing decisions' margins {differ}")
     return out
 

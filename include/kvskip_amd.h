@@ -96,6 +96,10 @@ typedef struct kvskip_attn_args {
   const int32_t* block_table;
   int64_t bt_stride;
   int32_t num_pages;
+
+  /* Single-pass V-skip (not in the reference, which reports only vcount): optional
+   * [B, Hkv, ceil(T / 64)] uint8, 1 where the block's V was read (entered the softmax), else 0. */
+  uint8_t* v_keep;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block
@@ -224,7 +228,7 @@ typedef struct kvskip_plan_args {
   /* Read by the POST decision only (not in the reference): if not NULL, the attended log-sum-exp
    * comes from the split partials of the step's LISTS pass instead of lse_att: lse_part is that
    * pass's part_ml ([B, Hq, lse_stride, 2], max and sum in log2 units), slots [0, lse_slots)
-   * (lse_slots <= 128). */
+   * (lse_slots <= 64). */
   const float* lse_part;
   int32_t lse_slots, lse_stride;
 } kvskip_plan_args;

@@ -28,9 +28,10 @@ run inside the next layer's split pass (planner.UpdateCarrier; flush() before re
 
 from __future__ import annotations
 
+
 import collections
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import torch
 import torch.nn.functional as F
@@ -185,8 +186,12 @@ def _refresh_post(layer, q, k, v, scale):
     st = KVSKIP.state.setdefault(layer, {})
     pp = st.get("post")
     if pp is None:
-        pp = st["post"] = PostPlanner(KVSKIP.policy(layer), count=KVSKIP.count,
-                                      carrier=KVSKIP.carrier if KVSKIP.carry else None)
+        # the reference's refresh_step reads delta, max_age, local, level and the dense heads only
+        # (src/kvskip_attn.py:215-270): the calibration, warm-up and token-index fields of the
+        # config are ignored there, so they are dropped here too
+        pol = replace(KVSKIP.policy(layer), calib=None, calib_warm=(), calib_auto_ix=None,
+                                  index_heads=(), index_union=False)
+        pp = st["post"] = PostPlanner(pol, count=KVSKIP.count, carrier=KVSKIP.carrier if KVSKIP.carry else None)
         if KVSKIP.count:
             KVSKIP.log[layer] = pp.counters
         return pp.first(q, k, v, scale)

@@ -141,6 +141,7 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
               pv4[nt][0], NI > 1 ? pv4[nt][1] : 0.f, NI > 2 ? pv4[nt][2] : 0.f, NI > 3 ? pv4[nt][3] : 0.f);
       }
       const bool need = blk == 0 || blk >= nb - p.local || __ballot(vote) != 0;
+      if (p.v_keep != nullptr && lane == 0) p.v_keep[(static_cast<int64_t>(b) * p.Hkv + h) * nb + blk] = need ? 1 : 0;
       __builtin_amdgcn_sched_barrier(0);
       if (need) {
         ++loaded;
@@ -236,6 +237,7 @@ __global__ void __launch_bounds__(NT, 2) vskip1_kernel(const AttnP p) {
           for (int rg = 0; rg < 8; ++rg) sPw[(8 * rg + r8) * GP + g] = e[rg] * c;
         }
       }
+      if (p.v_keep != nullptr && lane == 0) p.v_keep[(static_cast<int64_t>(b) * p.Hkv + h) * nb + blk] = need ? 1 : 0;
       if (need) {
         ++loaded;
 #pragma unroll
@@ -422,6 +424,7 @@ __global__ void __launch_bounds__(NT, 2) pv_kernel(const AttnP p) {
 // result is kvskip_select then kvskip_pv's, bit for bit, without the selection's launch.
 template <int D, int G, int R>
 __global__ void __launch_bounds__(NT, R > 16 ? 1 : 2) pv_select_kernel(const AttnP p, const kvskip_select_args sel) {
+  static_assert(NWAVE == SW, "select_core indexes its LDS and slots by SW wavefronts: the pass's workgroup");
   __shared__ uint64_t sKeep[R];
   __shared__ float sLk[SEL_MAX_G];
   __shared__ int sPre[R + 1];                 // kept blocks before slot r

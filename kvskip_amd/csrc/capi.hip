@@ -104,6 +104,7 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->block_table = a->block_table;
   p->bt_stride = a->bt_stride;
   p->num_pages = a->num_pages;
+  p->v_keep = a->v_keep;
   return KVSKIP_OK;
 }
 
@@ -417,8 +418,8 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
       (pl->slot_count > 0 ? pl->slot_base + pl->slot_count : pl->slot_base + a->num_splits) > a->num_splits)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: slots [slot_base, slot_base + slot_count) within num_splits");
   if (pl->lse_part != nullptr &&
-      (pl->lse_slots < 1 || pl->lse_slots > 128 || pl->lse_stride < pl->lse_slots))
-    return fail(KVSKIP_E_INVALID, "decode_splits_planned: lse_slots in 1..128, lse_stride >= lse_slots");
+      (pl->lse_slots < 1 || pl->lse_slots > 64 || pl->lse_stride < pl->lse_slots))
+    return fail(KVSKIP_E_INVALID, "decode_splits_planned: lse_slots in 1..64, lse_stride >= lse_slots");
   if (pl->pass_budget < 0 || pl->pass_budget > 65536)
     return fail(KVSKIP_E_INVALID, "decode_splits_planned: pass_budget in 0..65536");
   if (pl->pass_budget > 0 && a->B * a->Hkv > 16)

@@ -42,6 +42,7 @@ struct AttnP {
   const int* block_table;  // [B, bt_stride] or null: paged K / V (page stride k_sb / v_sb)
   int64_t bt_stride;
   int num_pages;
+  uint8_t* v_keep;  // single-pass V-skip: [B, Hkv, nb] 1 where the block's V was read
 };
 
 constexpr int MAX_RAGGED_B = 256;  // batch bound of the ragged partition (one scan per 64)

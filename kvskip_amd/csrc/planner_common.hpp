@@ -81,6 +81,7 @@ __device__ __forceinline__ int plan_chunks(int T) { return ((T + BLK - 1) / BLK 
 // others still read the old one).
 constexpr int DLP = 8;
 constexpr int LSI = 8;   // partial slots per team lane of an attended log-sum-exp from partials (<= 64 slots)
+static_assert(LSI * DLP == 64, "kvskip_plan_args.lse_slots is validated against 64");
 
 template <int CTRL>
 __device__ __forceinline__ void lse_dpp(float& m, float& s) {

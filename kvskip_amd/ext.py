@@ -309,9 +309,11 @@ def pv(P, v, blk_scale, block_idx, block_cnt, num_splits=1, want_f32=False, bloc
 
 
 def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=False, lse_prev=None,
-           block_table=None, T=None):
+           block_table=None, T=None, v_keep=None):
     """Single-pass V-skip (kernels/kvskip_ext.cpp:149-195). Returns [out, lse, out_f32 or None, vcount or None].
-    block_table, T (not in the reference): a paged cache (see _kv_dims; the MFMA engine)."""
+    block_table, T (not in the reference): a paged cache (see _kv_dims; the MFMA engine).
+    v_keep (not in the reference): uint8 [B, Hkv, ceil(T / 64)] on the device, set to 1 where a block's V
+    was read, else 0."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -340,6 +342,10 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
         _require(lse_prev.is_cuda and lse_prev.dtype == torch.float32 and lse_prev.is_contiguous()
                  and lse_prev.numel() == B * Hq, "lse_prev: contiguous fp32 [B, Hq]")
         a.lse_prev = lse_prev.data_ptr()
+    if v_keep is not None:
+        _require(v_keep.is_cuda and v_keep.dtype == torch.uint8 and v_keep.is_contiguous()
+                 and tuple(v_keep.shape) == (B, Hkv, (T + TILE - 1) // TILE), "v_keep: contiguous uint8 [B, Hkv, nb]")
+        a.v_keep = v_keep.data_ptr()
     _set_pages(a, block_table, k)
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_vskip1(ctypes.byref(a), _stream(dev)))

@@ -161,6 +161,16 @@ def select_blocks(logw: torch.Tensor, G: int, rule: str, value: float, local: in
     head the fewest blocks holding >= value of its mass (ties at the cut kept) and unites the group;
     block 0 and the `local` newest always. Returns keep [B, Hkv, nb] bool."""
     B, Hq, nb = logw.shape
+    # the device selection's limits (the reference's torch rule also runs on CPU tensors and at any
+    # size; here the selection is a device kernel only, with no host fallback)
+    if not logw.is_cuda:
+        raise RuntimeError("select_blocks runs on the device: logw must be a CUDA tensor")
+    if G < 1 or Hq % G != 0 or G > 8:
+        raise RuntimeError(f"select_blocks: group size G in 1..8 dividing Hq (got G={G}, Hq={Hq})")
+    if nb > 4096:
+        raise RuntimeError(f"select_blocks: at most 4096 blocks (got {nb})")
+    if not value > 0:
+        raise RuntimeError(f"select_blocks: value > 0 (got {value})")
     keep = torch.empty(B, Hq // G, nb, dtype=torch.uint8, device=logw.device)
     lw = logw.float().contiguous()
     ext().select(lw, torch.ones_like(lw), Hq // G, rule, value, local, keep=keep)
@@ -222,20 +232,25 @@ def vskip_two_pass(q, k, v, scale: float, rule: str = "topp", value: float = 0.9
 
 def vskip_one_pass(q, k, v, scale: float, tau: float = 1e-4, local: int = 2, num_splits: int | None = None,
                    out_f32: bool = False, count: bool = False, lse_prev: torch.Tensor | None = None,
-                   sync: bool = True, block_table: torch.Tensor | None = None, T: int | None = None) -> dict:
+                   sync: bool = True, block_table: torch.Tensor | None = None, T: int | None = None,
+                   keep: bool = False) -> dict:
     """Single-pass V-skip (kernels/kvskip.py:182-208): K read once; a block's V is read only if some
     head of the group estimates its weight >= tau, against lse_prev (e.g. the previous step's "lse")
     or else the sink block's log-sum-exp, a lower bound of the normaliser. count=True adds v_tiles
     [B, Hkv] (V blocks read) and, with sync=True, kept_frac. block_table, T (not in the reference):
-    page pools."""
+    page pools. keep=True (not in the reference) adds v_keep: bool [B, Hkv, nb], the blocks whose V
+    was read."""
     q = _as_bhd(q)
     B, Hkv = q.shape[0], k.shape[1]
     nb = math.ceil((k.shape[2] if block_table is None else int(T)) / TILE)
     if num_splits is None:
         num_splits = num_splits_for(B * Hkv, nb)
+    vk = torch.empty(B, Hkv, nb, dtype=torch.uint8, device=q.device) if keep else None
     out, lse, o32, vt = ext().vskip1(q, k, v, float(scale), float(tau), int(local), int(num_splits), out_f32, count,
-                                     lse_prev, **_paged(block_table, T))
+                                     lse_prev, **_paged(block_table, T), v_keep=vk)
     res = {"out": out, "lse": lse, "num_splits": num_splits}
+    if keep:
+        res["v_keep"] = vk.bool()
     if out_f32:
         res["out_f32"] = o32
     if count:

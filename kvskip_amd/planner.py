@@ -30,6 +30,7 @@ TILE = 64
 MARGIN = 64                      # spare block capacity of the state (src/kvskip_attn.py:399)
 BALANCE_MAX_LISTS = 16           # (b, KV head) lists a balanced planned pass decides in every workgroup
 RAGGED_DECIDE_MAX_B = 16         # sequences of a ragged batch whose lists a planned pass decides per KV head
+POST_MAX_SLOTS = 64              # first-pass partial slots the refresh mode's decision reads (lse_slots)
 KINDS = {"logit": 0, "add": 1, "peak": 2}
 
 
@@ -495,10 +496,12 @@ class PostPlanner(FusedPlanner):
             E.block_sums(k, self.NBC, out=s["csum"])
         self.t += 1
         self.T = T
-        S = min(K.num_splits_for(B * Hkv, nb), 128)       # 2 S slots per head in all, <= 256
+        # 2 S slots per head in all; the refresh pass's decision merges the first pass's S slots into
+        # its attended log-sum-exp, at most POST_MAX_SLOTS of them
+        S = min(K.num_splits_for(B * Hkv, nb), POST_MAX_SLOTS)
         budget = 0
         if self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1:
-            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 128)
+            budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, POST_MAX_SLOTS)
         b = self._post_bufs(q, S)
         pargs = E.plan_struct(q, k, s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"],
                               s["flags"], s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], float(scale),

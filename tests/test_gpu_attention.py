@@ -138,25 +138,42 @@ def test_masked_cfg2(gpu):
     check_decode(L.q, L.k, L.v, L.scale, gq, gk, gv, label="cfg2 dense")
 
 
+def _selection_margin(q, k, scale, rule, value):
+    """How close the oracle's selection of this input comes to flipping: for top-p its cut's distance
+    from the level (topp_heads), for tau the smallest |weight - tau|."""
+    logw = O.block_logw(*O.block_stats(q, k, scale))
+    if rule == "topp":
+        return float(O.topp_heads(logw, value)[1].min())
+    return float((torch.softmax(logw, -1) - value).abs().min())
+
+
 def test_write_p_and_two_pass(gpu):
-    q, k, v = rand_qkv(1, 32, 8, 3000, 128, seed=8, sink_gap=True)
-    gq, gk, gv = to_gpu(q, k, v)
+    """Pass 1's fp16 P, and the two-pass V-skip: the device selection identical to the oracle's
+    select_blocks on the first seed whose oracle margin exceeds 1e-6 (a decision closer than that to its
+    threshold can flip under float32 sums), the output exact attention over the selected blocks."""
     scale = 128 ** -0.5
-    r = K.decode(gq, gk, gv, scale, stats=True, load_v=False, write_p=True)
-    P = O.p_values(q, k, scale)
-    err = (r["p"].cpu().double() - P).abs().max().item()
-    assert err <= 1e-3, err                                  # fp16 P
     for rule, val in (("topp", 0.99), ("tau", 1e-4)):
+        for seed in range(8, 40):
+            q, k, v = rand_qkv(1, 32, 8, 3000, 128, seed=seed, sink_gap=True)
+            margin = _selection_margin(q, k, scale, rule, val)
+            if margin > 1e-6:
+                break
+        assert margin > 1e-6, f"every seed tried has a near tie ({margin:.2e})"
+        gq, gk, gv = to_gpu(q, k, v)
+        if rule == "topp":
+            r = K.decode(gq, gk, gv, scale, stats=True, load_v=False, write_p=True)
+            P = O.p_values(q, k, scale)
+            err = (r["p"].cpu().double() - P).abs().max().item()
+            assert err <= 1e-3, err                                  # fp16 P
         r2 = K.vskip_two_pass(gq, gk, gv, scale, rule=rule, value=val, out_f32=True)
         _, keep = O.vskip_two_pass(q, k, v, scale, rule=rule, value=val)
         keep_dev = r2["keep"].cpu()
-        mism = (keep_dev != keep).float().mean().item()
-        ref_out, _ = O.decode(q, k, v, scale, keep=keep_dev)   # kernels judged on the set they were given
+        ref_out, _ = O.decode(q, k, v, scale, keep=keep_dev)
         e16 = O.rel_err(r2["out"].cpu(), ref_out)
         e32 = O.rel_err(r2["out_f32"].cpu(), ref_out)
-        print(f"vskip2 {rule}: kept {keep.float().mean():.3f} (selection mismatch {mism:.4f}) "
+        print(f"vskip2 {rule} seed {seed}: kept {keep.float().mean():.3f}, oracle margin {margin:.2e}, "
               f"bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
-        assert mism <= 0.01
+        assert torch.equal(keep_dev, keep), (rule, int((keep_dev != keep).sum()))
         assert e16 <= BF16_TOL and e32 <= 5e-4          # fp16 P bounds the fp32 output error
 
 
@@ -196,6 +213,15 @@ def test_pv_split_counts_and_list_edges(gpu, S):
         assert O.rel_err(out.cpu(), ref) <= BF16_TOL, (D, G, S)
 
 
+def _same_kept_set(r, keep, z):
+    """The blocks whose V single-pass V-skip read (v_keep) are the oracle rule's, except a block whose
+    decision margin |z| (log units) is below float32 noise (1e-4); vcount is their count."""
+    got = r["v_keep"].cpu()
+    border = (z.abs() < 1e-4) & ~O.always_keep(keep.shape[-1], 2)
+    assert not bool(((got != keep) & ~border).any()), int(((got != keep) & ~border).sum())
+    assert torch.equal(r["v_tiles"].cpu().to(torch.int64), got.sum(-1).to(torch.int64))
+
+
 @pytest.mark.parametrize("tau", [1e-4, 1e-3])
 def test_vskip1_sink_and_lse_prev(gpu, tau):
     """bench/test_decode.py:131-151: kept set equals the fp64 rule's (except decisions within
@@ -206,14 +232,11 @@ def test_vskip1_sink_and_lse_prev(gpu, tau):
     scale = 128 ** -0.5
     lse_exact = torch.logsumexp(O.scores(q, k, scale), -1)
     for lp in (None, lse_exact.float()):
-        r = K.vskip_one_pass(gq, gk, gv, scale, tau=tau, out_f32=True, count=True,
+        r = K.vskip_one_pass(gq, gk, gv, scale, tau=tau, out_f32=True, count=True, keep=True,
                              lse_prev=None if lp is None else lp.cuda().contiguous())
         keep, z = O.vskip1_keep(q, k, scale, tau, 2, lse_prev=lp)
-        vcount_ref = keep.sum(-1)
-        borderline = ((z.abs() < 1e-4) & ~O.always_keep(keep.shape[-1], 2)).sum(-1)
-        diff = (r["v_tiles"].cpu() - vcount_ref).abs()
-        assert (diff <= borderline).all(), (r["v_tiles"], vcount_ref)
-        ref, lse = O.decode(q, k, v, scale, keep=keep)
+        _same_kept_set(r, keep, z)
+        ref, lse = O.decode(q, k, v, scale, keep=r["v_keep"].cpu())
         e16 = O.rel_err(r["out"].cpu(), ref)
         e32 = O.rel_err(r["out_f32"].cpu(), ref)
         print(f"vskip1 tau {tau:g} lse_prev={lp is not None}: kept {keep.float().mean():.3f} "
@@ -228,11 +251,10 @@ def test_vskip1_cfg3(gpu):
     lse_exact = torch.logsumexp(O.scores(L.q, L.k, L.scale), -1)
     lp = W.perturbed_lse(lse_exact, seed=33)
     gq, gk, gv = to_gpu(L.q, L.k, L.v)
-    r = K.vskip_one_pass(gq, gk, gv, L.scale, tau=1e-4, out_f32=True, count=True, lse_prev=lp.cuda())
+    r = K.vskip_one_pass(gq, gk, gv, L.scale, tau=1e-4, out_f32=True, count=True, keep=True, lse_prev=lp.cuda())
     keep, z = O.vskip1_keep(L.q, L.k, L.scale, 1e-4, 2, lse_prev=lp)
-    borderline = ((z.abs() < 1e-4) & ~O.always_keep(keep.shape[-1], 2)).sum(-1)
-    assert ((r["v_tiles"].cpu() - keep.sum(-1)).abs() <= borderline).all()
-    ref, _ = O.decode(L.q, L.k, L.v, L.scale, keep=keep)
+    _same_kept_set(r, keep, z)
+    ref, _ = O.decode(L.q, L.k, L.v, L.scale, keep=r["v_keep"].cpu())
     e16, e32 = O.rel_err(r["out"].cpu(), ref), O.rel_err(r["out_f32"].cpu(), ref)
     print(f"cfg3 vskip1: V kept {keep.float().mean():.3f} bf16 {e16:.2e} f32 {e32:.2e}", flush=True)
     assert e16 <= BF16_TOL and e32 <= F32_TOL

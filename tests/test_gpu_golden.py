@@ -49,8 +49,9 @@ def test_attention_golden(gpu):
     assert np.array_equal(keep, d["topp_keep"]), f"top-p sets differ (oracle margins {margin.min():.2e} and up)"
     # single-pass V-skip: V blocks read per (b, KV head)
     lp = torch.from_numpy(d["lse_prev"]).float().cuda()
-    res = K.vskip_one_pass(q, k, v, scale, tau=0.02, local=1, count=True, lse_prev=lp, num_splits=2)
+    res = K.vskip_one_pass(q, k, v, scale, tau=0.02, local=1, count=True, lse_prev=lp, num_splits=2, keep=True)
     assert np.abs(d["vskip_margin"]).min() > 1e-3
+    assert np.array_equal(res["v_keep"].cpu().numpy(), d["vskip_keep"])
     assert np.array_equal(res["v_tiles"].cpu().numpy(), d["vskip_keep"].sum(-1))
 
 

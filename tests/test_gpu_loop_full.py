@@ -19,12 +19,13 @@ within 1e-6 of the level on a few percent of refreshes here (the mass past the f
 spread over hundreds of tiny blocks), below the float32 noise of the device's sums. So each KV head
 is tracked as in sync (device state = oracle state) or not. While in sync every decision must be
 identical, and a difference is allowed only where the oracle's own margin for that decision is
-below NEAR (1e-5: |estimate - delta| for a refresh, the cut's distance from the level for a stored
+below NEAR (2e-6: |estimate - delta| for a refresh, the cut's distance from the level for a stored
 set, |correction - threshold| for a latch); anything else fails. The head then leaves sync and
 rejoins at the next step where both refresh it and its stored set, latch and correction agree
 again (a refresh replaces the rest of its state). Printed: agreement of read sets over all
-head-steps (the reference's criterion, >= 0.97, bench/test_planner.py:133), the in-sync share,
-every near-tie event with its margin, and the smallest margins compared in sync. Outputs, estimates
+head-steps (>= 0.995; the reference's criterion is >= 0.97, bench/test_planner.py:133), the in-sync
+share (>= 0.995), every near-tie event with its margin (at most MAX_NEAR per config), and the
+smallest margins compared in sync. Outputs, estimates
 and continuous state are checked on in-sync heads."""
 
 import importlib.util
@@ -42,9 +43,10 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 REL = 2e-3
-NEAR = 1e-5
-MIN_AGREE = 0.97       # bench/test_planner.py:133
-MIN_SYNC = 0.95
+NEAR = 2e-6            # an oracle margin below this is a float32 near tie (measured departures: 2.7e-7, 3.2e-7)
+MIN_AGREE = 0.995      # the reference's own criterion is 0.97 (bench/test_planner.py:133); measured >= 0.9985
+MIN_SYNC = 0.995       # measured >= 0.9983
+MAX_NEAR = 2           # near-tie departures allowed per config (measured: 1 each)
 AIX_THR = 0.1          # the stage-4 policy's latch threshold
 
 
@@ -160,7 +162,7 @@ def _summary(chks, what):
     n_near = sum(len(c.near) for c in chks)
     print(f"{what}: read sets identical on {agree:.4f} of head-steps, in sync {sync:.4f}, {n_near} near-tie "
           f"departures (all with oracle margin < {NEAR:g})", flush=True)
-    assert agree >= MIN_AGREE and sync >= MIN_SYNC, (agree, sync)
+    assert agree >= MIN_AGREE and sync >= MIN_SYNC and n_near <= MAX_NEAR, (agree, sync, n_near)
 
 
 def _state(fp):

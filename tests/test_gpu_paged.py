@@ -229,20 +229,21 @@ def test_paged_vskip_one_pass_matches_contiguous(G, D, T):
     for S in (1, 8):
         # random scores give blocks of nearly equal weight: tau just above the mean weight skips some
         for lp, tau in ((None, 1.2), (lse_prev, 1.2 / nb)):
-            ref = K.vskip_one_pass(q, k, v, D ** -0.5, tau=tau, num_splits=S, count=True, lse_prev=lp)
+            ref = K.vskip_one_pass(q, k, v, D ** -0.5, tau=tau, num_splits=S, count=True, lse_prev=lp, keep=True)
             got = K.vskip_one_pass(q, kp, vp, D ** -0.5, tau=tau, num_splits=S, count=True, lse_prev=lp,
-                                   block_table=table, T=T)
-            for key in ("out", "lse", "v_tiles"):
+                                   block_table=table, T=T, keep=True)
+            for key in ("out", "lse", "v_tiles", "v_keep"):
                 _same(got[key], ref[key], (key, S, lp is None))
             assert ref["v_tiles"].sum().item() < 2 * Hkv * nb, (S, lp is None)      # some V blocks skipped
     kg, vg = _gathered(kp, vp, table, [T, T])
     for lp, tau in ((None, 1.2), (lse_prev, 1.2 / nb)):
         got = K.vskip_one_pass(q, kp, vp, D ** -0.5, tau=tau, num_splits=8, count=True, lse_prev=lp,
-                               block_table=table, T=T)
+                               block_table=table, T=T, keep=True)
         lpd = None if lp is None else lp.cpu().double()
         o_ref, _, keep, cnt = O.vskip1(q.cpu(), kg, vg, D ** -0.5, tau, 2, lse_prev=lpd)
         _, z = O.vskip1_keep(q.cpu(), kg, D ** -0.5, tau, 2, lse_prev=lpd)
         assert float(z.abs().min()) > 1e-5                                  # no vote at float32 noise
+        assert torch.equal(got["v_keep"].cpu(), keep), ("paged one-pass votes vs oracle", lp is None)
         assert torch.equal(got["v_tiles"].cpu(), cnt), ("paged one-pass votes vs oracle", lp is None)
         rel_ok(got["out"], o_ref, ("paged one-pass vs oracle", lp is None))
 

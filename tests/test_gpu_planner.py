@@ -238,15 +238,16 @@ def test_planner_loop_gqa7_batch(gpu):
 
 @pytest.mark.parametrize("pol", [OP.Policy(), OP.Policy(delta=0.02, max_age=8, dense_heads=(3,))],
                          ids=["default", "age8_forced"])
-@pytest.mark.parametrize("B,G,Hkv", [(1, 4, 8), (2, 7, 4)])
-def test_post_planner_loop(gpu, pol, B, G, Hkv):
+@pytest.mark.parametrize("B,G,Hkv,T0", [(1, 4, 8, 4096), (2, 7, 4, 4096), (1, 4, 4, 33000)])
+def test_post_planner_loop(gpu, pol, B, G, Hkv, T0):
     """The refresh mode's device loop (PostPlanner: scores, attended lists, masked pass, decision
     against that pass's lse, refresh pass, update) against the oracle's post_step, free-running for
     30 steps with query drift and jumps: refresh decisions identical on every head-step (failures
     name the oracle's margin), the refresh pass's lists the blocks outside a refreshing head's
     attended set and none of the others, stored sets identical after every step, estimates within
-    1e-4, outputs within 2e-3."""
-    T0, steps = 4096, 30
+    1e-4, outputs within 2e-3. Four KV heads at T 33k: the split count (doubled by the balanced
+    partition) is capped at the 64 first-pass partial slots the refresh pass's decision merges."""
+    steps = 30
     run = W.planner_run(layers=1, B=B, Hq=G * Hkv, Hkv=Hkv, D=128, T0=T0, steps=steps, seed=6)
     qp = W.QueryProcess(run, 0, p_jump=0.05)
     k_cpu, v_cpu = run.k[0], run.v[0]

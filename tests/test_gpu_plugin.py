@@ -8,6 +8,7 @@ identical on every head-step, outputs within 2e-3), replay against exact attenti
 recorded lists. Besides, each mode gives what its kernels give when called directly (the same
 launches: bit for bit), and the refresh loop with carried updates the same lists as without."""
 
+from dataclasses import replace
 from types import SimpleNamespace
 
 import pytest
@@ -169,12 +170,15 @@ def test_refresh_mode_matches_oracle():
     identical on every head-step, the refresh pass's lists the blocks outside a refreshing head's
     attended set and none of the others' blocks, stored sets identical after each step, outputs within
     2e-3; the device counters add up the blocks of both passes (src/kvskip_attn.py:256,269), each
-    block once. Then the same with the updates
-    carried by the next layer's pass: the same triggers, outputs and final state."""
+    block once. The config also sets calibration, warm-up and token-index fields, which the reference's
+    refresh_step does not read (src/kvskip_attn.py:215-270): the mode runs as without them. Then the
+    same with the updates carried by the next layer's pass: the same triggers, outputs and final state."""
     ks, vs, qs, _ = _data(35)
-    kw = dict(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),))
+    kw = dict(mode="refresh", count=True, delta=0.02, max_age=4, dense_heads=((2, 1),), calib=0.05,
+              calib_kind="peak", calib_warm=(8, 2), calib_auto_ix=0.1)
     cfg = A.KvskipConfig(carry=False, **kw)
-    orc = {l: LayerOracle(oracle_policy(cfg.policy(l)), SCALE, post=True) for l in range(1, LAYERS)}
+    ignored = dict(calib=None, calib_warm=(), calib_auto_ix=None, index_heads=(), index_union=False)
+    orc = {l: LayerOracle(oracle_policy(replace(cfg.policy(l), **ignored)), SCALE, post=True) for l in range(1, LAYERS)}
     prev_keep, orc_trig = {}, {}
     seen = dict(refresh=0, kept=0, read=0)
 

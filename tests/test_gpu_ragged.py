@@ -132,7 +132,8 @@ def test_ragged_rejects(gpu):
 def test_planner_loop_ragged(gpu):
     """Config 5 in small: a ragged batch (3 sequences, 28 / 4 heads, G 7) through the fused planner
     loop for 24 steps, each sequence against its own oracle planner (refresh_pre_step semantics):
-    identical read sets on every head-step (borderline margins excepted), outputs within 2e-3."""
+    identical read sets and stored sets on every head-step in sync (a near tie in the oracle, margin
+    < 2e-6, takes a head out of sync until a common refresh), outputs within 2e-3."""
     from kvskip_amd import workloads as W
     from kvskip_amd.planner import FusedPlanner, Policy as DPolicy
     from oracle import planner as OP
@@ -147,7 +148,15 @@ def test_planner_loop_ragged(gpu):
     ids = run.ids.cuda()
     fp = FusedPlanner(DPolicy(**pol.__dict__))
     states = [None] * 3
-    same = total = border = 0
+    # Each (sequence, KV head) is tracked in sync (device state = oracle state) or not, as in the
+    # full-size loops (tests/test_gpu_loop_full.py): while in sync every read set and stored set must be
+    # identical, a difference is allowed only where the oracle's own margin is below NEAR (a float32
+    # near tie), and the head is then compared no more until both refresh it and its stored set,
+    # latch and correction agree again.
+    NEAR = 2e-6
+    off = [set() for _ in lens0]
+    same = total = in_sync = 0
+    departures, rejoined = [], []
     for t in range(steps):
         lens = [T0 + t + 1 for T0 in lens0]
         sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
@@ -157,6 +166,10 @@ def test_planner_loop_ragged(gpu):
         else:
             out_d = fp.step(q.cuda(), k, v, run.scale, ids=ids, seq_lens=sl)
         read_d = fp.read_mask(math.ceil(k.shape[2] / 64)).cpu()
+        trig_d = fp.state["trig"].bool().cpu()
+        keep_d = fp.state["keep"].bool().cpu()
+        calib_d = fp.state["calib"].double().cpu()
+        aix_d = fp.state["aix"].bool().cpu()
         for b, T in enumerate(lens):
             qb, kb, vb = q[b:b + 1], run.k[0][b:b + 1, :, :T], run.v[0][b:b + 1, :, :T]
             nbb = math.ceil(T / 64)
@@ -164,22 +177,43 @@ def test_planner_loop_ragged(gpu):
                 states[b], out_r = OP.init(qb, kb, vb, run.scale, pol)
                 read_r = torch.ones(1, Hkv, nbb, dtype=torch.bool)
                 margin = torch.full((1, Hkv), math.inf, dtype=torch.float64)
+                trig_r = torch.ones(Hkv, dtype=torch.bool)
             else:
                 idx_b = torch.from_numpy(OP.index_blocks(run.ids[b:b + 1].numpy(), T))
                 out_r, pr = OP.step(states[b], qb, kb, vb, pol, idx=idx_b)
-                read_r, margin = pr["read"], pr["margin"]
+                read_r, margin, trig_r = pr["read"], pr["margin"], pr["trig"][0]
             rd = read_d[b:b + 1, :, :nbb]
             assert not read_d[b, :, nbb:].any(), "a block past the sequence's end was listed"
-            diff = (rd != read_r).any(-1)
-            bad = diff & (margin < 1e-5)
-            border += int(bad.sum())
-            assert not bool((diff & (margin >= 1e-5)).any()), f"read set differs at step {t}, sequence {b}"
+            diff = (rd != read_r).any(-1)[0]
+            keep_r = states[b].keep[0, :, :nbb]
+            for h in range(Hkv):
+                if h in off[b]:
+                    if (trig_d[b, h] and trig_r[h] and torch.equal(keep_d[b, h, :nbb], keep_r[h])
+                            and bool(aix_d[b, h] == states[b].aix[0, h])
+                            and abs(float(calib_d[b, h] - states[b].calib[0, h])) <= 1e-4):
+                        off[b].discard(h)
+                        rejoined.append((t, b, h))
+                    continue
+                if diff[h]:
+                    m = float(margin[0, h])
+                    assert m < NEAR, f"read set differs at step {t}, sequence {b}, KV head {h} (oracle margin {m:.2e})"
+                elif not torch.equal(keep_d[b, h, :nbb], keep_r[h]):
+                    m = float(states[b].topp_heads[0, h * G:(h + 1) * G].min())
+                    assert m < NEAR, f"stored set differs at step {t}, sequence {b}, KV head {h} (top-p margin {m:.2e})"
+                else:
+                    continue
+                departures.append((t, b, h, m))
+                off[b].add(h)
+            on = torch.tensor([h not in off[b] for h in range(Hkv)])
             same += int((~diff).sum())
-            total += diff.numel()
-            hq = (~diff).repeat_interleave(G, 1)[0]
+            total += Hkv
+            in_sync += int(on.sum())
+            hq = on.repeat_interleave(G)
             if bool(hq.any()):
                 err = O.rel_err(out_d[b][hq].float().cpu()[None], out_r[0][hq][None])
                 assert err <= REL, (t, b, err)
-            assert (fp.state["calib"][b].double().cpu() - states[b].calib[0]).abs().max().item() <= 1e-4
-            assert torch.equal(fp.state["aix"][b].bool().cpu(), states[b].aix[0])
-    print(f"ragged planner loop: identical read sets on {same}/{total} head-steps, borderline {border}", flush=True)
+                assert (calib_d[b][on] - states[b].calib[0][on]).abs().max().item() <= 1e-4
+                assert torch.equal(aix_d[b][on], states[b].aix[0][on])
+    print(f"ragged planner loop: identical read sets on {same}/{total} head-steps, in sync {in_sync}/{total}, "
+          f"near-tie departures {departures}, rejoined {rejoined}", flush=True)
+    assert in_sync >= 0.995 * total and len(departures) <= 2, (in_sync, total, departures)
