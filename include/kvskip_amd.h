@@ -100,6 +100,13 @@ typedef struct kvskip_attn_args {
   /* Single-pass V-skip (not in the reference, which reports only vcount): optional
    * [B, Hkv, ceil(T / 64)] uint8, 1 where the block's V was read (entered the softmax), else 0. */
   uint8_t* v_keep;
+
+  /* Partition of a masked ragged pass (not in the reference; block_idx with seq_lens): 0 cuts each
+   * KV head's lists over the batch (chunks of ceil(sum_b cnt / num_splits) entries per head); 1
+   * cuts all B * Hkv lists by one length C = max(ceil(sum / (num_splits * Hkv)), ceil(max cnt /
+   * num_splits)), so a KV head whose lists hold more entries gets more workgroups (needs
+   * B * Hkv <= 512). The merge (kvskip_merge_splits) must be given the value its pass had. */
+  int32_t list_partition;
 } kvskip_attn_args;
 
 /* Split-K decode attention: dense (block_idx NULL) or over block lists, with optional per-block

@@ -30,7 +30,7 @@ class AttnArgs(ctypes.Structure):
         ("p_out", c_void_p), ("p_in", c_void_p), ("blk_scale", c_void_p),
         ("tau", c_float), ("local", c_int32), ("vcount", c_void_p), ("lse_prev", c_void_p),
         ("seq_lens", c_void_p), ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32),
-        ("v_keep", c_void_p),
+        ("v_keep", c_void_p), ("list_partition", c_int32),
     ]
 
 

@@ -154,6 +154,63 @@ __device__ __forceinline__ int ragged_chunks(const AttnP& p, int b, int h, bool 
   return (ragged_items(p, b, h, masked) + C - 1) / C;
 }
 
+// Partition over all B * Hkv lists of a masked ragged pass (p.list_partition = 1): chunks of one
+// length C = max(ceil(sum / (S Hkv)), ceil(most / S)) list entries (S = num_splits: the partial
+// slots of a list), numbered list by list (l = b Hkv + h), so a KV head whose lists hold more
+// entries (a refreshing sequence) gets more workgroups instead of longer chunks; the grid's
+// (S + B) Hkv slots hold every chunk (sum / C <= S Hkv, plus one partial chunk per list). Lane j
+// holds lists j + 64 r in nv. Returns C, uniform.
+constexpr int NRG = MAX_GLOBAL_LISTS / WAVE;
+
+__device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) {
+  const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
+  int tot = 0, most = 0;
+#pragma unroll
+  for (int r = 0; r < NRG; ++r) {
+    const int l = r * WAVE + lane;
+    nv[r] = l < nl ? min(max(p.block_cnt[l], 0), p.max_blocks) : 0;
+    tot += nv[r];
+    most = max(most, nv[r]);
+  }
+  tot = wave_sum_int(tot);
+  most = static_cast<int>(wave_max(static_cast<float>(most)));  // exact: counts <= 2^24
+  const int S = p.num_splits;
+  return __builtin_amdgcn_readfirstlane(max(1, max((tot + S * p.Hkv - 1) / (S * p.Hkv), (most + S - 1) / S)));
+}
+
+// Chunk number `it` of the partition over all lists: its list (b, h; b = -1 past the last chunk),
+// the chunk within the list and the list's entry count. Returns C. Uniform results.
+__device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk, int& items) {
+  const int lane = threadIdx.x % WAVE;
+  int nv[NRG];
+  const int C = global_chunk_len(p, nv);
+  int l_sel = -1;
+  chunk = 0;
+  items = 0;
+  int base = 0;
+#pragma unroll
+  for (int r = 0; r < NRG; ++r) {
+    if (r * WAVE >= p.B * p.Hkv) break;
+    const int ch = (nv[r] + C - 1) / C;
+    const int incl = wave_incl_scan(ch);
+    const int excl = base + incl - ch;
+    const uint64_t hit = __ballot(ch > 0 && it >= excl && it < excl + ch);
+    if (hit != 0) {
+      const int j = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+      l_sel = r * WAVE + j;
+      chunk = it - __shfl(excl, j, WAVE);
+      items = __shfl(nv[r], j, WAVE);
+    }
+    base += __shfl(incl, WAVE - 1, WAVE);
+  }
+  l_sel = __builtin_amdgcn_readfirstlane(l_sel);
+  b = l_sel >= 0 ? l_sel / p.Hkv : -1;
+  h = l_sel >= 0 ? l_sel % p.Hkv : 0;
+  chunk = __builtin_amdgcn_readfirstlane(chunk);
+  items = __builtin_amdgcn_readfirstlane(items);
+  return C;
+}
+
 // Byte range of one (b, head) of a K or V view: rows 0..T-1 of D bf16 each, row stride st.
 __device__ __forceinline__ uint32_t head_bytes(int T, int64_t st, int D) {
   return static_cast<uint32_t>((static_cast<int64_t>(T - 1) * st + D) * 2);
@@ -548,8 +605,13 @@ __device__ __forceinline__ void merge_body(const AttnP& p, int plain, int64_t hq
 // nothing attended, out 0 and lse -inf). Uniform over the workgroup.
 __device__ __forceinline__ int merge_count(const AttnP& p, int64_t hq) {
   if (p.seq_lens == nullptr) return p.num_splits;
-  return ragged_chunks(p, static_cast<int>(hq / p.Hq), static_cast<int>(hq % p.Hq) / (p.Hq / p.Hkv),
-                       p.block_idx != nullptr);
+  const int b = static_cast<int>(hq / p.Hq), h = static_cast<int>(hq % p.Hq) / (p.Hq / p.Hkv);
+  if (p.block_idx != nullptr && p.list_partition != 0) {
+    int nv[NRG];
+    const int C = global_chunk_len(p, nv);
+    return (ragged_items(p, b, h, true) + C - 1) / C;
+  }
+  return ragged_chunks(p, b, h, p.block_idx != nullptr);
 }
 
 // merge_body with the fewest slots that hold Sv partials (U halved while 4 U still does): a ragged

@@ -378,21 +378,29 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
     const int per = (n_items + p.num_splits - 1) / p.num_splits;
     i0 = min(n_items, split * per);
     n = min(n_items, i0 + per) - i0;
-  } else {  // ragged: chunks of C items over the whole batch, per KV head
+  } else {  // ragged: chunks of C items over the whole batch, per KV head or over all lists
     const int W = p.num_splits + p.B;
     const int it = xcd_remap(bid, W * p.Hkv);
-    h = it / W;
-    int chunk;
-    const int C = ragged_lookup(p, h, it % W, MASKED, b, chunk, n_items);
+    const bool global = MASKED && p.list_partition != 0;
+    int chunk, C;
+    if (global) {
+      C = global_lookup(p, it, b, h, chunk, n_items);
+    } else {
+      h = it / W;
+      C = ragged_lookup(p, h, it % W, MASKED, b, chunk, n_items);
+    }
     if constexpr (MASKED && STATS) {
-      if (it % W == 0) {  // (b', h) with an empty list have no chunk: their statistics are written here
+      // (b', eh) with an empty list have no chunk: their statistics are written by one workgroup
+      // per KV head eh (the head's first chunk slot; over all lists, workgroup eh)
+      const int eh = global ? (it < p.Hkv ? it : -1) : (it % W == 0 ? h : -1);
+      if (eh >= 0) {
         for (int b0 = wave * WAVE; b0 < p.B; b0 += NT) {
           const int bb = b0 + lane;
-          uint64_t empty = __ballot(bb < p.B && ragged_items(p, bb, h, true) == 0);
+          uint64_t empty = __ballot(bb < p.B && ragged_items(p, bb, eh, true) == 0);
           while (empty != 0) {
             const int be = b0 + __ffsll(static_cast<unsigned long long>(empty)) - 1;
             empty &= empty - 1;
-            const int64_t q0 = static_cast<int64_t>(be) * p.Hq + static_cast<int64_t>(h) * G;
+            const int64_t q0 = static_cast<int64_t>(be) * p.Hq + static_cast<int64_t>(eh) * G;
             for (int t = lane; t < G * p.nb; t += WAVE) {
               p.blk_max[(q0 + t / p.nb) * p.nb + t % p.nb] = NEG_INF;
               p.blk_sum[(q0 + t / p.nb) * p.nb + t % p.nb] = 0.f;

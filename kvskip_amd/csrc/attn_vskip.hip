@@ -459,25 +459,26 @@ __global__ void __launch_bounds__(NT, R > 16 ? 1 : 2) pv_select_kernel(const Att
                        [&](int blk, int g) { return __expf(sel.blk_max[(hq0 + g) * nb + blk] - sLk[g]); });
 }
 
-// Streaming read: workgroup i reads the i-th contiguous chunk of n 16-byte words, each thread
-// keeping 8 loads in flight, XOR-folded so the loads stay live.
-__global__ void __launch_bounds__(256) read_kernel(const u32x4* __restrict__ x, int64_t n, uint32_t* out) {
-  constexpr int U = 8;
-  const int64_t chunk = ((n + gridDim.x - 1) / gridDim.x + 256 * U - 1) / (256 * U) * (256 * U);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * chunk;
-  const int64_t end = min(n, base + chunk);
+// Streaming read of n 16-byte words in rows of 256 threads x RU words: workgroup i reads rows
+// i, i + grid, ... (neighbouring workgroups on neighbouring rows), each lane 4 non-temporal buffer
+// loads in flight, XOR-folded so the loads stay live. A row's buffer resource ends at the data, so
+// the last row's loads past it return zeros without a memory access. A sweep of loads in flight
+// per lane (4 / 8 / 16), 256 / 512 / 1024 threads, 256 to 4096 workgroups, contiguous chunks per
+// workgroup vs interleaved rows and global vs buffer loads put this form within 3% of the best at
+// 134 MB, 256 MiB and 2 GiB alike.
+constexpr int READ_NT = 256, READ_U = 4;
+
+__global__ void __launch_bounds__(READ_NT) read_kernel(const u32x4* __restrict__ x, int64_t n, uint32_t* out) {
+  constexpr int64_t ROW = READ_NT * READ_U;
   uint32_t a = 0;
-  int64_t i = base + threadIdx.x;
-  for (; i + (U - 1) * 256 < end; i += U * 256) {
-    u32x4 v[U];
+  const uint32_t voff = 16u * threadIdx.x;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * ROW; r0 < n; r0 += static_cast<int64_t>(gridDim.x) * ROW) {
+    const rsrc_t rr = make_rsrc(x + r0, static_cast<uint32_t>(16 * min(ROW, n - r0)));
+    u32x4 v[READ_U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = ld16_nt(x + i + u * 256);
+    for (int u = 0; u < READ_U; ++u) v[u] = bload16<BUF_NT>(rr, voff + 16u * READ_NT * u, 0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) a ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  for (; i < end; i += 256) {
-    const u32x4 v = ld16_nt(x + i);
-    a ^= v.x ^ v.y ^ v.z ^ v.w;
+    for (int u = 0; u < READ_U; ++u) a ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
   if (a == 0x9e3779b9u) out[0] = a;
 }
@@ -557,7 +558,7 @@ hipError_t launch_pv_select(const AttnP& p, const kvskip_select_args& sel, int D
 }
 
 hipError_t launch_read(const void* x, int64_t bytes, uint32_t* out, int blocks, hipStream_t s) {
-  hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const u32x4*>(x), bytes / 16,
+  hipLaunchKernelGGL(read_kernel, dim3(blocks), dim3(READ_NT), 0, s, reinterpret_cast<const u32x4*>(x), bytes / 16,
                      out);
   return hipGetLastError();
 }

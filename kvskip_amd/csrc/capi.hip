@@ -105,6 +105,7 @@ int prepare_attn(const kvskip_attn_args* a, bool need_q, bool need_k, bool need_
   p->bt_stride = a->bt_stride;
   p->num_pages = a->num_pages;
   p->v_keep = a->v_keep;
+  p->list_partition = a->list_partition;
   return KVSKIP_OK;
 }
 
@@ -168,6 +169,13 @@ static int check_decode(const kvskip_attn_args* a, int stats, int load_v, int ph
     if (a->num_splits < 2) return fail(KVSKIP_E_INVALID, "seq_lens needs num_splits >= 2");
     if (a->B > kvs::MAX_RAGGED_B) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: B <= %d", kvs::MAX_RAGGED_B);
     if (a->p_out != nullptr) return fail(KVSKIP_E_UNSUPPORTED, "seq_lens: no fp16 P output");
+  }
+  if (a->list_partition != 0) {
+    if (a->list_partition != 1) return fail(KVSKIP_E_INVALID, "list_partition in {0, 1}");
+    if (!masked || a->seq_lens == nullptr)
+      return fail(KVSKIP_E_INVALID, "list_partition 1 partitions a masked ragged pass (block_idx and seq_lens)");
+    if (a->B * a->Hkv > kvs::MAX_GLOBAL_LISTS)
+      return fail(KVSKIP_E_UNSUPPORTED, "list_partition 1: B * Hkv <= %d", kvs::MAX_GLOBAL_LISTS);
   }
   if (a->block_table != nullptr && (phase & 1)) {  // paged cache (the merge alone reads no K / V)
     const int rc = check_paged(a, p->nb, masked ? a->max_blocks : p->nb);
@@ -405,6 +413,9 @@ int kvskip_decode_splits_planned(const kvskip_attn_args* a, const kvskip_plan_ar
                                         "and decide separately for more)", a->B);
     if (a->block_table != nullptr)
       return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch reads a contiguous cache");
+    if (a->list_partition != 0)
+      return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch's lists are decided per KV head "
+                                        "(list_partition 0)");
     if (pl->pass_budget != 0 || pl->slot_base != 0 || pl->slot_count != 0 || pl->lse_part != nullptr ||
         pl->decide_mode == KVSKIP_DECIDE_POST)
       return fail(KVSKIP_E_UNSUPPORTED, "decode_splits_planned: a ragged batch takes no pass_budget, slots, lse_part "

@@ -43,9 +43,11 @@ struct AttnP {
   int64_t bt_stride;
   int num_pages;
   uint8_t* v_keep;  // single-pass V-skip: [B, Hkv, nb] 1 where the block's V was read
+  int list_partition;  // masked ragged pass: 0 per KV head, 1 over all B * Hkv lists
 };
 
 constexpr int MAX_RAGGED_B = 256;  // batch bound of the ragged partition (one scan per 64)
+constexpr int MAX_GLOBAL_LISTS = 512;  // B * Hkv bound of the partition over all lists
 
 constexpr int MAX_SPLITS = 256;
 

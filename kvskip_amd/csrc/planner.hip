@@ -559,8 +559,9 @@ hipError_t launch_merge_update_t(const AttnP& a, const kvskip_update_args& p, hi
   else if (nb <= 4 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 4>), grid, blk, 0, s, a, p);
   else if (nb <= 8 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 8>), grid, blk, 0, s, a, p);
   else if (nb <= 16 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 16>), grid, blk, 0, s, a, p);
-  else if (nb <= 32 * WAVE) hipLaunchKernelGGL((merge_update_kernel<D, G, 32>), grid, blk, 0, s, a, p);
-  else {  // > 2048 blocks: the fused kernel would spill; two launches
+  else {  // > 1024 blocks: two launches (at 1025 blocks, B 32, the fused form took 77 us against
+          // 9 + 30 us for the merge and the update apart: its updates' load chains under the merge's
+          // traffic)
     const hipError_t e = launch_combine(a, D, false, s);
     if (e != hipSuccess) return e;
     return launch_update_t<G>(p, s);

@@ -531,11 +531,13 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
       const int g = wave + NWV * j;
       if (g >= G) break;
       const int64_t hrow = hrow0 + g;
-      float cn[R <= 16 ? R : 1];  // cs_now of the refresh, in flight during the search
-      if constexpr (R <= 16) {
+      // cs_now of the refresh: the first CN slots in flight during the search, the rest loaded in
+      // groups of CN below (a group's loads issued before its stores: the stores may alias them, so a
+      // load per slot placed after the previous slot's stores waited a round trip each)
+      constexpr int CN = R < 16 ? R : 16;
+      float cn[CN];
 #pragma unroll
-        for (int r = 0; r < R; ++r) cn[r] = p.cs_now[hrow * p.NBC + min(lane + WAVE * r, nb - 1)];
-      }
+      for (int r = 0; r < CN; ++r) cn[r] = p.cs_now[hrow * p.NBC + min(lane + WAVE * r, nb - 1)];
       float mx = NEG_INF;
 #pragma unroll
       for (int r = 0; r < R; ++r) mx = fmaxf(mx, x[j][r]);
@@ -574,16 +576,23 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
       }
       // references of the refresh: lse_ref <- x, cs_ref <- cs_now (capacity tail: -inf / 0)
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int i = lane + WAVE * r;
-        if (i < p.NBC) {
-          float c;
-          if constexpr (R <= 16)
-            c = cn[r];
-          else
-            c = p.cs_now[hrow * p.NBC + min(i, nb - 1)];
-          p.lse_ref[hrow * p.NBC + i] = x[j][r];
-          p.cs_ref[hrow * p.NBC + i] = i < nb ? c : 0.f;
+      for (int c0 = 0; c0 < R; c0 += CN) {
+        float cc[CN];
+        if (c0 == 0 || WAVE * c0 < nb) {  // uniform: a group past the sequence stores only the tail values
+#pragma unroll
+          for (int r = 0; r < CN; ++r)
+            cc[r] = c0 == 0 ? cn[r] : p.cs_now[hrow * p.NBC + min(lane + WAVE * (c0 + r), nb - 1)];
+        } else {
+#pragma unroll
+          for (int r = 0; r < CN; ++r) cc[r] = 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < CN; ++r) {
+          const int i = lane + WAVE * (c0 + r);
+          if (i < p.NBC) {
+            p.lse_ref[hrow * p.NBC + i] = x[j][c0 + r];
+            p.cs_ref[hrow * p.NBC + i] = i < nb ? cc[r] : 0.f;
+          }
         }
       }
       for (int i = WAVE * R + lane; i < p.NBC; i += WAVE) {

@@ -112,7 +112,7 @@ def _set_pages(a, block_table, pool):
 
 
 def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=True, num_splits=1, stages=2,
-           want_f32=False, write_p=False, seq_lens=None, block_table=None, T=None, merge=True):
+           want_f32=False, write_p=False, seq_lens=None, block_table=None, T=None, merge=True, list_partition=0):
     """Split-K decode attention (kernels/kvskip_ext.cpp:25-101).
 
     Returns [out bf16 [B,Hq,D], lse fp32 [B,Hq], blk_max, blk_sum ([B,Hq,nb] or None), out_f32 (or None),
@@ -120,7 +120,9 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
 
     seq_lens (not in the reference): int32 [B] on the device, a ragged batch; sequence b attends
     tokens [0, clamp(seq_lens[b], 1, T)) of its view; num_splits is then the per-KV-head split
-    budget over the whole batch (>= 2).
+    budget over the whole batch (>= 2). list_partition (not in the reference; block lists with
+    seq_lens): 0 cuts each KV head's lists over the batch, 1 all B * Hkv lists by one chunk length
+    (kvskip_attn_args.list_partition).
     block_table, T (not in the reference): a paged cache, see _kv_dims (the pass with V, MFMA engine).
     merge=False (not in the reference; load_v=False): the split pass alone, no merge launch; the block
     statistics and P are whole, lse is not computed (returned as None)."""
@@ -154,18 +156,19 @@ def decode(q, k, v, scale, block_idx=None, block_cnt=None, stats=False, load_v=T
         part_ml = torch.empty(B, Hq, num_splits, 2, **f32)
     split_only = not merge and num_splits > 1
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens, phase=1 if split_only else 3, block_table=block_table, T=T)
+                   pbuf, part_acc, part_ml, seq_lens, phase=1 if split_only else 3, block_table=block_table, T=T,
+                   list_partition=list_partition)
     return [out, None if split_only else lse, bmax, bsum, out32, pbuf]
 
 
 def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stats=False, num_splits=1,
-                seq_lens=None, phase=3, block_table=None, T=None):
+                seq_lens=None, phase=3, block_table=None, T=None, list_partition=0):
     """decode() into caller-owned buffers, allocating nothing (not in the reference): bufs holds
     out bf16, lse fp32 and, as needed, blk_max / blk_sum fp32 (>= B*Hq*nb elements, written as
     [B, Hq, nb], -inf / 0 where a list skips a block) and part_acc / part_ml fp32
     (>= B*Hq*num_splits*D / *2 elements). The fused planner loop runs its passes this way.
     phase: 3 = the whole op, 1 = the split pass only (its merge left to merge_splits / merge_update),
-    2 = that merge alone. block_table, T: a paged cache (see _kv_dims)."""
+    2 = that merge alone (given the pass's list_partition). block_table, T: a paged cache (see _kv_dims)."""
     check_q(q)
     check_kv(k, "k")
     check_kv(v, "v")
@@ -187,7 +190,7 @@ def decode_into(q, k, v, scale, bufs: dict, block_idx=None, block_cnt=None, stat
         _require(part_ml.dtype == torch.float32 and part_ml.is_contiguous()
                  and part_ml.numel() >= B * Hq * num_splits * 2, "bufs: part_ml")
     _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, True, num_splits, out, lse, bmax, bsum, None, None,
-                   part_acc, part_ml, seq_lens, phase, block_table, T)
+                   part_acc, part_ml, seq_lens, phase, block_table, T, list_partition)
 
 
 class DecodeOp:
@@ -232,7 +235,7 @@ class DecodeOp:
 
 
 def _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
-                 part_ml, seq_lens=None, block_table=None, T=None) -> AttnArgs:
+                 part_ml, seq_lens=None, block_table=None, T=None, list_partition=0) -> AttnArgs:
     B, Hq, D, Hkv, T = _kv_dims(q, k, v, block_table, T)
     a = _attn_args(q, k, v, scale, B, Hq, Hkv, T, D)
     _set_pages(a, block_table, k)
@@ -253,6 +256,7 @@ def _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bma
     a.out, a.out_f32, a.lse = _ptr(out), _ptr(out32), lse.data_ptr()
     a.blk_max, a.blk_sum = _ptr(bmax), _ptr(bsum)
     a.p_out = _ptr(pbuf)
+    a.list_partition = int(list_partition)
     return a
 
 
@@ -260,9 +264,9 @@ _PHASES = {3: "kvskip_decode", 1: "kvskip_decode_splits", 2: "kvskip_merge_split
 
 
 def _launch_decode(q, k, v, scale, block_idx, block_cnt, stats, load_v, num_splits, out, lse, bmax, bsum, out32,
-                   pbuf, part_acc, part_ml, seq_lens=None, phase=3, block_table=None, T=None):
+                   pbuf, part_acc, part_ml, seq_lens=None, phase=3, block_table=None, T=None, list_partition=0):
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, out, lse, bmax, bsum, out32, pbuf, part_acc,
-                     part_ml, seq_lens, block_table, T)
+                     part_ml, seq_lens, block_table, T, list_partition)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(getattr(_native.lib(), _PHASES[phase])(ctypes.byref(a), int(bool(stats)), int(bool(load_v)),
@@ -561,14 +565,14 @@ def update(blk_max, blk_sum, trig, cs_now, keep, lse_ref, cs_ref, lse_att, T, le
 
 
 def merge_update(q, k, v, scale, bufs: dict, num_splits, update_args: tuple, update_kwargs: dict,
-                 block_idx=None, block_cnt=None, seq_lens=None, block_table=None, T=None):
+                 block_idx=None, block_cnt=None, seq_lens=None, block_table=None, T=None, list_partition=0):
     """The split merge of a decode_into(..., phase=1) pass (same q, k, v, bufs, list, num_splits >= 2)
     and update(*update_args, **update_kwargs), in one launch (kvskip_merge_update; not in the
-    reference). block_table, T: the pass's paged cache (see _kv_dims)."""
+    reference). block_table, T: the pass's paged cache (see _kv_dims); list_partition: the pass's."""
     B, Hq, D = q.shape
     _require(num_splits >= 2, "merge_update needs num_splits >= 2")
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], None, None, None,
-                     None, bufs["part_acc"], bufs["part_ml"], seq_lens, block_table, T)
+                     None, bufs["part_acc"], bufs["part_ml"], seq_lens, block_table, T, list_partition)
     u = _update_args(*update_args, **update_kwargs)
     dev = q.device
     with torch.cuda.device(dev):
@@ -589,7 +593,7 @@ def launch_update(update: UpdateArgs, device):
 
 
 def decode_splits_update(q, k, v, scale, bufs: dict, block_idx, block_cnt, num_splits, update: UpdateArgs,
-                         seq_lens=None, block_table=None, T=None):
+                         seq_lens=None, block_table=None, T=None, list_partition=0):
     """decode_into(..., stats=True, phase=1) over a block list (the whole op when num_splits == 1)
     and the update of ANOTHER layer (an update_struct), in one launch (kvskip_decode_splits_update;
     not in the reference). The update reads only its own layer's buffers. block_table, T: a paged cache."""
@@ -608,7 +612,7 @@ def decode_splits_update(q, k, v, scale, bufs: dict, block_idx, block_cnt, num_s
         _require(part_acc.numel() >= B * Hq * num_splits * D and part_ml.numel() >= B * Hq * num_splits * 2,
                  "bufs: split partials")
     a = _decode_args(q, k, v, scale, block_idx, block_cnt, num_splits, bufs["out"], bufs["lse"], bmax, bsum, None,
-                     None, part_acc, part_ml, seq_lens, block_table, T)
+                     None, part_acc, part_ml, seq_lens, block_table, T, list_partition)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_decode_splits_update(ctypes.byref(a), ctypes.byref(update), _stream(dev)))

@@ -30,6 +30,8 @@ TILE = 64
 MARGIN = 64                      # spare block capacity of the state (src/kvskip_attn.py:399)
 BALANCE_MAX_LISTS = 16           # (b, KV head) lists a balanced planned pass decides in every workgroup
 RAGGED_DECIDE_MAX_B = 16         # sequences of a ragged batch whose lists a planned pass decides per KV head
+GLOBAL_PARTITION_MAX_LISTS = 512  # B * Hkv bound of kvskip_attn_args.list_partition = 1
+GLOBAL_PARTITION_MAX_B = 16        # sequences up to which the planner cuts all heads' lists together
 POST_MAX_SLOTS = 64              # first-pass partial slots the refresh mode's decision reads (lse_slots)
 KINDS = {"logit": 0, "add": 1, "peak": 2}
 
@@ -121,16 +123,17 @@ class FusedPlanner:
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
                  decide_in_pass: bool = True, balance: bool = True, batch_balance: bool = True,
-                 ragged_in_pass: bool | None = None):
+                 ragged_in_pass: bool | None = None, global_partition: bool = True):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
         # plan's decision inside the masked pass: one launch fewer per step, the same decisions and
         # lists as plan's own decision launch
         self.decide_in_pass = decide_in_pass
         # a ragged batch (seq_lens, B > 1) of a contiguous cache: every workgroup of the pass decides
-        # its KV head's B lists (B <= RAGGED_DECIDE_MAX_B); None: when that prologue is cheaper than
-        # plan's decision launch (measured: groups of <= 4 query heads and B <= 8: config 4's shape
-        # at B 8 -1.2%; config 5, G 7 and B 16: +2.9%), True / False: always / never
+        # its KV head's B lists (B <= RAGGED_DECIDE_MAX_B), and the lists are cut per KV head. None
+        # (the default): never, plan decides in its own launch and the pass cuts the lists of all
+        # heads together (global_partition; measured per layer-step: config 4's shape at B 8 with
+        # stable queries 92.7 -> 75.9 us, at B 8 180.7 -> 177.8, config 5 135.5 -> 132.9)
         self.ragged_in_pass = ragged_in_pass
         # with the decision in the pass and B * Hkv <= 16: the lists of all heads cut by one chunk
         # length (kvskip_plan_args.pass_budget), so a refreshing head gets more workgroups than a
@@ -141,6 +144,13 @@ class FusedPlanner:
         # lengths, all T, as seq_lens; a refreshing head of one sequence then no longer sets the
         # pass's time alone
         self.batch_balance = batch_balance
+        # a ragged batch of <= GLOBAL_PARTITION_MAX_B sequences whose lists plan decided: the lists
+        # of every KV head cut by one chunk length (kvskip_attn_args.list_partition = 1), so a head
+        # with refreshing sequences gets more workgroups instead of longer chunks (with few lists
+        # per head their refreshes do not even out: at B 8 the per-head cut's longest chunk was 1.8x
+        # the global one's; at B 32 the per-head cut measured 3.5% faster)
+        self.global_partition = global_partition
+        self._lp = 0
         self._pargs = None
         self._pg = {}               # this step's paged cache (block_table, T), if any
         self.state = None
@@ -221,15 +231,18 @@ class FusedPlanner:
                                  part_ml=torch.empty(B * Hq * S * 2, **f32))
         s = self.state
         self._S = S
+        self._lp = lp = int(self._pargs is None and self.global_partition and seq_lens is not None
+                            and 1 < B <= GLOBAL_PARTITION_MAX_B and B * Hkv <= GLOBAL_PARTITION_MAX_LISTS)
         carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         if self._pargs is not None:
             self._pargs.pass_budget = budget
             E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens, **pg)
         elif carried is not None:
-            E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens, **pg)
+            E.decode_splits_update(q, k, v, scale, b, s["block_idx"], s["block_cnt"], S, carried, seq_lens,
+                                   list_partition=lp, **pg)
         else:
             E.decode_into(q, k, v, scale, b, s["block_idx"], s["block_cnt"], stats=True, num_splits=S,
-                          seq_lens=seq_lens, phase=1 if S > 1 else 3, **pg)
+                          seq_lens=seq_lens, phase=1 if S > 1 else 3, list_partition=lp, **pg)
         n = B * Hq * nb
         return b["out"], b["blk_max"][:n].view(B, Hq, nb), b["blk_sum"][:n].view(B, Hq, nb)
 
@@ -241,14 +254,14 @@ class FusedPlanner:
         if self.carrier is not None:
             if self._S > 1:
                 E.decode_into(q, k, v, scale, self.bufs, s["block_idx"], s["block_cnt"], stats=True,
-                              num_splits=self._S, seq_lens=seq_lens, phase=2, **self._pg)
+                              num_splits=self._S, seq_lens=seq_lens, phase=2, list_partition=self._lp, **self._pg)
             G = q.shape[1] // k.shape[1]
             self.carrier.put(self, G, E.update_struct(*update_args, **update_kwargs),
                              (dict(s), self.bufs, update_args, update_kwargs))
             return
         if self._S > 1:
             E.merge_update(q, k, v, scale, self.bufs, self._S, update_args, update_kwargs, s["block_idx"],
-                           s["block_cnt"], seq_lens, **self._pg)
+                           s["block_cnt"], seq_lens, list_partition=self._lp, **self._pg)
         else:
             E.update(*update_args, **update_kwargs)
 
@@ -258,11 +271,8 @@ class FusedPlanner:
         ragged batch decides in the pass as ragged_in_pass says (up to RAGGED_DECIDE_MAX_B sequences
         of a contiguous cache: every workgroup decides its KV head's lists over the batch); else plan
         decides."""
-        B, Hq = q.shape[0], q.shape[1]
-        G = Hq // plan_args[1].shape[1]
-        rag = self.ragged_in_pass
-        if rag is None:
-            rag = B <= 8 and G <= 4
+        B = q.shape[0]
+        rag = bool(self.ragged_in_pass)
         if self.decide_in_pass and (seq_lens is None or B == 1
                                     or (rag and B <= RAGGED_DECIDE_MAX_B and not self._pg)):
             self._pargs = E.plan_struct(*plan_args, **plan_kwargs)

@@ -64,6 +64,10 @@ def _args(**kw):
     (dict(num_splits=4), -1, "split partial buffers"),
     (dict(T=0), -1, "sizes must be positive"),
     (dict(block_idx=0x6000), -1, "block_cnt is required with block_idx"),
+    (dict(list_partition=2), -1, "list_partition in {0, 1}"),
+    (dict(list_partition=1), -1, "list_partition 1 partitions a masked ragged pass"),
+    (dict(list_partition=1, block_idx=0x6000, block_cnt=0x7000, num_splits=4, part_acc=0x8000, part_ml=0x9000,
+          B=65, seq_lens=0xa000), -2, "list_partition 1: B * Hkv <= 512"),
 ])
 def test_decode_validation(kw, code, msg):
     lib = _native.lib()

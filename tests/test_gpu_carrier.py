@@ -154,7 +154,9 @@ def test_ragged_decision_in_pass(gpu, lens, Hkv, G, D, carry):
     qs = [[qps[l].next().cuda() for l in range(layers)] for _ in range(steps)]
     pol = lambda: Policy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
     cr = [UpdateCarrier(), UpdateCarrier()] if carry else [None, None]
-    ref = [FusedPlanner(pol(), count=False, carrier=cr[0], decide_in_pass=False) for _ in range(layers)]
+    # the reference cuts the lists per KV head as the in-pass decision does (global_partition off)
+    ref = [FusedPlanner(pol(), count=False, carrier=cr[0], decide_in_pass=False, global_partition=False)
+           for _ in range(layers)]
     dut = [FusedPlanner(pol(), count=False, carrier=cr[1], ragged_in_pass=True) for _ in range(layers)]
     for t in range(steps):
         sl = torch.tensor([T + t + 1 for T in lens], dtype=torch.int32, device="cuda")

@@ -70,8 +70,12 @@ def test_ragged_dense_stats(gpu, G, D, S):
         assert O.rel_err(r["out"][b:b + 1].float().cpu(), ref) <= REL
 
 
+@pytest.mark.parametrize("lp", [0, 1])
 @pytest.mark.parametrize("S", [2, 16, 128])
-def test_ragged_masked_stats(gpu, S):
+def test_ragged_masked_stats(gpu, S, lp):
+    """Masked ragged pass against the oracle per sequence, lists cut per KV head (lp 0) or over all
+    lists (lp 1, kvskip_attn_args.list_partition); with lp 1 the split pass and its merge as two
+    calls give the op's bits."""
     lens = [4096, 70, 2500, 640, 1, 3333]
     Hkv, G, D = 4, 7, 128
     Hq = Hkv * G
@@ -99,7 +103,14 @@ def test_ragged_masked_stats(gpu, S):
     bufs = _bufs(B, Hq, D, nb, S)
     sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
     E.decode_into(q.cuda(), k.cuda(), v.cuda(), scale, bufs, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
-                  seq_lens=sl)
+                  seq_lens=sl, list_partition=lp)
+    if lp:
+        two = _bufs(B, Hq, D, nb, S)
+        for phase in (1, 2):
+            E.decode_into(q.cuda(), k.cuda(), v.cuda(), scale, two, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
+                          seq_lens=sl, phase=phase, list_partition=lp)
+        for key in ("out", "lse", "blk_max", "blk_sum"):
+            assert torch.equal(two[key], bufs[key]), key
     bmax = bufs["blk_max"].view(B, Hq, nb).cpu()
     bsum = bufs["blk_sum"].view(B, Hq, nb).cpu()
     out = bufs["out"].float().cpu()
