@@ -412,7 +412,7 @@ def main():
                  (torch.rand(16, generator=g5, dtype=torch.float64) * math.log(16) + math.log(4096)).tolist()]
         res["planner_cfg5"] = bench_planner(dev, layers=28, steps=min(args.planner_steps, args.cfg5_steps), B=16,
                                             Hq=28, Hkv=4, ragged=lens5, dense_layer0=False, seed=5, chunk=8,
-                                            tag="cfg5")
+                                            tag="cfg5", one_launch_plan=True)
         torch.cuda.empty_cache()
         res["planner_cfg5"]["oracle_agreement"] = planner_agreement(dev, cfg=5)
         torch.cuda.empty_cache()
@@ -625,7 +625,7 @@ def pmc_paths(q, ks, vs, scale, bi, bc, dev):
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
-                  Hkv=8, ragged=None, dense_layer0=True, seed=4, p_jump=0.03, post=False):
+                  Hkv=8, ragged=None, dense_layer0=True, seed=4, p_jump=0.03, post=False, one_launch_plan=False):
     """The device-side planner loop over `layers` attention layers for `steps` decode steps (one
     token appended per step and sequence), query drift + jumps, stage-4 policy (delta 0.05, max
     age 32, calibration 0.05 peak, warm-up (32, 8), token-index latch at 0.1;
@@ -634,7 +634,9 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     eager pass with counters gives the read fraction and refresh rate; the timed passes replay HIP
     graphs of `chunk` steps x all layers (decisions still made on the device) for the planner loop
     and for dense decode of every layer. post: the reference's "refresh" mode instead (PostPlanner,
-    the trigger after the masked pass; its default policy: delta 0.05, max age 32, no calibration)."""
+    the trigger after the masked pass; its default policy: delta 0.05, max age 32, no calibration).
+    one_launch_plan: also time the loop with plan as one launch (FusedPlanner.plan_one_launch), where
+    plan decides in its own launch(es): three launches per layer-step."""
     import torch
 
     from kvskip_amd import ext as E
@@ -687,9 +689,9 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
             else:
                 planners[l].step(qs[t, l], k, v, run.scale, idx=idx_all[t], seq_lens=sl_all[t])
 
-    def make(count, carrier):
+    def make(count, carrier, **kw):
         return [None] * first_planned + [PostPlanner(pol, count=count, carrier=carrier) if post else
-                                         FusedPlanner(pol, count=count, carrier=carrier)
+                                         FusedPlanner(pol, count=count, carrier=carrier, **kw)
                                          for _ in range(first_planned, layers)]
 
     # eager pass with counters
@@ -742,6 +744,13 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
     planners = make(False, None)
     us_plan_own = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0))
     del planners
+    us_plan_one = math.nan
+    if one_launch_plan:
+        carrier = UpdateCarrier()
+        planners = make(False, carrier, plan_one_launch=True)
+        us_plan_one = timed(lambda t: planner_pass(planners, t), init=lambda: planner_pass(planners, 0),
+                            tail=carrier.flush)
+        del planners
     us_dense = timed(lambda t: [dense_layer(l, t) for l in range(layers)])
     n = (steps - 1) * layers
     us_replay, n_replay = replay_one_graph(run, qs, ids, pol, layers, first_planned, steps, T0) \
@@ -756,6 +765,7 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
            "blocks_read_frac": read / total,
            "refresh_rate": refresh / head_steps, "us_per_layer_step_policy": us_plan / n,
            "us_per_layer_step_policy_update_own_launch": us_plan_own / n,
+           "us_per_layer_step_policy_one_launch_plan": us_plan_one / n if one_launch_plan else None,
            "us_per_layer_step_policy_one_graph_replayed": us_replay / n_replay if n_replay else None,
            "us_per_layer_step_dense": us_dense / n, "time_vs_dense": us_plan / us_dense,
            "dense_GBs": (B * Hkv * (T0 + steps // 2) * D * 4 / (us_dense / n) / 1e3) if ragged is None else None,
@@ -763,7 +773,8 @@ def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, rev
            "ms_per_decode_step_dense": us_dense / (steps - 1) / 1e3}
     log(f"{tag}: policy {us_plan / n:.2f} us/layer-step ({'refresh mode, ' if post else ''}updates carried; "
         f"{us_plan_own / n:.2f} with their own launch) vs dense {us_dense / n:.2f} (x{us_plan / us_dense:.3f}), {us_plan / (steps - 1) / 1e3:.3f} ms per "
-        f"{layers}-layer step" + (f"; one graph replayed per step: {us_replay / n_replay:.2f}" if n_replay else ""))
+        f"{layers}-layer step" + (f"; one graph replayed per step: {us_replay / n_replay:.2f}" if n_replay else "")
+        + (f"; plan as one launch: {us_plan_one / n:.2f}" if one_launch_plan else ""))
     del run, qs
     return out
 

@@ -238,6 +238,12 @@ typedef struct kvskip_plan_args {
    * (lse_slots <= 64). */
   const float* lse_part;
   int32_t lse_slots, lse_stride;
+  /* Optional, with part (not in the reference): [B * Hkv] int32, zero before the first call and left
+   * zero by every call. kvskip_plan is then ONE launch: the last scores workgroup of each (b, KV
+   * head) to finish (counted on its ticket with an agent-scope atomic, after agent-scope stores of
+   * the partials) makes the head's decision and writes its list. Calls that share a ticket array
+   * must not overlap in time. Ignored by kvskip_plan_scores and kvskip_decode_splits_planned. */
+  int32_t* ticket;
 } kvskip_plan_args;
 
 #define KVSKIP_DECIDE_PLAN 0

@@ -51,7 +51,7 @@ class PlanArgs(ctypes.Structure):
         ("ids", c_void_p), ("ids_sb", c_int64), ("idx_out", c_void_p),
         ("block_table", c_void_p), ("bt_stride", c_int64), ("num_pages", c_int32), ("pass_budget", c_int32),
         ("decide_mode", c_int32), ("slot_base", c_int32), ("slot_count", c_int32),
-        ("lse_part", c_void_p), ("lse_slots", c_int32), ("lse_stride", c_int32),
+        ("lse_part", c_void_p), ("lse_slots", c_int32), ("lse_stride", c_int32), ("ticket", c_void_p),
     ]
 
 

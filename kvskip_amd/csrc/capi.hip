@@ -331,6 +331,7 @@ static int check_plan(const kvskip_plan_args* p) {
 int kvskip_plan(const kvskip_plan_args* p, void* stream) {
   const int rc = check_plan(p);
   if (rc != KVSKIP_OK) return rc;
+  if (p->ticket != nullptr && p->part == nullptr) return fail(KVSKIP_E_INVALID, "plan: ticket needs the part workspace");
   return launched(kvs::launch_plan(*p, static_cast<hipStream_t>(stream)), "kvskip_plan");
 }
 

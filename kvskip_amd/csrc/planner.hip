@@ -231,7 +231,59 @@ __global__ void __launch_bounds__(PNT) plan_kernel(const kvskip_plan_args p) {
   }
 }
 
-template <int D, int G>
+// The decision of (b, KV head h) from the scores pass's C partials and its block list (one
+// wavefront): plan_decide_kernel's body; COH: the partials come from other workgroups of the same
+// launch (agent-scope loads).
+template <int G, bool COH>
+__device__ __forceinline__ void decide_list(const kvskip_plan_args& p, int b, int h, int lane) {
+  // The sequence's length, used only after the decision: loaded first through an index the
+  // compiler takes for a per-lane one (a vector load, waited for at its use; as a scalar load its
+  // wait came before the decision's loads were issued). Without lengths lse_ref stands in (read
+  // only here, at least B entries), its value unused.
+  int bv = b;
+  asm volatile("" : "+v"(bv));
+  const int32_t sl = (p.seq_lens != nullptr ? p.seq_lens : reinterpret_cast<const int32_t*>(p.lse_ref))[bv];
+  uint32_t mk[DCL];
+  const bool tr = decide_head<G, COH>(p, b, h, lane, mk, true, true);
+  const int Tb = p.seq_lens != nullptr ? min(max(sl, 1), p.T) : p.T;  // seq_T's rule
+  const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
+  if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
+  write_block_list(p, static_cast<int64_t>(b) * p.Hkv + h, nb, tr, mk, lane);
+}
+
+// A scores partial written for the decision of the same launch (COH: relaxed agent-scope atomic
+// store, which goes past this XCD's L2 to the device's coherence point) or for a later launch.
+template <bool COH>
+__device__ __forceinline__ void st_part(float* a, float v) {
+  if constexpr (COH)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(a), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *a = v;
+}
+
+// The end of a scores workgroup of the one-launch plan (kvskip_plan_args.ticket): once its partial
+// stores have completed (s_waitcnt vmcnt(0) in every thread, then the barrier), one agent-scope
+// atomic add on the (b, KV head)'s ticket; the workgroup that draws C - 1 (every other partial
+// complete before it) decides the head from all C partials, then sets the ticket back to 0 for
+// the next call. No workgroup waits for another.
+template <int G>
+__device__ __forceinline__ void decide_if_last(const kvskip_plan_args& p, int b, int h, int C) {
+  __shared__ int sLast;
+  const int64_t bh = static_cast<int64_t>(b) * p.Hkv + h;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    sLast = __hip_atomic_fetch_add(p.ticket + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == C - 1 ? 1 : 0;
+  __syncthreads();
+  if (sLast == 0 || threadIdx.x >= WAVE) return;
+  decide_list<G, true>(p, b, h, threadIdx.x);
+  if (threadIdx.x == 0) __hip_atomic_store(p.ticket + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// FUSED (kvskip_plan_args.ticket set): the one-launch plan, the decision by each head's last
+// workgroup (decide_if_last); else the scores pass alone, its partials published by the kernel's end.
+template <int D, int G, bool FUSED>
 __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args p) {
   constexpr int DL = D / 16, DW = DL / 4, SP = part_stride(G);
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, C = gridDim.x;
@@ -243,10 +295,11 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   if (c * WCB >= nb) {  // a chunk past the sequence's blocks (ragged batch): the empty partial
     float* part = p.part + (bh * C + c) * SP;
     if (tid < G) {
-      part[tid] = NEG_INF;
-      part[G + tid] = 0.f;
+      st_part<FUSED>(part + tid, NEG_INF);
+      st_part<FUSED>(part + G + tid, 0.f);
     }
-    if (tid == 0) part[2 * G] = __uint_as_float(0u);
+    if (tid == 0) st_part<FUSED>(part + 2 * G, __uint_as_float(0u));
+    if constexpr (FUSED) decide_if_last<G>(p, b, h, C);
     return;
   }
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hq + static_cast<int64_t>(h) * G) * p.NBC;
@@ -407,35 +460,23 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
     float m = NEG_INF, sv = 0.f;
 #pragma unroll
     for (int w = 0; w < WW; ++w) lse_merge(m, sv, sM[w][lane], sS[w][lane]);
-    part[lane] = m;
-    part[G + lane] = sv;
+    st_part<FUSED>(part + lane, m);
+    st_part<FUSED>(part + G + lane, sv);
   }
   if (tid == 0) {
     uint32_t mk = 0;
 #pragma unroll
     for (int w = 0; w < WW; ++w) mk |= sMask[w] << (8 * w);
-    part[2 * G] = __uint_as_float(mk);
+    st_part<FUSED>(part + 2 * G, __uint_as_float(mk));
   }
+  if constexpr (FUSED) decide_if_last<G>(p, b, h, C);
 }
 
 // One wavefront per (b, KV head): the decision from the C = ceil(nb / 32) partials (decide_head,
 // the arithmetic the planned pass's prologue repeats) and the list compacted from the chunk masks.
 template <int G>
 __global__ void __launch_bounds__(WAVE) plan_decide_kernel(const kvskip_plan_args p) {
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  // The sequence's length, used only after the decision: loaded first through an index the
-  // compiler takes for a per-lane one (a vector load, waited for at its use; as a scalar load its
-  // wait came before the decision's loads were issued). Without lengths lse_ref stands in (read
-  // only here, at least B entries), its value unused.
-  int bv = b;
-  asm volatile("" : "+v"(bv));
-  const int32_t sl = (p.seq_lens != nullptr ? p.seq_lens : reinterpret_cast<const int32_t*>(p.lse_ref))[bv];
-  uint32_t mk[DCL];
-  const bool tr = decide_head<G>(p, b, h, lane, mk, true, true);
-  const int Tb = p.seq_lens != nullptr ? min(max(sl, 1), p.T) : p.T;  // seq_T's rule
-  const int nb = (Tb + BLK - 1) / BLK;  // the sequence's blocks
-  if (p.seq_lens_out != nullptr && h == 0 && lane == 0) p.seq_lens_out[b] = Tb;
-  write_block_list(p, static_cast<int64_t>(b) * p.Hkv + h, nb, tr, mk, lane);
+  decide_list<G, false>(p, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 template <int G, int R>
@@ -527,9 +568,12 @@ __global__ void __launch_bounds__(256) token_index_kernel(const int32_t* ids, in
 
 template <int D, int G>
 hipError_t launch_plan_t(const kvskip_plan_args& p, hipStream_t s) {
-  if (p.part != nullptr) {
+  if (p.part != nullptr && p.ticket != nullptr) {
     const int nb = (p.T + BLK - 1) / BLK;
-    hipLaunchKernelGGL((plan_scores_kernel<D, G>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p);
+    hipLaunchKernelGGL((plan_scores_kernel<D, G, true>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p);
+  } else if (p.part != nullptr) {
+    const int nb = (p.T + BLK - 1) / BLK;
+    hipLaunchKernelGGL((plan_scores_kernel<D, G, false>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p);
     hipLaunchKernelGGL((plan_decide_kernel<G>), dim3(p.Hkv, p.B), dim3(WAVE), 0, s, p);
   } else {
     hipLaunchKernelGGL((plan_kernel<D, G>), dim3(p.Hkv, p.B), dim3(PNT), 0, s, p);
@@ -604,7 +648,7 @@ hipError_t launch_plan_scores(const kvskip_plan_args& p, hipStream_t s) {
   const int nb = (p.T + BLK - 1) / BLK;
 #define KVS_CASE(DD, GG)                                                                                     \
   if (p.D == DD && G == GG) {                                                                                \
-    hipLaunchKernelGGL((plan_scores_kernel<DD, GG>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p); \
+    hipLaunchKernelGGL((plan_scores_kernel<DD, GG, false>), dim3((nb + WCB - 1) / WCB, p.Hkv, p.B), dim3(WNT), 0, s, p); \
     return hipGetLastError();                                                                                \
   }
   KVS_CASE(64, 1) KVS_CASE(64, 2) KVS_CASE(64, 4) KVS_CASE(64, 7) KVS_CASE(64, 8)

@@ -83,12 +83,24 @@ constexpr int DLP = 8;
 constexpr int LSI = 8;   // partial slots per team lane of an attended log-sum-exp from partials (<= 64 slots)
 static_assert(LSI * DLP == 64, "kvskip_plan_args.lse_slots is validated against 64");
 
+// A scores partial, read (COH) with a relaxed agent-scope atomic load: one that another workgroup
+// of the same launch wrote through agent-scope stores, past this XCD's L2 (which may hold a stale
+// copy of the line: partials of several workgroups share one).
+template <bool COH>
+__device__ __forceinline__ float ld_part(const float* a) {
+  if constexpr (COH)
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(a), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+  else
+    return *a;
+}
+
 template <int CTRL>
 __device__ __forceinline__ void lse_dpp(float& m, float& s) {
   lse_merge(m, s, dpp<CTRL>(m), dpp<CTRL>(s));
 }
 
-template <int G, int NH>
+template <int G, int NH, bool COH = false>
 __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const int (&bh)[NH], int lane,
                                              uint32_t (&mk)[NH][DCL], bool (&tr)[NH], bool write,
                                              bool write_age = true) {
@@ -104,7 +116,7 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
   for (int k = 0; k < NH; ++k) {
     const float* pb = p.part + static_cast<int64_t>(bh[k]) * C * SP;
 #pragma unroll
-    for (int j = 0; j < DCL; ++j) mk[k][j] = __float_as_uint(pb[min(lane + WAVE * j, C - 1) * SP + 2 * G]);
+    for (int j = 0; j < DCL; ++j) mk[k][j] = __float_as_uint(ld_part<COH>(pb + min(lane + WAVE * j, C - 1) * SP + 2 * G));
   }
   // The per-list values are the same on every lane; read through an index the compiler takes for a
   // per-lane one, they stay in vector registers, where a uniform value would be moved to a scalar
@@ -149,8 +161,8 @@ __device__ __forceinline__ void decide_heads(const kvskip_plan_args& p, const in
       ps[i] = 0.f;
       if (i < NI) {
         const int cc = min(t + DLP * i, C - 1);
-        pm[i] = pb[cc * SP + g];
-        ps[i] = pb[cc * SP + G + g];
+        pm[i] = ld_part<COH>(pb + cc * SP + g);
+        ps[i] = ld_part<COH>(pb + cc * SP + G + g);
       }
     }
 #pragma unroll
@@ -239,13 +251,13 @@ __device__ __forceinline__ void apply_decide_mode(int mode, uint32_t (&mk)[NH][D
   }
 }
 
-template <int G>
+template <int G, bool COH = false>
 __device__ __forceinline__ bool decide_head(const kvskip_plan_args& p, int b, int h, int lane, uint32_t (&mk)[DCL],
                                             bool write, bool write_age = true, int mode = DECIDE_PLAN, int nb = 0) {
   const int bh[1] = {b * p.Hkv + h};
   uint32_t m[1][DCL];
   bool tr[1];
-  decide_heads<G, 1>(p, bh, lane, m, tr, write, write_age);
+  decide_heads<G, 1, COH>(p, bh, lane, m, tr, write, write_age);
   apply_decide_mode<1>(mode, m, tr, lane, nb);
 #pragma unroll
   for (int j = 0; j < DCL; ++j) mk[j] = m[0][j];

@@ -358,7 +358,8 @@ def vskip1(q, k, v, scale, tau, local=2, num_splits=1, want_f32=False, count=Fal
 
 def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None):
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None,
+         ticket=None):
     """Device-side refresh planner before the pass (kernels/kvskip_ext.cpp:205-267); in place.
 
     part (not in the reference): fp32 workspace of plan_part_floats(...) elements; with it the
@@ -369,10 +370,13 @@ def plan(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, b
     this step (for the step's update, which may run later).
     ids, idx_out (not in the reference; need part, and idx None): token ids int32 [B, >= T]; the
     plan finds this step's token-index blocks itself and writes them to idx_out (uint8 [B, NBC]).
-    block_table, T (not in the reference): k is the page pool of a paged cache (see _kv_dims)."""
+    block_table, T (not in the reference): k is the page pool of a paged cache (see _kv_dims).
+    ticket (not in the reference; needs part): int32 [B * Hkv] on the device, zero before the first
+    call and left zero by each call; the plan is then one launch (each head decided by its last
+    scores workgroup, kvskip_plan_args.ticket). Calls sharing one must not overlap in time."""
     p = _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale,
                    delta, max_age, local, add_token, idx, calib, est, calib_on, calib_kind, aix, part, seq_lens,
-                   seq_lens_out, ids, idx_out, block_table, T)
+                   seq_lens_out, ids, idx_out, block_table, T, ticket)
     dev = q.device
     with torch.cuda.device(dev):
         _native.check(_native.lib().kvskip_plan(ctypes.byref(p), _stream(dev)))
@@ -427,7 +431,8 @@ def decode_splits_planned(q, k, v, scale, bufs: dict, pargs: PlanArgs, num_split
 
 def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, trig, block_idx, block_cnt, scale, delta,
          max_age, local, add_token, idx=None, calib=None, est=None, calib_on=False, calib_kind=0, aix=None,
-         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None):
+         part=None, seq_lens=None, seq_lens_out=None, ids=None, idx_out=None, block_table=None, T=None,
+               ticket=None):
     """kvskip_plan_args of plan(), validated. block_table, T: a paged cache (see _kv_dims)."""
     _require(q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.stride(2) == 1, "q: CUDA bf16 [B, Hq, D]")
     check_kv(k, "k")
@@ -490,6 +495,11 @@ def _plan_args(q, k, csum, lse_ref, cs_ref, keep, lse_att, age, flags, cs_now, t
         _require(idx_out.dtype == torch.uint8 and idx_out.is_contiguous() and tuple(idx_out.shape) == (B, NBC),
                  "idx_out: uint8 [B, NBC]")
         p.ids, p.ids_sb, p.idx_out = ids.data_ptr(), ids.stride(0), idx_out.data_ptr()
+    if ticket is not None:
+        _require(part is not None, "plan: ticket needs part")
+        _require(ticket.is_cuda and ticket.dtype == torch.int32 and ticket.is_contiguous() and ticket.numel() == B * Hkv,
+                 "ticket: contiguous int32 [B * Hkv] on the device")
+        p.ticket = ticket.data_ptr()
     return p
 
 

@@ -123,7 +123,7 @@ class FusedPlanner:
 
     def __init__(self, policy: Policy, count: bool = True, carrier: UpdateCarrier | None = None,
                  decide_in_pass: bool = True, balance: bool = True, batch_balance: bool = True,
-                 ragged_in_pass: bool | None = None, global_partition: bool = True):
+                 ragged_in_pass: bool | None = None, global_partition: bool = True, plan_one_launch: bool = False):
         self.policy = policy
         self.carrier = carrier      # shared by the layers: updates ride on the next layer's pass
         # plan's decision inside the masked pass: one launch fewer per step, the same decisions and
@@ -150,6 +150,13 @@ class FusedPlanner:
         # per head their refreshes do not even out: at B 8 the per-head cut's longest chunk was 1.8x
         # the global one's; at B 32 the per-head cut measured 3.5% faster)
         self.global_partition = global_partition
+        # plan with its decision in the scores launch (kvskip_plan_args.ticket): each head decided by
+        # its last scores workgroup, one launch instead of two where plan decides. Off by default:
+        # graph-replayed, the last workgroup's chain (its partial stores acknowledged at the device's
+        # coherence point, the ticket's round trip, the partials read past L2) cost more than the
+        # launch it saves (per layer-step: B 8 stable 75.9 -> 77.9 us, config 5 132.9 -> 134.1); it
+        # saves a launch's host time where a loop is not captured
+        self.plan_one_launch = plan_one_launch
         self._lp = 0
         self._pargs = None
         self._pg = {}               # this step's paged cache (block_table, T), if any
@@ -186,6 +193,7 @@ class FusedPlanner:
             tlen=torch.zeros(B, dtype=torch.int32, device=dev),       # this step's lengths (ragged)
             lens=torch.zeros(B, dtype=torch.int32, device=dev),       # all T, for batch_balance
             part=torch.empty(E.plan_part_floats(B, Hq, Hkv, NBC), **f32),     # multi-workgroup plan
+            ticket=torch.zeros(B * Hkv, dtype=torch.int32, device=dev),      # one-launch plan (self-resetting)
         )
 
     def _grow(self, NBC):
@@ -279,7 +287,7 @@ class FusedPlanner:
             E.plan_scores(self._pargs, q.device)
         else:
             self._pargs = None
-            E.plan(*plan_args, **plan_kwargs)
+            E.plan(*plan_args, ticket=self.state["ticket"] if self.plan_one_launch else None, **plan_kwargs)
 
     def _age(self):
         return dict(age=self.state["age"]) if self._pargs is not None else {}

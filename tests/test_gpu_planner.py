@@ -103,6 +103,7 @@ def test_plan_update_kernels(gpu, G, D, B, Hkv, T0):
         qd = q.cuda()
         # the multi-workgroup plan on a copy of the state, then the one-workgroup plan on the state
         wide = {key: s[key].clone() for key in ("csum", "age", "cs_now", "trig", "block_idx", "block_cnt", "est")}
+        one = {key: s[key].clone() for key in wide}
         E.plan(qd, k[:, :, :T], wide["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], wide["age"],
                s["flags"], wide["cs_now"], wide["trig"], wide["block_idx"], wide["block_cnt"], run.scale, pol.delta,
                OP.max_age_at(pol, step), pol.local, True, None, s["calib"], wide["est"], True,
@@ -110,6 +111,20 @@ def test_plan_update_kernels(gpu, G, D, B, Hkv, T0):
         E.plan(qd, k[:, :, :T], s["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], s["age"], s["flags"],
                s["cs_now"], s["trig"], s["block_idx"], s["block_cnt"], run.scale, pol.delta, OP.max_age_at(pol, step),
                pol.local, True, None, s["calib"], s["est"], True, OP.KINDS[pol.calib_kind], None)
+        # the one-launch plan (ticket: the decision by each head's last scores workgroup) on another
+        # copy: bit-identical to the two launches, its tickets back to zero
+        ticket = torch.zeros(B * Hkv, dtype=torch.int32, device="cuda")
+        E.plan(qd, k[:, :, :T], one["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], one["age"],
+               s["flags"], one["cs_now"], one["trig"], one["block_idx"], one["block_cnt"], run.scale, pol.delta,
+               OP.max_age_at(pol, step), pol.local, True, None, s["calib"], one["est"], True,
+               OP.KINDS[pol.calib_kind], None, part=s["part"], ticket=ticket)
+        for key in ("csum", "cs_now", "trig", "block_cnt", "age", "est"):
+            assert torch.equal(one[key], wide[key]), f"one-launch plan: {key}"
+        for bb in range(B):
+            for hh in range(Hkv):
+                n = int(wide["block_cnt"][bb, hh])
+                assert torch.equal(one["block_idx"][bb, hh, :n], wide["block_idx"][bb, hh, :n]), "one-launch plan: list"
+        assert (ticket == 0).all()
         for key in ("csum", "cs_now", "trig", "block_cnt", "age"):       # same arithmetic per row
             assert torch.equal(wide[key], s[key]), f"wide plan: {key}"
         for bb in range(B):
@@ -387,3 +402,75 @@ def test_index_latch_on_heads_not_refreshing(gpu):
              False, 2, aix, thr)
     assert aix.cpu().tolist() == [[0, 1]]
     assert calib.cpu().tolist() == [[thr, up]]
+
+
+@pytest.mark.parametrize("B,Hkv,G,D,ragged", [(8, 8, 4, 128, False), (16, 4, 7, 128, True), (3, 2, 8, 64, True)])
+def test_plan_one_launch_loop(gpu, B, Hkv, G, D, ragged):
+    """The planner loop of a batch whose lists plan decides (lengths in device memory), with plan as
+    one launch (each head decided by its last scores workgroup; FusedPlanner.plan_one_launch) and as
+    two: bit-identical outputs and state on every step, the tickets back to zero; then one step's
+    plan captured in a HIP graph and replayed three times from a saved state, each replay against
+    the two-launch plan on that state (the tickets reset themselves between replays)."""
+    steps = 8
+    lens = [1500 + 977 * (b % 5) for b in range(B)] if ragged else None
+    run = W.planner_run(layers=1, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=3000 if lens is None else max(lens), steps=steps,
+                        seed=61 + B + G, ragged=lens)
+    k, v = run.k[0].cuda(), run.v[0].cuda()
+    ids = run.ids.to(torch.int32).cuda()
+    qp = W.QueryProcess(run, 0, p_jump=0.2, revert=True)
+    pol = DPolicy(calib=0.05, calib_kind="peak", calib_warm=(4, 2), calib_auto_ix=0.1)
+    one, two = FusedPlanner(pol, count=False, plan_one_launch=True), FusedPlanner(pol, count=False)
+    keys = ("keep", "lse_ref", "cs_ref", "lse_att", "age", "trig", "block_idx", "block_cnt", "calib", "aix", "cs_now",
+            "est", "csum")
+    Tcap = k.shape[2]
+    for t in range(steps):
+        q = qp.next().cuda()
+        if lens is None:
+            T = 3000 + t + 1
+            kv, sl = (k[:, :, :T], v[:, :, :T]), torch.full((B,), T, dtype=torch.int32, device="cuda")
+        else:
+            kv = (k, v)
+            sl = torch.tensor([L + t + 1 for L in lens], dtype=torch.int32, device="cuda")
+        outs = [(fp.first(q, *kv, run.scale, seq_lens=sl) if t == 0 else
+                 fp.step(q, *kv, run.scale, ids=ids, seq_lens=sl)).clone() for fp in (one, two)]
+        assert two._pargs is None                 # plan decided in its own launch(es)
+        assert torch.equal(outs[0], outs[1]), t
+        for key in keys:
+            assert torch.equal(one.state[key], two.state[key]), (t, key)
+        assert (one.state["ticket"] == 0).all()
+    # graph replays of one plan call (the planner's own arguments, from a saved state)
+    s = one.state
+    T = (3000 + steps + 1) if lens is None else Tcap
+    kk = k[:, :, :T] if lens is None else k
+    sl = torch.full((B,), T, dtype=torch.int32, device="cuda") if lens is None else \
+        torch.tensor([L + steps + 1 for L in lens], dtype=torch.int32, device="cuda")
+    q = qp.next().cuda()
+    mut = ("csum", "age", "cs_now", "trig", "block_idx", "block_cnt", "est")
+    saved = {key: s[key].clone() for key in mut}
+
+    def plan_call(st, ticket):
+        E.plan(q, kk, st["csum"], s["lse_ref"], s["cs_ref"], s["keep"], s["lse_att"], st["age"], s["flags"],
+               st["cs_now"], st["trig"], st["block_idx"], st["block_cnt"], run.scale, pol.delta, pol.max_age,
+               pol.local, True, None, s["calib"], st["est"], True, 2, None, part=s["part"], seq_lens=sl,
+               ticket=ticket)
+
+    ref = {key: saved[key].clone() for key in mut}
+    plan_call(ref, None)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        plan_call(s, s["ticket"])                 # warm-up outside the capture
+        with torch.cuda.graph(g, stream=side):
+            plan_call(s, s["ticket"])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for key in mut:
+            s[key].copy_(saved[key])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for key in mut:
+            assert torch.equal(s[key], ref[key]), (rep, key)
+        assert (s["ticket"] == 0).all(), rep
