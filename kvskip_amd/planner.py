@@ -31,7 +31,7 @@ MARGIN = 64                      # spare block capacity of the state (src/kvskip
 BALANCE_MAX_LISTS = 16           # (b, KV head) lists a balanced planned pass decides in every workgroup
 RAGGED_DECIDE_MAX_B = 16         # sequences of a ragged batch whose lists a planned pass decides per KV head
 GLOBAL_PARTITION_MAX_LISTS = 512  # B * Hkv bound of kvskip_attn_args.list_partition = 1
-GLOBAL_PARTITION_MAX_B = 16        # sequences up to which the planner cuts all heads' lists together
+GLOBAL_PARTITION_MAX_B = 64        # sequences up to which the planner cuts all heads' lists together
 POST_MAX_SLOTS = 64              # first-pass partial slots the refresh mode's decision reads (lse_slots)
 KINDS = {"logit": 0, "add": 1, "peak": 2}
 
@@ -146,9 +146,9 @@ class FusedPlanner:
         self.batch_balance = batch_balance
         # a ragged batch of <= GLOBAL_PARTITION_MAX_B sequences whose lists plan decided: the lists
         # of every KV head cut by one chunk length (kvskip_attn_args.list_partition = 1), so a head
-        # with refreshing sequences gets more workgroups instead of longer chunks (with few lists
-        # per head their refreshes do not even out: at B 8 the per-head cut's longest chunk was 1.8x
-        # the global one's; at B 32 the per-head cut measured 3.5% faster)
+        # with refreshing sequences gets more workgroups instead of longer chunks (at B 8 the
+        # per-head cut's longest chunk was 1.8x the global one's; per layer-step B 8 stable 94.1 ->
+        # 73.9 us, B 32 at 64k 651 -> 630, config 5 132.4 -> 131.5)
         self.global_partition = global_partition
         # plan with its decision in the scores launch (kvskip_plan_args.ticket): each head decided by
         # its last scores workgroup, one launch instead of two where plan decides. Off by default:
@@ -220,6 +220,11 @@ class FusedPlanner:
         Hkv = k.shape[1]
         # one sequence (its length in device memory) is split as an unragged batch
         S = K.num_splits_for(B * Hkv, nb) if seq_lens is None or B == 1 else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv)
+        if seq_lens is not None and B > 16 and Hq // Hkv <= 4:
+            # many lists: twice the chunk slots, so that the queued workgroups even out the chunks'
+            # lengths (B 32 at 64k, all lists cut together: 629 -> 607 us per layer-step; 168 slots
+            # 609; at B 8 56 stays best: 73.9 vs 78.7 at 84)
+            S = min(256, 2 * S)
         budget = 0
         if (self._pargs is not None and self.balance and B * Hkv <= BALANCE_MAX_LISTS and S > 1
                 and (seq_lens is None or B == 1)):
