@@ -302,7 +302,7 @@ int kvskip_merge_update(const kvskip_attn_args* a, const kvskip_update_args* u, 
  * reference: a layer's update only reads that layer's statistics and is only read by that
  * layer's next plan, so the device planner loop runs it inside the next layer's pass (under its
  * streaming) instead of in a launch of its own. u and a must not share outputs; u's group size
- * equals a's. Updates over more than 1024 blocks, or with the VALU engine selected, run as two
+ * equals a's. Updates over more than 1536 blocks, or with the VALU engine selected, run as two
  * launches (same results). */
 int kvskip_decode_splits_update(const kvskip_attn_args* a, const kvskip_update_args* u, void* stream);
 

@@ -45,6 +45,7 @@ hipError_t launch_planned_p(const AttnP& a, const kvskip_plan_args& pa, const kv
   if (nb <= 2 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 2, PAGED, RAG>), grid, blk, 0, s, a, pa, *u);
   else if (nb <= 4 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 4, PAGED, RAG>), grid, blk, 0, s, a, pa, *u);
   else if (nb <= 8 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 8, PAGED, RAG>), grid, blk, 0, s, a, pa, *u);
+  else if (nb <= 16 * WAVE) hipLaunchKernelGGL((planned_split_kernel<D, G, 16, PAGED, RAG>), grid, blk, 0, s, a, pa, *u);
   else hipLaunchKernelGGL((planned_split_kernel<D, G, CARRY_MAX_R, PAGED, RAG>), grid, blk, 0, s, a, pa, *u);
   return hipGetLastError();
 }

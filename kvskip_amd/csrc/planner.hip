@@ -589,6 +589,7 @@ hipError_t launch_update_t(const kvskip_update_args& p, hipStream_t s) {
   else if (nb <= 4 * WAVE) hipLaunchKernelGGL((update_kernel<G, 4>), grid, blk, 0, s, p);
   else if (nb <= 8 * WAVE) hipLaunchKernelGGL((update_kernel<G, 8>), grid, blk, 0, s, p);
   else if (nb <= 16 * WAVE) hipLaunchKernelGGL((update_kernel<G, 16>), grid, blk, 0, s, p);
+  else if (nb <= 24 * WAVE) hipLaunchKernelGGL((update_kernel<G, 24>), grid, blk, 0, s, p);
   else if (nb <= 32 * WAVE) hipLaunchKernelGGL((update_kernel<G, 32>), grid, blk, 0, s, p);
   else if (nb <= 64 * WAVE) hipLaunchKernelGGL((update_kernel<G, 64>), grid, blk, 0, s, p);
   else return hipErrorInvalidValue;

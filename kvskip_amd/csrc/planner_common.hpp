@@ -321,9 +321,10 @@ __device__ __forceinline__ void write_block_list(const kvskip_plan_args& p, int6
 }
 
 // An update carried by a pass runs in the pass's NWAVE-wavefront workgroups, over up to
-// CARRY_MAX_R * 64 blocks (longer: its own launch first).
+// CARRY_MAX_R * 64 blocks (longer: its own launch first). R = 24 (1025..1536 blocks, B 32 at 64k)
+// still fits the pass's registers; R = 32 did not.
 constexpr int carry_waves(int G) { return G < NWAVE ? G : NWAVE; }
-constexpr int CARRY_MAX_R = 16;
+constexpr int CARRY_MAX_R = 24;
 
 // Order-preserving key of a float (larger float -> larger key).
 __device__ __forceinline__ uint32_t fkey(float y) {
@@ -465,7 +466,7 @@ __device__ __forceinline__ uint32_t topp_theta(const uint32_t (&key)[R], const f
 template <int G, int R, int NWV>
 __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, int b) {
   constexpr int HPW = (G + NWV - 1) / NWV;
-  constexpr int RC = R < 16 ? R : 16;  // register slots whose loads are in flight together
+  constexpr int RC = R <= 16 ? R : (R % 16 == 0 ? 16 : 8);  // register slots whose loads are in flight together
   if (threadIdx.x >= NWV * WAVE) {
     __syncthreads();
     return;
@@ -546,7 +547,7 @@ __device__ __forceinline__ void update_body(const kvskip_update_args& p, int h, 
       // cs_now of the refresh: the first CN slots in flight during the search, the rest loaded in
       // groups of CN below (a group's loads issued before its stores: the stores may alias them, so a
       // load per slot placed after the previous slot's stores waited a round trip each)
-      constexpr int CN = R < 16 ? R : 16;
+      constexpr int CN = R <= 16 ? R : (R % 16 == 0 ? 16 : 8);
       float cn[CN];
 #pragma unroll
       for (int r = 0; r < CN; ++r) cn[r] = p.cs_now[hrow * p.NBC + min(lane + WAVE * r, nb - 1)];

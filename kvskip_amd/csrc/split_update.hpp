@@ -28,6 +28,7 @@ hipError_t launch_split_update_t(const AttnP& a, const kvskip_update_args& u, hi
   if (nb <= 2 * WAVE) hipLaunchKernelGGL((split_update_kernel<D, G, RAG, 2, PAGED>), grid, blk, 0, s, a, u);
   else if (nb <= 4 * WAVE) hipLaunchKernelGGL((split_update_kernel<D, G, RAG, 4, PAGED>), grid, blk, 0, s, a, u);
   else if (nb <= 8 * WAVE) hipLaunchKernelGGL((split_update_kernel<D, G, RAG, 8, PAGED>), grid, blk, 0, s, a, u);
+  else if (nb <= 16 * WAVE) hipLaunchKernelGGL((split_update_kernel<D, G, RAG, 16, PAGED>), grid, blk, 0, s, a, u);
   else hipLaunchKernelGGL((split_update_kernel<D, G, RAG, CARRY_MAX_R, PAGED>), grid, blk, 0, s, a, u);
   return hipGetLastError();
 }
