@@ -131,6 +131,54 @@ def test_ragged_masked_stats(gpu, S, lp):
         assert (bmax[b, :, nbb:] == -math.inf).all() and (bsum[b, :, nbb:] == 0).all(), (b, T)
 
 
+def test_list_partition_all_lists_at_its_bound(gpu):
+    """list_partition 1 at B * Hkv = 512 lists (its bound: eight counts per lane): the same outputs as
+    the per-head cut to the split merge's rounding, bit-identical statistics, empty and full lists
+    among them, and 513 lists refused."""
+    B, Hkv, G, D, cap = 64, 8, 2, 64, 640
+    Hq = Hkv * G
+    g = torch.Generator().manual_seed(77)
+    lens = [int(x) for x in torch.randint(1, cap + 1, (B,), generator=g)]
+    q, k, v = _layer(lens, Hq, Hkv, D, cap, seed=78)
+    nb = math.ceil(cap / 64)
+    keep = torch.rand(B, Hkv, nb, generator=g) < 0.4
+    for b, T in enumerate(lens):
+        keep[b, :, math.ceil(T / 64):] = False
+    keep[3] = False                                          # empty lists
+    keep[5, :, :math.ceil(lens[5] / 64)] = True              # full lists
+    bi = torch.zeros(B, Hkv, nb, dtype=torch.int32)
+    bc = torch.zeros(B, Hkv, dtype=torch.int32)
+    for b in range(B):
+        for h in range(Hkv):
+            idx = torch.nonzero(keep[b, h])[:, 0].to(torch.int32)
+            bi[b, h, :len(idx)] = idx
+            bc[b, h] = len(idx)
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    S = 8
+    res = []
+    for lp in (0, 1):
+        bufs = _bufs(B, Hq, D, nb, S)
+        E.decode_into(q.cuda(), k.cuda(), v.cuda(), 0.125, bufs, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
+                      seq_lens=sl, list_partition=lp)
+        res.append(bufs)
+    assert torch.equal(res[0]["blk_max"], res[1]["blk_max"]) and torch.equal(res[0]["blk_sum"], res[1]["blk_sum"])
+    assert (res[0]["out"].float() - res[1]["out"].float()).abs().max().item() <= 2e-2
+    fin = torch.isfinite(res[0]["lse"])
+    assert torch.equal(fin, torch.isfinite(res[1]["lse"]))
+    assert (res[0]["lse"][fin] - res[1]["lse"][fin]).abs().max().item() <= 1e-5
+    for b, T in [(0, lens[0]), (5, lens[5]), (40, lens[40])]:
+        nbb = math.ceil(T / 64)
+        ref, _ = O.decode(q[b:b + 1], k[b:b + 1, :, :T], v[b:b + 1, :, :T], 0.125, keep=keep[b:b + 1, :, :nbb])
+        live = keep[b].any(-1).repeat_interleave(G)
+        if live.any():
+            assert O.rel_err(res[1]["out"].view(B, Hq, D)[b][live].float().cpu()[None], ref[0][live][None]) <= REL
+    q2, k2, v2 = _layer([10] * 65, Hq, Hkv, D, 64, seed=79)
+    with pytest.raises(RuntimeError, match="B \\* Hkv <= 512"):
+        E.decode(q2.cuda(), k2.cuda(), v2.cuda(), 0.125, torch.zeros(65, Hkv, 1, dtype=torch.int32, device="cuda"),
+                 torch.ones(65, Hkv, dtype=torch.int32, device="cuda"), num_splits=4,
+                 seq_lens=torch.full((65,), 10, dtype=torch.int32, device="cuda"), list_partition=1)
+
+
 def test_ragged_rejects(gpu):
     q, k, v = _layer([10, 20], 8, 2, 64, 64, seed=1)
     sl = torch.tensor([10, 20], dtype=torch.int32, device="cuda")
