@@ -628,10 +628,15 @@ __device__ void merge_fit(const AttnP& p, int plain, int64_t hq, int slice, int 
   merge_body<D, U, WITH_V>(p, plain, hq, slice, Sv);
 }
 
+// Workgroup (x, y) of the (B Hq, D / 32) grid takes item xcd_remap(x + y B Hq) in (query head, dim
+// slice) order, so a KV head's merges run on the XCD that ran its splits (work_coords' mapping),
+// whose L2 still holds the partials just written (config 2's op 26.87 -> 26.52 us).
 template <int D, int U, bool WITH_V>
 __global__ void __launch_bounds__(256) combine_kernel(const AttnP p, int plain) {
-  const int64_t hq = blockIdx.x;
-  merge_fit<D, U, WITH_V>(p, plain, hq, blockIdx.y, merge_count(p, hq));
+  const int nsl = gridDim.y;
+  const int m = xcd_remap(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x * nsl);
+  const int64_t hq = m / nsl;
+  merge_fit<D, U, WITH_V>(p, plain, hq, m % nsl, merge_count(p, hq));
 }
 
 // merge_body with U chosen at run time from the head's partial count.
