@@ -117,9 +117,10 @@ def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = Fal
     bf16 (None with load_v=False), lse [B, Hq] fp32, num_splits, and as asked blk_max / blk_sum
     [B, Hq, nb] fp32, out_f32, p (fp16 [B, Hq, nb*64] = exp(s - blk_max)).
     Not in the reference: seq_lens (int32 [B] on the device) makes a ragged batch over views of
-    capacity T, the split budget shared by the batch; block_table (int32 [B, >= ceil(T / 64)]) with T
-    makes k, v page pools [num_pages, Hkv, 64, D]; merge=False (with load_v=False) skips the split
-    merge, leaving lse None."""
+    capacity T, the split budget shared by the batch (with a plan, up to 512 lists, the lists of all
+    KV heads cut by one chunk length: kvskip_attn_args.list_partition); block_table (int32 [B, >=
+    ceil(T / 64)]) with T makes k, v page pools [num_pages, Hkv, 64, D]; merge=False (with
+    load_v=False) skips the split merge, leaving lse None."""
     q = _as_bhd(q)
     B, Hkv = q.shape[0], k.shape[1]
     tokens = k.shape[2] if block_table is None else int(T)
@@ -129,9 +130,10 @@ def decode(q, k, v, scale: float, *, plan: Plan | None = None, stats: bool = Fal
         num_splits = (ragged_splits(B, Hkv, items, G=q.shape[1] // Hkv) if seq_lens is not None
                       else num_splits_for(B * Hkv, items))
     lists = (None, None) if plan is None else (plan.block_idx, plan.block_cnt)
+    lp = int(plan is not None and seq_lens is not None and B > 1 and B * Hkv <= 512)
     out, lse, bmax, bsum, o32, p = ext().decode(q, k, v, float(scale), *lists, stats, load_v, int(num_splits),
                                                 int(stages), out_f32, write_p, seq_lens, **_paged(block_table, T),
-                                                merge=merge)
+                                                merge=merge, list_partition=lp)
     res = {"out": out, "lse": lse, "num_splits": num_splits}
     extra = {"blk_max": bmax, "blk_sum": bsum} if stats else {}
     if out_f32:

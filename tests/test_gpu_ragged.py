@@ -111,6 +111,11 @@ def test_ragged_masked_stats(gpu, S, lp):
                           seq_lens=sl, phase=phase, list_partition=lp)
         for key in ("out", "lse", "blk_max", "blk_sum"):
             assert torch.equal(two[key], bufs[key]), key
+        # the front-end op with a plan over a ragged batch cuts all lists together (its own split count)
+        r = K.decode(q.cuda(), k.cuda(), v.cuda(), scale, plan=K.Plan(bi.cuda(), bc.cuda(), int(bc.max()), nb),
+                     stats=True, seq_lens=sl)
+        assert torch.equal(r["blk_max"].flatten(), bufs["blk_max"]) and torch.equal(r["blk_sum"].flatten(), bufs["blk_sum"])
+        assert (r["out"].float() - bufs["out"].float()).abs().max().item() <= 2e-2
     bmax = bufs["blk_max"].view(B, Hq, nb).cpu()
     bsum = bufs["blk_sum"].view(B, Hq, nb).cpu()
     out = bufs["out"].float().cpu()
