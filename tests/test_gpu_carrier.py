@@ -102,13 +102,14 @@ def test_decode_splits_update_rejects_group_mismatch(gpu):
         E.decode_splits_update(q2, k, k, 0.125, bufs, bi, bc, 2, u)
 
 
+@pytest.mark.parametrize("B", [3, 24])
 @pytest.mark.parametrize("carry", [False, True])
-def test_batch_balanced_partition(gpu, carry):
-    """B 3 x 8 KV heads (24 lists, over the balanced pass's 16): the planner passes the lengths (all
-    T) as seq_lens, so the ragged partition cuts each KV head's lists over the batch. Against the
-    per-(sequence, head) split (batch_balance=False): identical state on every step, outputs to
-    float rounding."""
-    layers, B, Hkv, G, D, T0, steps = 2, 3, 8, 4, 64, 1900, 6
+def test_batch_balanced_partition(gpu, carry, B):
+    """B 3 and 24 x 8 KV heads (24 and 192 lists, over the balanced pass's 16): the planner passes
+    the lengths (all T) as seq_lens, so the ragged pass cuts the lists of all KV heads together (B 24:
+    with twice the chunk slots). Against the per-(sequence, head) split (batch_balance=False):
+    identical state on every step, outputs to float rounding."""
+    layers, Hkv, G, D, T0, steps = 2, 8, 4, 64, 1900, 6
     run = W.planner_run(layers=layers, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, T0=T0, steps=steps, seed=77)
     ks = [k.cuda() for k in run.k]
     vs = [v.cuda() for v in run.v]
