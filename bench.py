@@ -131,8 +131,8 @@ def main():
     ap.add_argument("--pmc-target", action="store_true",
                     help="profiling target only: 20 dense config-2 decodes + copy kernels of known size, then exit")
     ap.add_argument("--pmc-paths", action="store_true",
-                    help="profiling target only: config 2 masked + stats, the peaked two-pass V-skip op, a short "
-                         "config-4 planner loop, + copy kernels of known size, then exit")
+                    help="profiling target only: config 2 masked + stats, the peaked two-pass V-skip op, short "
+                         "config-4 and B 32 / 64k planner loops, + copy kernels of known size, then exit")
     ap.add_argument("--planner-only", action="store_true",
                     help="profiling target only: the config-4 planner loop (--planner-layers x --planner-steps), "
                          "its result as one JSON line, then exit")
@@ -577,8 +577,9 @@ def pmc_target(dense, dev):
 def pmc_paths(q, ks, vs, scale, bi, bc, dev):
     """Profiling target for rocprofv3 --pmc beyond the dense pass: 20 config-2 masked + statistics
     ops (the bench's list), 20 two-pass V-skip ops on the peaked layer (pass 1, select, pass 2),
-    a config-4 planner loop of 4 layers x 12 steps (updates carried), then the known-size copy and
-    read of pmc_target."""
+    a config-4 planner loop of 4 layers x 12 steps (updates carried), a B 32 / 64k stable-query loop
+    of 2 layers x 6 steps (each planned pass's listed blocks printed, to price it), then the
+    known-size copy and read of pmc_target."""
     import torch
 
     from kvskip_amd import ext as E
@@ -613,6 +614,31 @@ def pmc_paths(q, ks, vs, scale, bi, bc, dev):
     carrier.flush()
     torch.cuda.synchronize()
     del run, pls
+    # B 32 at 64k with stable queries (the planner_b32_64k_stable leg's shape), 2 planned layers x 6
+    # steps, updates carried: plan (scores, decision), the masked pass over all KV heads' lists cut
+    # together with the previous layer's update in it (1025 blocks: 24 slots per lane), the merge
+    layers, steps, B32, T32 = 2, 6, 32, 65536
+    run = W.planner_run(layers=layers, B=B32, T0=T32, steps=steps, seed=4, device=dev)
+    qps = [W.QueryProcess(run, l, noise=0.25, revert=True, p_jump=0.003) for l in range(layers)]
+    ids = run.ids.to(dev)
+    NBC = math.ceil((T32 + 1) / 64) + 64
+    idx = torch.zeros(B32, NBC, dtype=torch.uint8, device=dev)
+    carrier = UpdateCarrier()
+    pls = [FusedPlanner(pol, count=False, carrier=carrier) for _ in range(layers)]
+    b32_lists = []  # (step, layer, blocks listed by its planned pass), in launch order
+    for t in range(steps):
+        E.token_index(ids, T32 + t + 1, NBC, out=idx)   # as the bench's loop: the index found beforehand
+        for l in range(layers):
+            k, v = run.k[l][:, :, :T32 + t + 1], run.v[l][:, :, :T32 + t + 1]
+            ql = qps[l].next().to(dev)
+            if t == 0:
+                pls[l].first(ql, k, v, run.scale)
+            else:
+                pls[l].step(ql, k, v, run.scale, idx=idx)
+                b32_lists.append((t, l, int(pls[l].state["block_cnt"].sum())))
+    carrier.flush()
+    torch.cuda.synchronize()
+    del run, pls
     a = torch.ones(128 << 20, dtype=torch.bfloat16, device=dev)
     b = torch.empty_like(a)
     o = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -621,7 +647,8 @@ def pmc_paths(q, ks, vs, scale, bi, bc, dev):
     for _ in range(5):
         E.read_bw(a, o, 1024)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_paths": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2}), flush=True)
+    print(json.dumps({"pmc_paths": "done", "copy_bytes": a.numel() * 2, "read_bytes": a.numel() * 2,
+                      "b32_pass_blocks": b32_lists, "b32_block_bytes": 2 * 64 * 128 * 2}), flush=True)
 
 
 def bench_planner(dev, layers=32, T0=32768, steps=128, chunk=16, noise=0.25, revert=False, tag="cfg4", B=1, Hq=32,
