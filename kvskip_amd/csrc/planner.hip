@@ -286,7 +286,11 @@ __device__ __forceinline__ void decide_if_last(const kvskip_plan_args& p, int b,
 template <int D, int G, bool FUSED>
 __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args p) {
   constexpr int DL = D / 16, DW = DL / 4, SP = part_stride(G);
+  // One field of each 64-byte line of the argument block, fetched together up front: read where
+  // the code first needs them, the fields' lines came in one after another, a scalar-load wait
+  // for each before the pass's loads were issued.
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, C = gridDim.x;
+  asm volatile("" ::"s"(p.q), "s"(p.lse_ref), "s"(p.est), "s"(p.part), "s"(p.ids), "s"(C));
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
   const int Tb = seq_T(p.seq_lens, b, p.T);
   const int nb = (Tb + BLK - 1) / BLK;
@@ -322,17 +326,19 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   __shared__ uint32_t sMask[WW];
   const int base = c * WCB + wave * (4 * WU);  // this wavefront's blocks: base + 4 u + rs
 
-  // Token index (ids given; kvskip_token_index's rule): lane l checks the 8 tokens 8 (l % 8) + [0, 8)
-  // of block base + l / 8, so the wavefront finds its own 8 blocks (bit i: block base + i); the
-  // workgroups of KV head 0 also write them to idx_out for the update. The ids are loaded here and
-  // compared after the pass's other loads are issued (the comparison waits for them).
+  // Token index (ids given; kvskip_token_index's rule): the wavefront's BPW blocks, LPB lanes per
+  // block, lane l checking the TPL tokens TPL (l % LPB) + [0, TPL) of block base + l / LPB (bit i
+  // of the result: block base + i); the workgroups of KV head 0 also write them to idx_out for the
+  // update. The ids are loaded here and compared after the pass's other loads are issued (the
+  // comparison waits for them).
+  constexpr int BPW = 4 * WU, LPB = WAVE / BPW, TPL = BLK / LPB;
   const int32_t* ids = p.ids != nullptr ? p.ids + b * p.ids_sb : nullptr;
-  const int ix_blk = base + (lane >> 3), ix_j0 = ix_blk * BLK + 8 * (lane & 7);
-  int32_t ix_cur = 0, ix_x[9];  // the current token; tokens j0 - 1 .. j0 + 7 (clamped loads)
+  const int ix_blk = base + lane / LPB, ix_j0 = ix_blk * BLK + TPL * (lane % LPB);
+  int32_t ix_cur = 0, ix_x[TPL + 1];  // the current token; tokens j0 - 1 .. j0 + TPL - 1 (clamped loads)
   if (ids != nullptr) {
     ix_cur = ids[Tb - 1];
 #pragma unroll
-    for (int e = 0; e < 9; ++e) ix_x[e] = ids[min(max(ix_j0 - 1 + e, 0), Tb - 1)];
+    for (int e = 0; e <= TPL; ++e) ix_x[e] = ids[min(max(ix_j0 - 1 + e, 0), Tb - 1)];
   }
 
   // Every load is issued without waiting for the flags (an index head's extra loads are unused).
@@ -390,16 +396,17 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   if (ids != nullptr) {
     bool hit = false;
 #pragma unroll
-    for (int e = 1; e < 9; ++e) {
+    for (int e = 1; e <= TPL; ++e) {
       const int j = ix_j0 + e - 1;
       hit |= (j < Tb - 1 && ix_x[e] == ix_cur) || (j < Tb && j >= 1 && ix_x[e - 1] == ix_cur);
     }
     const uint64_t bal = __ballot(hit);
+    constexpr uint64_t LM = LPB == WAVE ? ~uint64_t(0) : (uint64_t(1) << LPB) - 1;
     uint32_t ixw = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ixw |= ((bal >> (8 * i)) & 0xffu) != 0 ? 1u << i : 0u;
-    if (h == 0 && (lane & 7) == 0 && ix_blk < nb)
-      p.idx_out[static_cast<int64_t>(b) * p.NBC + ix_blk] = (ixw >> (lane >> 3)) & 1;
+    for (int i = 0; i < BPW; ++i) ixw |= ((bal >> (LPB * i)) & LM) != 0 ? 1u << i : 0u;
+    if (h == 0 && lane % LPB == 0 && ix_blk < nb)
+      p.idx_out[static_cast<int64_t>(b) * p.NBC + ix_blk] = (ixw >> (lane / LPB)) & 1;
 #pragma unroll
     for (int u = 0; u < WU; ++u) ib[u] = (ixw >> (4 * u + rs)) & 1;
   }
@@ -466,7 +473,7 @@ __global__ void __launch_bounds__(WNT) plan_scores_kernel(const kvskip_plan_args
   if (tid == 0) {
     uint32_t mk = 0;
 #pragma unroll
-    for (int w = 0; w < WW; ++w) mk |= sMask[w] << (8 * w);
+    for (int w = 0; w < WW; ++w) mk |= sMask[w] << (BPW * w);
     st_part<FUSED>(part + 2 * G, __uint_as_float(mk));
   }
   if constexpr (FUSED) decide_if_last<G>(p, b, h, C);
