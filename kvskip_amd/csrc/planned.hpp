@@ -14,6 +14,7 @@ namespace {
 template <int D, int G, int R, bool PAGED, bool RAG = false>
 __global__ void __launch_bounds__(NT, 2) planned_split_kernel(const AttnP a, const kvskip_plan_args pa,
                                                               const kvskip_update_args u) {
+  prefetch_planned_args<(R > 0)>();  // the update's arguments only where it is carried
   const int n_update = R > 0 ? u.B * u.Hkv : 0;
   const int i = blockIdx.x;
   if constexpr (R > 0) {
