@@ -155,12 +155,19 @@ __device__ __forceinline__ int ragged_chunks(const AttnP& p, int b, int h, bool 
 }
 
 // Partition over all B * Hkv lists of a masked ragged pass (p.list_partition = 1): chunks of one
-// length C = max(ceil(sum / (S Hkv)), ceil(most / S)) list entries (S = num_splits: the partial
-// slots of a list), numbered list by list (l = b Hkv + h), so a KV head whose lists hold more
-// entries (a refreshing sequence) gets more workgroups instead of longer chunks; the grid's
-// (S + B) Hkv slots hold every chunk (sum / C <= S Hkv, plus one partial chunk per list). Lane j
-// holds lists j + 64 r in nv. Returns C, uniform.
+// length C list entries, numbered list by list (l = b Hkv + h), so a KV head whose lists hold more
+// entries (a refreshing sequence) gets more workgroups instead of longer chunks. C0 = max(ceil(sum /
+// (S Hkv)), ceil(most / S)) (S = num_splits: the partial slots of a list) fits the grid's (S + B) Hkv
+// slots (sum / C0 <= S Hkv, plus at most one partial chunk per list). Where the whole grid is
+// resident (at most RESIDENT_SLOTS workgroups: two per CU) and chunks are long (C0 >= 32 entries),
+// C is the smallest length whose chunks (sum over the lists of ceil(n_l / C)) still fit the grid,
+// found by bisection: set for S Hkv slots, C0 left two full chunks on most CUs and partial ones on
+// the rest (per layer-step with carried updates, config 5 131.1 -> 125.0 us, B 8 179.1 -> 173.4);
+// with short chunks or a queued grid the shorter chunks' fixed costs win (bisected for every grid:
+// B 8 with stable queries +0.4 us, B 32 at 64k +3.5 us). Lane j holds lists j + 64 r in nv.
+// Returns C, uniform.
 constexpr int NRG = MAX_GLOBAL_LISTS / WAVE;
+constexpr int RESIDENT_SLOTS = 512;
 
 __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) {
   const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
@@ -174,8 +181,24 @@ __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) 
   }
   tot = wave_sum_int(tot);
   most = static_cast<int>(wave_max(static_cast<float>(most)));  // exact: counts <= 2^24
-  const int S = p.num_splits;
-  return __builtin_amdgcn_readfirstlane(max(1, max((tot + S * p.Hkv - 1) / (S * p.Hkv), (most + S - 1) / S)));
+  const int S = p.num_splits, slots = (S + p.B) * p.Hkv;
+  const int c_min = max(1, (most + S - 1) / S);
+  int hi = __builtin_amdgcn_readfirstlane(max(c_min, (tot + S * p.Hkv - 1) / (S * p.Hkv)));
+  if (slots > RESIDENT_SLOTS || hi < 32) return hi;
+  int lo = __builtin_amdgcn_readfirstlane(max(c_min, (tot + slots - 1) / slots));
+  while (lo < hi) {  // uniform: the chunk count does not grow with C
+    const int mid = (lo + hi) >> 1;
+    int n = 0;
+#pragma unroll
+    for (int r = 0; r < NRG; ++r)
+      if (r * WAVE < nl) n += (nv[r] + mid - 1) / mid;
+    n = __builtin_amdgcn_readfirstlane(wave_sum_int(n));
+    if (n <= slots)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
 }
 
 // Chunk number `it` of the partition over all lists: its list (b, h; b = -1 past the last chunk),
