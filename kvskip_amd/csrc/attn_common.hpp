@@ -98,28 +98,74 @@ __device__ __forceinline__ int ragged_items(const AttnP& p, int b, int h, bool m
   return (seq_len(p, b) + BLK - 1) / BLK;
 }
 
-// Ragged partition of KV head h, uniform over the wavefront: chunks of C = ceil(sum_b items_b / S)
-// items, numbered sequence by sequence (at most S + B chunks per head). For chunk number `it`:
-// b (-1 past the head's last chunk), the chunk within b and b's item count. Returns C.
-__device__ int ragged_lookup(const AttnP& p, int h, int it, bool masked, int& b, int& chunk, int& items) {
-  constexpr int NR = MAX_RAGGED_B / WAVE;
-  const int lane = threadIdx.x % WAVE;
-  int nv[NR];
-  int tot = 0;
+// Chunk lengths of the ragged partitions. A length C0 set for S slots of a (S + B)-slot grid
+// (S = num_splits) leaves the grid's last B slots to the sequences' (or lists') partial chunks, so
+// where the whole grid is resident (at most RESIDENT_SLOTS workgroups: two per CU) most CUs hold
+// full chunks and the rest partial ones. There, with long chunks (C0 >= 32 items), C is the smallest
+// length whose chunks (sum of ceil(n / C) over the lanes' counts nv) still fit the slots, found by
+// bisection between lo and C0 (C0 fits), and at least lo; with short chunks or a queued grid the
+// shorter chunks' fixed costs win. Config 5's dense pass (per-head partition, one workgroup per CU):
+// 121.0 -> 113.2 us per layer-step. Uniform.
+constexpr int RESIDENT_SLOTS = 512;
+
+template <int NR>
+__device__ __forceinline__ int fit_chunk_len(const AttnP& p, const int (&nv)[NR], int n_lists, int lo, int c0,
+                                             int slots) {
+  if ((p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS || c0 < 32) return c0;
+  int hi = c0;
+  lo = __builtin_amdgcn_readfirstlane(min(lo, c0));
+  while (lo < hi) {  // the chunk count does not grow with C
+    const int mid = (lo + hi) >> 1;
+    int n = 0;
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
+    for (int r = 0; r < NR; ++r)
+      if (r * WAVE < n_lists) n += (nv[r] + mid - 1) / mid;
+    n = __builtin_amdgcn_readfirstlane(wave_sum_int(n));
+    if (n <= slots)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
+}
+
+// Ragged partition of KV head h (per head; list_partition 0): the items of its B sequences (blocks,
+// or list entries when masked) in chunks of one length C, numbered sequence by sequence, at most
+// S + B chunks per head (C0 = ceil(sum_b items_b / S); bisected as fit_chunk_len says, at least
+// ceil(most / S) so that no sequence has more than S chunks). Lane j holds sequences j + 64 r in nv.
+// Returns C, uniform.
+constexpr int NRB = MAX_RAGGED_B / WAVE;
+
+__device__ __forceinline__ int ragged_chunk_len(const AttnP& p, int h, bool masked, int (&nv)[NRB]) {
+  const int lane = threadIdx.x % WAVE;
+  int tot = 0, most = 0;
+#pragma unroll
+  for (int r = 0; r < NRB; ++r) {
     const int bb = r * WAVE + lane;
     nv[r] = bb < p.B ? ragged_items(p, bb, h, masked) : 0;
     tot += nv[r];
+    most = max(most, nv[r]);
   }
   tot = wave_sum_int(tot);
-  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  most = static_cast<int>(wave_max(static_cast<float>(most)));  // exact: counts <= 2^24
+  const int S = p.num_splits;
+  const int c0 = __builtin_amdgcn_readfirstlane(max(1, (tot + S - 1) / S));
+  const int lo = max(max(1, (most + S - 1) / S), (tot + S + p.B - 1) / (S + p.B));
+  return fit_chunk_len(p, nv, p.B, lo, c0, S + p.B);
+}
+
+// Chunk number `it` of KV head h's ragged partition, uniform over the wavefront: b (-1 past the
+// head's last chunk), the chunk within b and b's item count. Returns C.
+__device__ int ragged_lookup(const AttnP& p, int h, int it, bool masked, int& b, int& chunk, int& items) {
+  const int lane = threadIdx.x % WAVE;
+  int nv[NRB];
+  const int C = ragged_chunk_len(p, h, masked, nv);
   b = -1;
   chunk = 0;
   items = 0;
   int base = 0;
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
+  for (int r = 0; r < NRB; ++r) {
     if (r * WAVE >= p.B) break;
     const int ch = (nv[r] + C - 1) / C;
     const int incl = wave_incl_scan(ch);
@@ -136,38 +182,24 @@ __device__ int ragged_lookup(const AttnP& p, int h, int it, bool masked, int& b,
   b = __builtin_amdgcn_readfirstlane(b);  // uniform: scalar registers for the addressing that follows
   chunk = __builtin_amdgcn_readfirstlane(chunk);
   items = __builtin_amdgcn_readfirstlane(items);
-  return __builtin_amdgcn_readfirstlane(C);
+  return C;
 }
 
 // Chunks (split partials) of (b, KV head h) under the ragged partition.
 __device__ __forceinline__ int ragged_chunks(const AttnP& p, int b, int h, bool masked) {
-  constexpr int NR = MAX_RAGGED_B / WAVE;
-  const int lane = threadIdx.x % WAVE;
-  int tot = 0;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int bb = r * WAVE + lane;
-    tot += bb < p.B ? ragged_items(p, bb, h, masked) : 0;
-  }
-  tot = wave_sum_int(tot);
-  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  int nv[NRB];
+  const int C = ragged_chunk_len(p, h, masked, nv);
   return (ragged_items(p, b, h, masked) + C - 1) / C;
 }
 
 // Partition over all B * Hkv lists of a masked ragged pass (p.list_partition = 1): chunks of one
 // length C list entries, numbered list by list (l = b Hkv + h), so a KV head whose lists hold more
 // entries (a refreshing sequence) gets more workgroups instead of longer chunks. C0 = max(ceil(sum /
-// (S Hkv)), ceil(most / S)) (S = num_splits: the partial slots of a list) fits the grid's (S + B) Hkv
-// slots (sum / C0 <= S Hkv, plus at most one partial chunk per list). Where the whole grid is
-// resident (at most RESIDENT_SLOTS workgroups: two per CU) and chunks are long (C0 >= 32 entries),
-// C is the smallest length whose chunks (sum over the lists of ceil(n_l / C)) still fit the grid,
-// found by bisection: set for S Hkv slots, C0 left two full chunks on most CUs and partial ones on
-// the rest (per layer-step with carried updates, config 5 131.1 -> 125.0 us, B 8 179.1 -> 173.4);
-// with short chunks or a queued grid the shorter chunks' fixed costs win (bisected for every grid:
-// B 8 with stable queries +0.4 us, B 32 at 64k +3.5 us). Lane j holds lists j + 64 r in nv.
-// Returns C, uniform.
+// (S Hkv)), ceil(most / S)) fits the grid's (S + B) Hkv slots (sum / C0 <= S Hkv, plus at most one
+// partial chunk per list), bisected as fit_chunk_len says (per layer-step with carried updates,
+// config 5 131.1 -> 125.0 us, B 8 179.1 -> 173.4; bisected for every grid, B 8 with stable queries
+// +0.4 us and B 32 at 64k +3.5 us). Lane j holds lists j + 64 r in nv. Returns C, uniform.
 constexpr int NRG = MAX_GLOBAL_LISTS / WAVE;
-constexpr int RESIDENT_SLOTS = 512;
 
 __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) {
   const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
@@ -183,22 +215,8 @@ __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) 
   most = static_cast<int>(wave_max(static_cast<float>(most)));  // exact: counts <= 2^24
   const int S = p.num_splits, slots = (S + p.B) * p.Hkv;
   const int c_min = max(1, (most + S - 1) / S);
-  int hi = __builtin_amdgcn_readfirstlane(max(c_min, (tot + S * p.Hkv - 1) / (S * p.Hkv)));
-  if (slots > RESIDENT_SLOTS || hi < 32) return hi;
-  int lo = __builtin_amdgcn_readfirstlane(max(c_min, (tot + slots - 1) / slots));
-  while (lo < hi) {  // uniform: the chunk count does not grow with C
-    const int mid = (lo + hi) >> 1;
-    int n = 0;
-#pragma unroll
-    for (int r = 0; r < NRG; ++r)
-      if (r * WAVE < nl) n += (nv[r] + mid - 1) / mid;
-    n = __builtin_amdgcn_readfirstlane(wave_sum_int(n));
-    if (n <= slots)
-      hi = mid;
-    else
-      lo = mid + 1;
-  }
-  return lo;
+  const int c0 = __builtin_amdgcn_readfirstlane(max(c_min, (tot + S * p.Hkv - 1) / (S * p.Hkv)));
+  return fit_chunk_len(p, nv, nl, max(c_min, (tot + slots - 1) / slots), c0, slots);
 }
 
 // Chunk number `it` of the partition over all lists: its list (b, h; b = -1 past the last chunk),

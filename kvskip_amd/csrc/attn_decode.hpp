@@ -175,7 +175,7 @@ __device__ bool planned_balanced(const AttnP& p, const kvskip_plan_args& pa, int
 // A planned pass over a ragged batch (seq_lens, B <= BAL_MAX_LISTS): workgroup `it` of KV head h
 // decides the head's B lists (b, h) in its prologue (wavefront w: b = w + NWAVE j; the head's
 // workgroup 0 stores trig and est) and takes chunk `it` of the ragged partition over their lengths
-// (a refreshing list: the sequence's blocks; C = ceil(sum / num_splits) items per chunk, numbered
+// (a refreshing list: the sequence's blocks; chunks of ragged_chunk_len's length, numbered
 // sequence by sequence, as ragged_lookup does over the block counts this pass writes, so that the
 // ragged merge finds the same chunks). Outputs as planned_balanced_nh's, plus the sequence's length
 // Tb and blocks nbb; the head's workgroup 0 also writes the statistics and the zero count of a list
@@ -210,10 +210,16 @@ __device__ bool planned_ragged_nh(const AttnP& p, const kvskip_plan_args& pa, in
     }
   }
   __syncthreads();
-  // the partition, lane q holding list q (every wavefront computes the same)
+  // the partition, lane q holding list q (every wavefront computes the same; ragged_chunk_len's
+  // length over these counts, which the list writers leave in block_cnt for the merge)
   const int cq = lane < B ? sCnt[lane] : 0;
   const int tot = wave_sum_int(cq);
-  const int C = max(1, (tot + p.num_splits - 1) / p.num_splits);
+  const int most = static_cast<int>(wave_max(static_cast<float>(cq)));  // exact: counts <= 2^24
+  const int S = p.num_splits;
+  int nvq[NRB] = {};
+  nvq[0] = cq;
+  const int C = fit_chunk_len(p, nvq, B, max(max(1, (most + S - 1) / S), (tot + S + B - 1) / (S + B)),
+                              __builtin_amdgcn_readfirstlane(max(1, (tot + S - 1) / S)), S + B);
   const int ch = (cq + C - 1) / C;  // none for an empty list
   const int incl = wave_incl_scan(ch);
   if (it == 0) {  // the head's lists with nothing to read: statistics (-inf, 0) and count 0
