@@ -63,17 +63,22 @@ def num_splits_for(bh: int, n_tiles: int, sms: int | None = None, max_splits: in
     return best
 
 
-def ragged_splits(B: int, Hkv: int, nb_max: int, sms: int | None = None, G: int = 4) -> int:
+def ragged_splits(B: int, Hkv: int, nb_max: int, sms: int | None = None, G: int = 4, carry: bool = False) -> int:
     """Split budget per KV head for a ragged batch (seq_lens), at least 8 blocks per chunk at full
     length, in 2..256. Groups of up to 4 query heads: 7/8 of two workgroups per CU over all KV heads,
     the last eighth left to the sequences' partial last chunks (measured, 8 KV heads: B 8 planner
     loop 183.3 -> 178.5 us per layer-step at 64 -> 56 splits, B 32 at 64k 652.9 -> 630.0; 48 and 40
     were slower). Larger groups (more arithmetic per block): the grid's S + B chunk slots per KV head
-    fill one workgroup per CU (G 7, B 16 ragged dense 133.5 -> 121.1 us; that fit for G 4 cost B 32 at
-    64k 11%, since its B spare slots per head mostly idle)."""
+    fill two workgroups per CU (config 5 dense 113.6 -> 112.2 us, its planner loop with the update
+    beside the merge 144.0 -> 137.7), or one per CU for a pass that carries another layer's update
+    (`carry`: its G-wavefront update workgroups then share the CUs; config 5's loop 125.2 at one per
+    CU, 126.9 at two, 132.2 at two less the update's workgroups)."""
     cus = sms or num_sms()
     Hkv = max(Hkv, 1)
-    per_head = cus * 2 // Hkv - cus // (4 * Hkv) if G <= 4 else cus // Hkv - B
+    if G <= 4:
+        per_head = cus * 2 // Hkv - cus // (4 * Hkv)
+    else:
+        per_head = (cus if carry else cus * 2) // Hkv - B
     return max(2, min(256, per_head, max(1, B * nb_max // 8)))
 
 

@@ -218,8 +218,10 @@ class FusedPlanner:
         split) and the [B, Hq, nb] statistics views."""
         B, Hq, D = q.shape
         Hkv = k.shape[1]
+        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         # one sequence (its length in device memory) is split as an unragged batch
-        S = K.num_splits_for(B * Hkv, nb) if seq_lens is None or B == 1 else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv)
+        S = (K.num_splits_for(B * Hkv, nb) if seq_lens is None or B == 1
+             else K.ragged_splits(B, Hkv, nb, G=Hq // Hkv, carry=carried is not None))
         if seq_lens is not None and B > 16 and Hq // Hkv <= 4:
             # many lists: twice the chunk slots, so that the queued workgroups even out the chunks'
             # lengths (B 32 at 64k, all lists cut together: 629 -> 607 us per layer-step; 168 slots
@@ -233,7 +235,12 @@ class FusedPlanner:
             # given a second full chunk would double the critical path); the same with and without
             # a carried update, so both cut the lists alike. S becomes the partial slots per head.
             budget, S = max(S * B * Hkv - 2 * B * Hkv, B * Hkv), min(2 * S, 256)
-        n_st, n_part = B * Hq * self.NBC, B * Hq * S * D
+        S_buf = S
+        if seq_lens is not None and B > 1 and Hq // Hkv > 4:
+            # the budget differs with and without a carried update: partials room for the larger,
+            # so that a step allocates nothing either way
+            S_buf = max(S, K.ragged_splits(B, Hkv, nb, G=Hq // Hkv))
+        n_st, n_part = B * Hq * self.NBC, B * Hq * S_buf * D
         b = self.bufs
         if b is None or b["blk_max"].numel() < n_st or b["part_acc"].numel() < n_part or b["out"].shape != q.shape:
             dev = q.device
@@ -241,12 +248,11 @@ class FusedPlanner:
             b = self.bufs = dict(out=torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev),
                                  lse=torch.empty(B, Hq, **f32), blk_max=torch.empty(n_st, **f32),
                                  blk_sum=torch.empty(n_st, **f32), part_acc=torch.empty(n_part, **f32),
-                                 part_ml=torch.empty(B * Hq * S * 2, **f32))
+                                 part_ml=torch.empty(B * Hq * S_buf * 2, **f32))
         s = self.state
         self._S = S
         self._lp = lp = int(self._pargs is None and self.global_partition and seq_lens is not None
                             and 1 < B <= GLOBAL_PARTITION_MAX_B and B * Hkv <= GLOBAL_PARTITION_MAX_LISTS)
-        carried = self.carrier.take(self, Hq // Hkv) if self.carrier is not None else None
         if self._pargs is not None:
             self._pargs.pass_budget = budget
             E.decode_splits_planned(q, k, v, scale, b, self._pargs, S, carried, seq_lens, **pg)
