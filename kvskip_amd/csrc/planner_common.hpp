@@ -54,9 +54,10 @@ constexpr int MAX_NB = 4096;   // planner block capacity: update holds a head's 
 // ceil(nb / 32) workgroups (4 wavefronts, 8 block rows each), each publishing per query head the
 // (m, s) log-sum-exp of its unattended blocks' estimates and the 32-bit mask of its attended
 // blocks; the decision (plan_decide, or the prologue of the masked pass) merges them, decides and
-// compacts from the masks. The kernel boundary publishes the partials (a last-arriving-workgroup
-// ticket would need an agent-scope release per workgroup, an L2 write-back each, which costs more
-// than the launch).
+// compacts from the masks. The kernel boundary publishes the partials; in the one-launch plan
+// (kvskip_plan_args.ticket) agent-scope stores and a per-head ticket do, and each head's last
+// scores workgroup decides (an agent-scope release per workgroup instead, an L2 write-back each,
+// cost more than the launch).
 constexpr int WW = 4;                // wavefronts per workgroup
 constexpr int WU = 2;                // row groups (4 rows) per wavefront
 constexpr int WCB = WW * WU * 4;     // 32 blocks per workgroup
