@@ -220,19 +220,24 @@ __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) 
 }
 
 // Chunk number `it` of the partition over all lists: its list (b, h; b = -1 past the last chunk),
-// the chunk within the list and the list's entry count. Returns C. Uniform results.
+// the chunk within the list and the list's entry count. Returns C. Uniform results. A grid longer
+// than the resident slots (queued workgroups start as others end) takes the lists' full chunks
+// first and their partial last chunks after them, so that it ends on its shortest chunks (B 32 at
+// 64k, stable queries: 592.4 -> 579.8 us per layer-step); a resident grid takes them list by list.
 __device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk, int& items) {
-  const int lane = threadIdx.x % WAVE;
+  const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
   int nv[NRG];
   const int C = global_chunk_len(p, nv);
+  const bool queued = (p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS;
   int l_sel = -1;
   chunk = 0;
   items = 0;
   int base = 0;
+  // round one: every chunk of a list (resident grid) or its full chunks (queued grid)
 #pragma unroll
   for (int r = 0; r < NRG; ++r) {
-    if (r * WAVE >= p.B * p.Hkv) break;
-    const int ch = (nv[r] + C - 1) / C;
+    if (r * WAVE >= nl) break;
+    const int ch = queued ? nv[r] / C : (nv[r] + C - 1) / C;
     const int incl = wave_incl_scan(ch);
     const int excl = base + incl - ch;
     const uint64_t hit = __ballot(ch > 0 && it >= excl && it < excl + ch);
@@ -243,6 +248,22 @@ __device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk,
       items = __shfl(nv[r], j, WAVE);
     }
     base += __shfl(incl, WAVE - 1, WAVE);
+  }
+  if (queued && __builtin_amdgcn_readfirstlane(l_sel) < 0) {  // round two: the partial last chunks
+#pragma unroll
+    for (int r = 0; r < NRG; ++r) {
+      if (r * WAVE >= nl) break;
+      const int part = nv[r] % C != 0 ? 1 : 0;
+      const int incl = wave_incl_scan(part);
+      const uint64_t hit = __ballot(part != 0 && it == base + incl - 1);
+      if (hit != 0) {
+        const int j = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+        l_sel = r * WAVE + j;
+        items = __shfl(nv[r], j, WAVE);
+        chunk = items / C;
+      }
+      base += __shfl(incl, WAVE - 1, WAVE);
+    }
   }
   l_sel = __builtin_amdgcn_readfirstlane(l_sel);
   b = l_sel >= 0 ? l_sel / p.Hkv : -1;
