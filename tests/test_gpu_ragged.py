@@ -184,6 +184,73 @@ def test_list_partition_all_lists_at_its_bound(gpu):
                  seq_lens=torch.full((65,), 10, dtype=torch.int32, device="cuda"), list_partition=1)
 
 
+@pytest.mark.parametrize("S", [56, 8])
+def test_list_partition_queued_grid(gpu, S):
+    """list_partition 1 over a grid longer than the resident 512 workgroups (S 56: (56 + 16) x 8 =
+    576), whose chunk numbering takes every list's full chunks first and the partial last chunks
+    after them, and over a resident one (S 8) with the same lists: lists empty, shorter than one
+    chunk, exact multiples of the chunk length and with a partial last chunk, in both rounds of 64
+    lists. Against the per-head cut and the oracle: bit-identical statistics, outputs to the split
+    merge's rounding, each sequence's output and log-sum-exp within the tolerances."""
+    B, Hkv, G, D, cap = 16, 8, 2, 64, 4096
+    Hq = Hkv * G
+    nb = cap // 64
+    g = torch.Generator().manual_seed(91)
+    lens = [cap if b % 3 else int(x) for b, x in enumerate(torch.randint(2600, cap, (B,), generator=g))]
+    q, k, v = _layer(lens, Hq, Hkv, D, cap, seed=92)
+    pattern = [0, 1, 3, 4, 8, 12, 13, 16, 20, 31, 32, 5, 2, 24, 7, 28, 36, 40, 17, 9]
+    counts = [[pattern[(b * Hkv + 3 * h) % len(pattern)] for h in range(Hkv)] for b in range(B)]
+    # the chunk length the pass derives (global_chunk_len; a queued grid takes C0 unfitted), used
+    # here only to show that the lists cover every case of the numbering
+    flat = [n for row in counts for n in row]
+    C = max(max(1, -(-max(flat) // S)), -(-sum(flat) // (S * Hkv)))
+    if S == 56:
+        assert (S + B) * Hkv > 512 and C == 5
+        assert {0, 1, 3, 5, 40} <= set(flat) and any(n % C for n in flat[64:]) and any(0 < n < C for n in flat[64:])
+    keep = torch.zeros(B, Hkv, nb, dtype=torch.bool)
+    for b, T in enumerate(lens):
+        nbb = math.ceil(T / 64)
+        for h in range(Hkv):
+            keep[b, h, torch.randperm(nbb, generator=g)[:counts[b][h]]] = True
+    bi = torch.zeros(B, Hkv, nb, dtype=torch.int32)
+    bc = torch.zeros(B, Hkv, dtype=torch.int32)
+    for b in range(B):
+        for h in range(Hkv):
+            idx = torch.nonzero(keep[b, h])[:, 0].to(torch.int32)
+            bi[b, h, :len(idx)] = idx
+            bc[b, h] = len(idx)
+    assert bc.flatten().tolist() == flat
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    res = []
+    for lp in (0, 1):
+        bufs = _bufs(B, Hq, D, nb, S)
+        E.decode_into(q.cuda(), k.cuda(), v.cuda(), 0.125, bufs, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
+                      seq_lens=sl, list_partition=lp)
+        res.append(bufs)
+    two = _bufs(B, Hq, D, nb, S)
+    for phase in (1, 2):
+        E.decode_into(q.cuda(), k.cuda(), v.cuda(), 0.125, two, bi.cuda(), bc.cuda(), stats=True, num_splits=S,
+                      seq_lens=sl, phase=phase, list_partition=1)
+    for key in ("out", "lse", "blk_max", "blk_sum"):
+        assert torch.equal(two[key], res[1][key]), key
+    assert torch.equal(res[0]["blk_max"], res[1]["blk_max"]) and torch.equal(res[0]["blk_sum"], res[1]["blk_sum"])
+    assert (res[0]["out"].float() - res[1]["out"].float()).abs().max().item() <= 2e-2
+    fin = torch.isfinite(res[0]["lse"])
+    assert torch.equal(fin, torch.isfinite(res[1]["lse"]))
+    assert (res[0]["lse"][fin] - res[1]["lse"][fin]).abs().max().item() <= 1e-5
+    out = res[1]["out"].float().cpu()
+    lse_d = res[1]["lse"].cpu().double()
+    for b, T in enumerate(lens):
+        nbb = math.ceil(T / 64)
+        kb = keep[b:b + 1, :, :nbb]
+        ref, lse = O.decode(q[b:b + 1], k[b:b + 1, :, :T], v[b:b + 1, :, :T], 0.125, keep=kb)
+        live = kb.any(-1).repeat_interleave(G, 1)[0]
+        if live.any():
+            assert O.rel_err(out[b][live][None], ref[0][live][None]) <= REL, (b, T)
+            assert (lse_d[b][live] - lse[0][live]).abs().max().item() <= LSE_TOL
+        assert (out[b][~live] == 0).all() and (lse_d[b][~live] == -math.inf).all()
+
+
 def test_ragged_rejects(gpu):
     q, k, v = _layer([10, 20], 8, 2, 64, 64, seed=1)
     sl = torch.tensor([10, 20], dtype=torch.int32, device="cuda")
