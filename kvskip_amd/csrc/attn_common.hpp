@@ -222,8 +222,10 @@ __device__ __forceinline__ int global_chunk_len(const AttnP& p, int (&nv)[NRG]) 
 // Chunk number `it` of the partition over all lists: its list (b, h; b = -1 past the last chunk),
 // the chunk within the list and the list's entry count. Returns C. Uniform results. A grid longer
 // than the resident slots (queued workgroups start as others end) takes the lists' full chunks
-// first and their partial last chunks after them, so that it ends on its shortest chunks (B 32 at
-// 64k, stable queries: 592.4 -> 579.8 us per layer-step); a resident grid takes them list by list.
+// first and their partial last chunks after them, the longer half of those first, so that it ends
+// on its shortest chunks (B 32 at 64k, stable queries: 592.4 -> 579.8 us per layer-step, and
+// 580.2-582.0 -> 577.6-578.1 with the two classes of partial chunks); a resident grid takes them
+// list by list.
 __device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk, int& items) {
   const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
   int nv[NRG];
@@ -249,11 +251,13 @@ __device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk,
     }
     base += __shfl(incl, WAVE - 1, WAVE);
   }
-  if (queued && __builtin_amdgcn_readfirstlane(l_sel) < 0) {  // round two: the partial last chunks
+  // rounds two and three: the partial last chunks, the longer ones (at least C / 2) first
+  for (int cls = 0; cls < 2 && queued && __builtin_amdgcn_readfirstlane(l_sel) < 0; ++cls) {
 #pragma unroll
     for (int r = 0; r < NRG; ++r) {
       if (r * WAVE >= nl) break;
-      const int part = nv[r] % C != 0 ? 1 : 0;
+      const int rem = nv[r] % C;
+      const int part = rem != 0 && (2 * rem >= C) == (cls == 0) ? 1 : 0;
       const int incl = wave_incl_scan(part);
       const uint64_t hit = __ballot(part != 0 && it == base + incl - 1);
       if (hit != 0) {
