@@ -192,9 +192,10 @@ __device__ __forceinline__ int ragged_chunks(const AttnP& p, int b, int h, bool 
   return (ragged_items(p, b, h, masked) + C - 1) / C;
 }
 
-// Partition over all B * Hkv lists of a masked ragged pass (p.list_partition = 1): chunks of one
-// length C list entries, numbered list by list (l = b Hkv + h), so a KV head whose lists hold more
-// entries (a refreshing sequence) gets more workgroups instead of longer chunks. C0 = max(ceil(sum /
+// Partition over all B * Hkv lists of a masked ragged pass (p.list_partition = 1): ceil(n / C)
+// chunks of each list's n entries (their bounds: decode_body), numbered list by list (l = b Hkv +
+// h), so a KV head whose lists hold more entries (a refreshing sequence) gets more workgroups
+// instead of longer chunks. C0 = max(ceil(sum /
 // (S Hkv)), ceil(most / S)) fits the grid's (S + B) Hkv slots (sum / C0 <= S Hkv, plus at most one
 // partial chunk per list), bisected as fit_chunk_len says (per layer-step with carried updates,
 // config 5 131.1 -> 125.0 us, B 8 179.1 -> 173.4; bisected for every grid, B 8 with stable queries

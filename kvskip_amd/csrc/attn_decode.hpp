@@ -175,9 +175,9 @@ __device__ bool planned_balanced(const AttnP& p, const kvskip_plan_args& pa, int
 // A planned pass over a ragged batch (seq_lens, B <= BAL_MAX_LISTS): workgroup `it` of KV head h
 // decides the head's B lists (b, h) in its prologue (wavefront w: b = w + NWAVE j; the head's
 // workgroup 0 stores trig and est) and takes chunk `it` of the ragged partition over their lengths
-// (a refreshing list: the sequence's blocks; chunks of ragged_chunk_len's length, numbered
-// sequence by sequence, as ragged_lookup does over the block counts this pass writes, so that the
-// ragged merge finds the same chunks). Outputs as planned_balanced_nh's, plus the sequence's length
+// (a refreshing list: the sequence's blocks; each list cut into ceil(n / C) chunks of near-equal
+// length, C ragged_chunk_len's, numbered sequence by sequence, as ragged_lookup and decode_body do
+// over the block counts this pass writes, so that the ragged merge finds the same chunks). Outputs as planned_balanced_nh's, plus the sequence's length
 // Tb and blocks nbb; the head's workgroup 0 also writes the statistics and the zero count of a list
 // with nothing to read. Returns false for a workgroup past the head's chunks. Uniform results.
 template <int G, int NH>
@@ -243,8 +243,8 @@ __device__ bool planned_ragged_nh(const AttnP& p, const kvskip_plan_args& pa, in
   b = q_sel;
   n_items = __builtin_amdgcn_readlane(cq, q_sel);
   dense = sTr[q_sel] != 0;
-  i0 = min(n_items, split * C);
-  n = min(n_items, i0 + C) - i0;
+  i0 = split * n_items / ch_sel;  // the list's ch_sel chunks of near-equal length, as decode_body's
+  n = (split + 1) * n_items / ch_sel - i0;
   Tb = seq_len(p, b);
   nbb = (Tb + BLK - 1) / BLK;
   writer = false;  // the list's last chunk writes the list at its end
@@ -384,7 +384,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
     const int per = (n_items + p.num_splits - 1) / p.num_splits;
     i0 = min(n_items, split * per);
     n = min(n_items, i0 + per) - i0;
-  } else {  // ragged: chunks of C items over the whole batch, per KV head or over all lists
+  } else {  // ragged: ceil(n / C) chunks per list over the whole batch, per KV head or over all lists
     const int W = p.num_splits + p.B;
     const bool global = MASKED && p.list_partition != 0;
     // per KV head: a head's chunk slots on one XCD (its first slots are the busy ones on every XCD);
@@ -421,8 +421,18 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
     }
     if (b < 0) return;
     split = chunk;
-    i0 = chunk * C;
-    n = min(n_items, i0 + C) - i0;
+    // A list's ceil(n / C) chunks: of near-equal length (no chunk of a few items beside full ones:
+    // B 8 172.9 -> 171.4 us per layer-step, config 5's dense pass 111.9 -> 111.3), or of C items
+    // and a partial last over all lists of a queued grid (global_lookup's order takes the partial
+    // chunks last) or of groups over 4 (config 5's loop 125.1 -> 126.6 cut near-equal).
+    if (global && (G > 4 || (p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS)) {
+      i0 = chunk * C;
+      n = min(n_items, i0 + C) - i0;
+    } else {
+      const int k = max(1, (n_items + C - 1) / C);
+      i0 = chunk * n_items / k;
+      n = (chunk + 1) * n_items / k - i0;
+    }
     Tb = seq_len(p, b);
     nbb = (Tb + BLK - 1) / BLK;
   }
