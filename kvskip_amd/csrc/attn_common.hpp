@@ -108,10 +108,16 @@ __device__ __forceinline__ int ragged_items(const AttnP& p, int b, int h, bool m
 // 121.0 -> 113.2 us per layer-step. Uniform.
 constexpr int RESIDENT_SLOTS = 512;
 
+// A ragged grid ((num_splits + B) * Hkv workgroups) longer than the resident slots: its queued
+// workgroups start as others end.
+__device__ __forceinline__ bool grid_queued(const AttnP& p) {
+  return (p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS;
+}
+
 template <int NR>
 __device__ __forceinline__ int fit_chunk_len(const AttnP& p, const int (&nv)[NR], int n_lists, int lo, int c0,
                                              int slots) {
-  if ((p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS || c0 < 32) return c0;
+  if (grid_queued(p) || c0 < 32) return c0;
   int hi = c0;
   lo = __builtin_amdgcn_readfirstlane(min(lo, c0));
   while (lo < hi) {  // the chunk count does not grow with C
@@ -231,7 +237,7 @@ __device__ int global_lookup(const AttnP& p, int it, int& b, int& h, int& chunk,
   const int lane = threadIdx.x % WAVE, nl = p.B * p.Hkv;
   int nv[NRG];
   const int C = global_chunk_len(p, nv);
-  const bool queued = (p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS;
+  const bool queued = grid_queued(p);
   int l_sel = -1;
   chunk = 0;
   items = 0;

@@ -425,7 +425,7 @@ __device__ __forceinline__ void decode_body(const AttnP& p, int bid, const kvski
     // B 8 172.9 -> 171.4 us per layer-step, config 5's dense pass 111.9 -> 111.3), or of C items
     // and a partial last over all lists of a queued grid (global_lookup's order takes the partial
     // chunks last) or of groups over 4 (config 5's loop 125.1 -> 126.6 cut near-equal).
-    if (global && (G > 4 || (p.num_splits + p.B) * p.Hkv > RESIDENT_SLOTS)) {
+    if (global && (G > 4 || grid_queued(p))) {
       i0 = chunk * C;
       n = min(n_items, i0 + C) - i0;
     } else {
